@@ -1,0 +1,230 @@
+#!/usr/bin/env python3
+"""Benchmark of the ConvRot INT8 linear path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+
+A *step* is one ``xpu_kernels.int8.linear`` at config 3 of BASELINE.json
+(x bf16 [4096,1280] with 1% outlier channels x30, W prepared from bf16
+[10240,1280], bias bf16 [10240]): rotate+quantize of x, then the int8 MFMA
+GEMM with the dequant+bias epilogue fused into its store.  Inputs are resident
+in HBM before the timed region; W is prepared once, untimed.  W warm-up steps,
+then exactly K steps between two ``torch.cuda.synchronize()`` calls, timed with
+HIP events on the stream the kernels run on (torch's current stream).
+
+``value`` is end-to-end TOP/s at config 3 (2*M*N*K = 107.37 GOP per step).
+The other configurations are measured after it and reported under ``extra``.
+``roofline`` is the GEMM kernel's own average duration against the dense INT8
+MFMA peak; ``cpu_baseline`` times the oracle (a numpy port of the reference
+chain) on a bounded row sample of config 3 on this host.  One JSON line on
+stdout; progress goes to stderr.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for p in (ROOT, os.path.join(ROOT, "oko-xpu-kernels_amd")):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+PEAK_INT8_TOPS = 5000.0          # MI355X dense int8 MFMA, TOP/s
+PEAK_HBM_GBPS = 8000.0           # MI355X HBM3E, GB/s
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def activation(torch, m, k, seed=0, n_out=None, mult=30.0, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(m, k, generator=g) * scale
+    n_out = max(1, round(0.01 * k)) if n_out is None else n_out
+    if n_out:
+        x[:, torch.randperm(k, generator=g)[:n_out]] *= mult
+    return x.to(torch.bfloat16)
+
+
+def weight(torch, n, k, seed=1, std=0.02):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(n, k, generator=g) * std).to(torch.bfloat16)
+
+
+def timed(torch, fn, steps, warmup):
+    """Average ms per call of ``fn`` over ``steps`` calls (HIP events on the
+    current stream, after ``warmup`` untimed calls)."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(steps):
+        fn()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / steps
+
+
+def cpu_baseline(seconds):
+    """The oracle's chain (rotate+quantize, int_mm, dequant) on a row sample
+    of config 3, on this host's cores."""
+    import numpy as np
+    import oracle as O
+    rng = np.random.default_rng(0)
+    m, k, n = 256, 1280, 10240
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    x[:, rng.permutation(k)[:13]] *= 30
+    xb = O.f32_to_bf16(x)
+    w8 = rng.integers(-127, 128, (n, k), dtype=np.int8)
+    ws = rng.uniform(1e-4, 1e-3, n).astype(np.float32)
+    bias = rng.standard_normal(n).astype(np.float32) * 0.01
+    O.linear(xb, w8, ws, bias)                       # warm-up
+    times = []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        O.linear(xb, w8, ws, bias)
+        times.append(time.perf_counter() - t0)
+    med = sorted(times)[len(times) // 2]
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return {
+        "value": round(2.0 * m * n * k / med / 1e12, 5),
+        "unit": "TOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"oracle.linear (numpy: Hadamard+quantize, exact float64 BLAS int_mm, "
+                  f"dequant) on {m} of config 3's 4096 rows, K=1280, N=10240; median of "
+                  f"{len(times)} runs ({med * 1e3:.1f} ms each)",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--only-main", action="store_true", help="config 3 only (for profiling)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path "
+              f"(asked for --gpus {args.gpus})", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from xpu_kernels import int8
+    from xpu_kernels.int8 import _lib as L
+    if not int8.available():
+        raise SystemExit(f"libxpuint8 unavailable: {L._ERR}")
+    dev = torch.device("cuda", 0)
+    K, W = args.steps, args.warmup
+
+    # ---------------------------------------------------------- config 3
+    M, Kd, N = 4096, 1280, 10240
+    x = activation(torch, M, Kd).to(dev)
+    w8, ws = int8.prepare_weight(weight(torch, N, Kd).to(dev))
+    bias = weight(torch, 1, N, seed=2, std=0.01)[0].to(dev)
+    ops3 = 2.0 * M * N * Kd
+    log(f"[bench] config 3 linear {M}x{Kd}x{N}: {W} warm-up + {K} timed steps")
+    ms = timed(torch, lambda: int8.linear(x, w8, ws, bias), K, W)
+    value = ops3 / (ms * 1e-3) / 1e12
+
+    # the dominant kernel alone: the GEMM with the fused epilogue
+    xq, xs = int8.quantize(x)
+    out = torch.empty((M, N), device=dev, dtype=torch.bfloat16)
+    lib = L._lib()
+    bias32 = bias.float()
+
+    def gemm():
+        lib.xpuint8_linear_gemm_stream(L._stream(dev), L._ptr(xq), L._ptr(xs), L._ptr(w8),
+                                       L._ptr(ws), L._ptr(bias32), L._ptr(out), M, N, Kd)
+    ms_gemm = timed(torch, gemm, K, W)
+    gemm_tops = ops3 / (ms_gemm * 1e-3) / 1e12
+    ms_q3 = timed(torch, lambda: int8.quantize(x), K, W)
+    log(f"[bench] step {ms:.4f} ms = {value:.1f} TOP/s; GEMM {ms_gemm:.4f} ms = "
+        f"{gemm_tops:.1f} TOP/s; quantize {ms_q3:.4f} ms")
+
+    extra = {"config3_gemm_ms": round(ms_gemm, 5), "config3_quantize_ms": round(ms_q3, 5)}
+    if not args.only_main:
+        # ------------------------------------------------------ config 2
+        x2 = activation(torch, 4096, 5120).to(dev)
+        ms_q = timed(torch, lambda: int8.quantize(x2), K, W)
+        bytes_q = 2 * 4096 * 5120 + 4096 * 5120 + 4 * 4096
+        w2 = weight(torch, 10240, 1280).to(dev)
+        ms_p = timed(torch, lambda: int8.prepare_weight(w2), K, W)
+        bytes_p = 3 * 10240 * 1280 + 4 * 10240
+        extra["config2_rotate_quant"] = {
+            "ms": round(ms_q, 5), "GB/s": round(bytes_q / (ms_q * 1e-3) / 1e9, 1),
+            "frac_hbm_peak": round(bytes_q / (ms_q * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4)}
+        extra["config2_prepare_weight"] = {
+            "ms": round(ms_p, 5), "GB/s": round(bytes_p / (ms_p * 1e-3) / 1e9, 1)}
+        log(f"[bench] config 2: rotate+quant {ms_q:.4f} ms, prepare_weight {ms_p:.4f} ms")
+        # ------------------------------------------------------ config 4
+        xf = activation(torch, 4096, 1280, seed=3).to(dev)
+        up8, ups = int8.prepare_weight(weight(torch, 10240, 1280, seed=4).to(dev))
+        dn8, dns = int8.prepare_weight(weight(torch, 1280, 5120, seed=5).to(dev))
+        db = weight(torch, 1, 1280, seed=6, std=0.01)[0].to(dev)
+        ms_f = timed(torch, lambda: int8.ffn(xf, up8, ups, dn8, dns, db, act="geglu_erf"), K, W)
+        ops4 = 2.0 * 4096 * 1280 * 10240 + 2.0 * 4096 * 5120 * 1280
+        extra["config4_ffn"] = {"ms": round(ms_f, 5), "TOP/s": round(ops4 / (ms_f * 1e-3) / 1e12, 1)}
+        log(f"[bench] config 4: ffn {ms_f:.4f} ms")
+        # ------------------------------------------------------ config 5
+        w5_8, w5_s = int8.prepare_weight(weight(torch, 5120, 1280, seed=7).to(dev))
+        dy = (torch.randn(4096, 5120, generator=torch.Generator().manual_seed(8)) * 1e-3
+              ).to(torch.bfloat16).to(dev)
+        x5 = activation(torch, 4096, 1280, seed=9).to(dev)
+        ms_dx = timed(torch, lambda: int8.linear_dx_int8(dy, w5_8, w5_s), K, W)
+        ms_dw = timed(torch, lambda: int8.linear_dw(dy, x5), K, W)
+        ms_rq = timed(torch, lambda: int8.quantize_row(dy, w5_s), K, W)
+        ops5 = 2.0 * 4096 * 5120 * 1280
+        bytes_rq = 3 * 4096 * 5120 + 4 * 4096
+        extra["config5_dx_int8"] = {"ms": round(ms_dx, 5), "TOP/s": round(ops5 / (ms_dx * 1e-3) / 1e12, 1)}
+        extra["config5_dw"] = {"ms": round(ms_dw, 5), "TFLOP/s": round(ops5 / (ms_dw * 1e-3) / 1e12, 1)}
+        extra["config5_quantize_row"] = {"ms": round(ms_rq, 5),
+                                         "GB/s": round(bytes_rq / (ms_rq * 1e-3) / 1e9, 1)}
+        xs16 = activation(torch, 16, 4096, seed=10).to(dev)
+        sk8, sks = int8.prepare_weight(weight(torch, 4096, 4096, seed=11).to(dev))
+        ms_sk = timed(torch, lambda: int8.linear(xs16, sk8, sks), K, W)
+        bytes_sk = 4096 * 4096 + 2 * 16 * 4096 * 2 + 4 * 4096 + 4 * 16
+        extra["config5_skinny_m16"] = {"ms": round(ms_sk, 5),
+                                       "GB/s": round(bytes_sk / (ms_sk * 1e-3) / 1e9, 1)}
+        log(f"[bench] config 5: dx {ms_dx:.4f} ms, dW {ms_dw:.4f} ms, quantize_row {ms_rq:.4f} ms, "
+            f"skinny {ms_sk:.4f} ms")
+
+    line = {
+        "metric": "int8_linear TOPS (M=4096,K=1280,N=10240); rotate+quant HBM GB/s",
+        "value": round(value, 2),
+        "unit": "TOP/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (BASELINE.json config 3 recipe, torch CPU generator seed 0)",
+        "config": {"workload": "config 3: int8_linear forward M=4096 K=1280 N=10240 "
+                               "(rotate+quantize + int8 MFMA GEMM with fused dequant+bias)",
+                   "M": M, "K": Kd, "N": N, "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": round(gemm_tops, 2), "peak": PEAK_INT8_TOPS,
+                     "unit": "TOP/s", "frac": round(gemm_tops / PEAK_INT8_TOPS, 4),
+                     "traffic": None,
+                     "kernel": "gemm_i8 with dequant epilogue (2*M*N*K int ops per launch)"},
+        "extra": extra,
+    }
+    if not args.no_cpu:
+        log(f"[bench] CPU baseline ({args.cpu_seconds:.0f} s)")
+        line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    else:
+        line["cpu_baseline"] = None
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,165 @@
+/* libxpuint8 for MI355X (gfx950): the ConvRot INT8 linear as a C ABI.
+ *
+ * Drop-in for the C ABI of okolenmi/oko-xpu-kernels'
+ * include/xpu_kernels/convrot.h (lines cited per function), which
+ * python/xpu_kernels/int8/_lib.py binds through ctypes.  Differences:
+ *
+ *  - the `_stream` variants take a HIP stream (`hipStream_t`, passed as
+ *    `const void *`; NULL is the default stream) where the reference takes a
+ *    `sycl::queue *`.  They enqueue asynchronously and never wait.  The
+ *    non-stream variants run on the default stream and synchronize it.
+ *  - the entry points the reference left to torch (`torch._int_mm`, the
+ *    prepare_weight / quantize_row / linear_dw chains) are here too, so the
+ *    whole path runs in this library: see the second half of this file.
+ *
+ * Conventions.  Every pointer is a device pointer to a contiguous row-major
+ * buffer owned by the caller; the library allocates no device memory.  bf16
+ * tensors are passed as `void *` (16-bit storage).  Sizes are int64_t.  Every
+ * function returns 0 on success or an error code, with a message available
+ * from xpuint8_last_error() (thread-local):
+ *   1 no usable device (or init failed)      4 unsupported size
+ *   2 bad dimensions (<= 0, N % 16, stride)  5 HIP launch / runtime error
+ *   3 K not a multiple of 256                6 bad argument (null pointer,
+ *                                              unknown activation)
+ * Arguments are validated before any device call, so argument errors are
+ * reported identically with or without a GPU.
+ */
+#ifndef XPUINT8_H
+#define XPUINT8_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- library ----------------------------------------------------------- */
+
+/* Select the current HIP device, check it is gfx950 and upload the
+ * activation tables.  Replaces convrot.h:31-32. */
+int xpuint8_init(void);
+
+/* Device name ("AMD Instinct MI355X ..."), or NULL if no device.
+ * Replaces convrot.h:34-35. */
+const char *xpuint8_device_name(void);
+
+/* The ConvRot group size, 256.  Replaces convrot.h:37-39. */
+int xpuint8_convrot_groupsize(void);
+
+/* Message of the last error on this thread.  Replaces convrot.h:115. */
+const char *xpuint8_last_error(void);
+
+/* ---- the reference's own entry points ---------------------------------- */
+
+/* Rotate + quantize: bf16 x[M,K] -> int8 q[M,K] + fp32 scale[M].
+ * K % 256 == 0.  Replaces convrot.h:41-49. */
+int xpuint8_convrot_quantize(const void *x, int8_t *q, float *scale, int64_t M, int64_t K);
+int xpuint8_convrot_quantize_stream(const void *stream, const void *x, int8_t *q, float *scale,
+                                    int64_t M, int64_t K);
+
+/* The same with an activation fused into the load (ids as convrot.h:51-59:
+ * 1 gelu_tanh [M,K], 2 swiglu [M,2K] = [gate|up], 3 situ [M,2K] =
+ * [hidden|gate], 4 geglu_erf [M,2K] = [hidden|gate], 5 gelu_erf [M,K]).
+ * K is the output width.  Replaces convrot.h:60-64. */
+int xpuint8_convrot_quantize_act(const void *x, int8_t *q, float *scale, int64_t M, int64_t K,
+                                 int32_t activation);
+int xpuint8_convrot_quantize_act_stream(const void *stream, const void *x, int8_t *q,
+                                        float *scale, int64_t M, int64_t K, int32_t activation);
+
+/* int8 w8[N,K] * fp32 w_scale[N] -> bf16 out[N,K] with the rotation undone
+ * (the inverse of prepare_weight).  Replaces convrot.h:66-72. */
+int xpuint8_dequant_weight(const void *w8, const float *w_scale, void *out, int64_t N,
+                           int64_t K);
+int xpuint8_dequant_weight_stream(const void *stream, const void *w8, const float *w_scale,
+                                  void *out, int64_t N, int64_t K);
+
+/* Rotation only, bf16 x[M,K] -> bf16 xr[M,K].  Replaces convrot.h:74-76. */
+int xpuint8_convrot_rotate_bf16(const void *x, void *xr, int64_t M, int64_t K);
+int xpuint8_convrot_rotate_bf16_stream(const void *stream, const void *x, void *xr, int64_t M,
+                                       int64_t K);
+
+/* out[m,n] = bf16(float(acc[m,n]) * (w_scale[n] * x_scale[m]) + bias[n]);
+ * bias may be NULL; N % 16 == 0.  Replaces convrot.h:78-86. */
+int xpuint8_dequant_epilogue(const int32_t *acc, void *out, const float *x_scale,
+                             const float *w_scale, const float *bias, int64_t M, int64_t N);
+int xpuint8_dequant_epilogue_stream(const void *stream, const int32_t *acc, void *out,
+                                    const float *x_scale, const float *w_scale,
+                                    const float *bias, int64_t M, int64_t N);
+
+/* The same on a [M,N] column slice of a [M, acc_row_stride] accumulator.
+ * Replaces convrot.h:87-97. */
+int xpuint8_dequant_epilogue_slice(const int32_t *acc, void *out, const float *x_scale,
+                                   const float *w_scale, const float *bias, int64_t M,
+                                   int64_t N, int64_t acc_row_stride);
+int xpuint8_dequant_epilogue_slice_stream(const void *stream, const int32_t *acc, void *out,
+                                          const float *x_scale, const float *w_scale,
+                                          const float *bias, int64_t M, int64_t N,
+                                          int64_t acc_row_stride);
+
+/* Dequant + activation (3 situ, 4 geglu_erf: acc [M,2K] = [hidden|gate];
+ * 5 gelu_erf: acc [M,K]) + rotate + quantize -> int8 q[M,K] + scale[M].
+ * w_scale has 2K (paired) or K entries.  Replaces convrot.h:98-113. */
+int xpuint8_dequant_act_quantize(const void *acc, int8_t *q, float *scale, const float *x_scale,
+                                 const float *w_scale, int64_t M, int64_t K, int32_t activation);
+int xpuint8_dequant_act_quantize_stream(const void *stream, const void *acc, int8_t *q,
+                                        float *scale, const float *x_scale,
+                                        const float *w_scale, int64_t M, int64_t K,
+                                        int32_t activation);
+
+/* ---- what the reference delegated to torch ----------------------------- */
+
+/* c[M,N] = a[M,K] @ b[N,K]^T, int8 x int8 -> int32, exact.  K % 16 == 0,
+ * K <= 131072 (no int32 overflow).  Replaces torch._int_mm(a, b.t()) at
+ * python/xpu_kernels/int8/ops.py:587 and :634. */
+int xpuint8_int8_gemm_stream(const void *stream, const int8_t *a, const int8_t *b, int32_t *c,
+                             int64_t M, int64_t N, int64_t K);
+
+/* c[M,N] = a[M,K] @ b[K,N] (both row-major: the contraction runs down b's
+ * rows).  `work` is a caller-owned int8 buffer of N*K bytes that receives b^T.
+ * Replaces torch._int_mm(q, w8) at python/xpu_kernels/int8/ops.py:371. */
+int xpuint8_int8_gemm_nn_stream(const void *stream, const int8_t *a, const int8_t *b, int32_t *c,
+                                int64_t M, int64_t N, int64_t K, int8_t *work);
+
+/* The linear's GEMM with the dequant epilogue fused into its store:
+ * out[m,n] = bf16(float(sum_k xq[m,k] w8[n,k]) * (w_scale[n] * x_scale[m]) + bias[n]),
+ * bit-identical to xpuint8_int8_gemm_stream followed by
+ * xpuint8_dequant_epilogue_stream.  bias may be NULL; N % 16 == 0.
+ * Replaces torch._int_mm + dequant at python/xpu_kernels/int8/ops.py:634-638. */
+int xpuint8_linear_gemm_stream(const void *stream, const int8_t *xq, const float *x_scale,
+                               const int8_t *w8, const float *w_scale, const float *bias,
+                               void *out, int64_t M, int64_t N, int64_t K);
+
+/* linear_dx_int8's GEMM: dx[m,k] = bf16(float(sum_n q[m,n] w8[n,k]) * a[m]),
+ * the NN product with the row-scale epilogue.  `work` holds w8^T (K*N bytes).
+ * Replaces torch._int_mm(q, w8) + dequant(acc, a, ones) at
+ * python/xpu_kernels/int8/ops.py:371-376. */
+int xpuint8_dx_gemm_stream(const void *stream, const int8_t *q, const float *a,
+                           const int8_t *w8, void *dx, int64_t M, int64_t N, int64_t K,
+                           int8_t *work);
+
+/* prepare_weight in one kernel, bit-identical to the torch chain of
+ * python/xpu_kernels/int8/ops.py:93-99: bf16 w[N,K] -> int8 q[N,K] + fp32
+ * scale[N].  (xpuint8_convrot_quantize is prepare_weight_fused.) */
+int xpuint8_prepare_weight_stream(const void *stream, const void *w, int8_t *q, float *scale,
+                                  int64_t N, int64_t K);
+
+/* Per-row int8 quantization without rotation (the gradient row quantizer):
+ * x bf16 [M,N] -> q int8 [M,N] + scale fp32 [M], bit-identical to
+ * quantize_row_torch (python/xpu_kernels/int8/ops.py:320-330).  With a
+ * non-NULL col_scale[N] the row is first bf16(x * bf16(col_scale)), the
+ * dy * w_scale product of ops.py:366.  N % 16 == 0.  Replaces the Triton
+ * quantize_row (python/xpu_kernels/triton/quantize.py:63-126). */
+int xpuint8_quantize_row_stream(const void *stream, const void *x, const float *col_scale,
+                                int8_t *q, float *scale, int64_t M, int64_t N);
+
+/* Host copy of an activation table (65536 bf16 entries indexed by the bf16
+ * bit pattern of the input): 0 gelu_erf, 1 gelu_tanh, 2 silu, 3 situ's
+ * tanh(bf16(x/4)), 4 sigmoid, 5 situ's tanh(bf16(x/25)).  No device needed.
+ * No counterpart in the reference: it exposes the exact functions the fused
+ * activations apply, for verification. */
+int xpuint8_activation_table(int32_t id, uint16_t *out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* XPUINT8_H */

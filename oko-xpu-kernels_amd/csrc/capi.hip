@@ -1,0 +1,358 @@
+// The C ABI (include/xpuint8.h): argument validation, error reporting, device
+// initialisation and dispatch to the launchers in kernels.hpp.
+//
+// Validation runs before any HIP call, so an argument error is reported the
+// same way on a machine without a GPU.  Errors are thread-local strings
+// (the reference keeps one process-global string, src/xpuint8.cpp:36-50).
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+
+#include "activations.hpp"
+#include "kernels.hpp"
+#include "../../include/xpuint8.h"
+
+namespace xpuint8 {
+
+// Device copy of the activation tables.  Host code reaches it only through
+// the address hipGetSymbolAddress returns for the current device.
+__device__ uint16_t g_act_tables[kNumTables * kTabSize];
+
+namespace {
+
+thread_local std::string t_error;
+
+int fail(int code, const std::string& msg) {
+    t_error = msg;
+    return code;
+}
+
+constexpr int kMaxDevices = 64;
+std::mutex g_mutex;
+std::string g_device_name[kMaxDevices];
+const uint16_t* g_tab_dev[kMaxDevices] = {};
+std::atomic<bool> g_ready[kMaxDevices] = {};
+
+// Per-device set-up: architecture check and table upload.  Returns 0 or an
+// error code (message set).
+int ensure_device() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return fail(1, "no HIP device available");
+    if (dev < 0 || dev >= kMaxDevices) return fail(1, "device index out of range");
+    if (g_ready[dev].load(std::memory_order_acquire)) return 0;
+    std::lock_guard<std::mutex> lock(g_mutex);
+    if (g_ready[dev].load(std::memory_order_relaxed)) return 0;
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, dev) != hipSuccess)
+        return fail(1, "hipGetDeviceProperties failed");
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(1, std::string("libxpuint8 is built for gfx950 only; device ") +
+                           std::to_string(dev) + " is " + prop.gcnArchName);
+    void* sym = nullptr;
+    hipError_t e = hipGetSymbolAddress(&sym, HIP_SYMBOL(g_act_tables));
+    if (e != hipSuccess || sym == nullptr)
+        return fail(5, std::string("hipGetSymbolAddress(activation tables): ") + hipGetErrorString(e));
+    e = hipMemcpy(sym, host_activation_tables(), sizeof(uint16_t) * kNumTables * kTabSize,
+                  hipMemcpyHostToDevice);
+    if (e != hipSuccess)
+        return fail(5, std::string("uploading the activation tables: ") + hipGetErrorString(e));
+    g_tab_dev[dev] = static_cast<const uint16_t*>(sym);
+    g_device_name[dev] = prop.name;
+    g_ready[dev].store(true, std::memory_order_release);
+    return 0;
+}
+
+int launched(hipError_t e, const char* what) {
+    if (e != hipSuccess) return fail(5, std::string(what) + ": " + hipGetErrorString(e));
+    return 0;
+}
+
+// Synchronous wrappers: run on the default stream and wait for it.
+int finish(int rc, const char* what) {
+    if (rc != 0) return rc;
+    const hipError_t e = hipStreamSynchronize(nullptr);
+    if (e != hipSuccess) return fail(5, std::string(what) + ": " + hipGetErrorString(e));
+    return 0;
+}
+
+hipStream_t as_stream(const void* s) { return static_cast<hipStream_t>(const_cast<void*>(s)); }
+
+constexpr int64_t kMaxK = 131072;          // 127*127*K < 2^31
+constexpr int64_t kMaxDim = (int64_t(1) << 31) - 1;
+constexpr int64_t kMaxGemmM = int64_t(65535) * 128;   // grid.y limit of the GEMM launch
+
+int check_rows(int64_t M, int64_t K) {
+    if (M <= 0 || K <= 0) return fail(2, "M and K must be positive");
+    if (K % 256 != 0) return fail(3, "K must be divisible by the ConvRot group size (256)");
+    if (K > kMaxK || M > kMaxDim) return fail(4, "K must be <= 131072 and M < 2^31");
+    return 0;
+}
+
+int check_epilogue(int64_t M, int64_t N) {
+    if (M <= 0 || N <= 0 || N % 16 != 0)
+        return fail(2, "M, N must be positive and N must be a multiple of 16");
+    if (M > kMaxDim || N > kMaxDim) return fail(4, "M and N must be < 2^31");
+    return 0;
+}
+
+int check_gemm(int64_t M, int64_t N, int64_t K) {
+    if (M <= 0 || N <= 0 || K <= 0) return fail(2, "M, N and K must be positive");
+    if (K % 16 != 0) return fail(2, "K must be a multiple of 16");
+    if (K > kMaxK) return fail(4, "K must be <= 131072 (int32 accumulator range)");
+    if (M > kMaxGemmM || N > kMaxDim) return fail(4, "M must be <= 8388480 and N < 2^31");
+    return 0;
+}
+
+// Every buffer is read and written with 16-byte vector accesses.
+#define XPU_NONNULL(p)                                          \
+    if (!(p)) return fail(6, #p " must not be null");           \
+    if (reinterpret_cast<uintptr_t>(p) % 16 != 0)               \
+    return fail(6, #p " must be 16-byte aligned")
+#define XPU_ALIGNED_OPT(p)                                      \
+    if ((p) && reinterpret_cast<uintptr_t>(p) % 16 != 0)        \
+    return fail(6, #p " must be 16-byte aligned")
+#define XPU_TRY(expr)              \
+    do {                           \
+        const int rc_ = (expr);    \
+        if (rc_ != 0) return rc_;  \
+    } while (0)
+
+int act_ok(int32_t act) {
+    if (act < 1 || act > 5)
+        return fail(6, "activation must be 1 (GELU-tanh), 2 (SwiGLU), 3 (situ), 4 (GEGLU) "
+                       "or 5 (GELU-erf)");
+    return 0;
+}
+
+}  // namespace
+
+const uint16_t* activation_tables() {
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    return (dev >= 0 && dev < kMaxDevices) ? g_tab_dev[dev] : nullptr;
+}
+
+}  // namespace xpuint8
+
+using namespace xpuint8;
+
+extern "C" {
+
+int xpuint8_init(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return fail(1, "no HIP device available");
+    return ensure_device();
+}
+
+const char* xpuint8_device_name(void) {
+    if (ensure_device() != 0) return nullptr;
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    return g_device_name[dev].c_str();
+}
+
+int xpuint8_convrot_groupsize(void) { return 256; }
+
+const char* xpuint8_last_error(void) { return t_error.c_str(); }
+
+// ---------------------------------------------------------------- quantize
+int xpuint8_convrot_quantize_stream(const void* stream, const void* x, int8_t* q, float* scale,
+                                    int64_t M, int64_t K) {
+    XPU_TRY(check_rows(M, K));
+    XPU_NONNULL(x); XPU_NONNULL(q); XPU_NONNULL(scale);
+    XPU_TRY(ensure_device());
+    return launched(convrot_quantize(as_stream(stream), x, q, scale, M, int(K), 0),
+                    "convrot_quantize");
+}
+
+int xpuint8_convrot_quantize(const void* x, int8_t* q, float* scale, int64_t M, int64_t K) {
+    return finish(xpuint8_convrot_quantize_stream(nullptr, x, q, scale, M, K), "convrot_quantize");
+}
+
+int xpuint8_convrot_quantize_act_stream(const void* stream, const void* x, int8_t* q,
+                                        float* scale, int64_t M, int64_t K, int32_t activation) {
+    XPU_TRY(act_ok(activation));
+    XPU_TRY(check_rows(M, K));
+    XPU_NONNULL(x); XPU_NONNULL(q); XPU_NONNULL(scale);
+    XPU_TRY(ensure_device());
+    return launched(convrot_quantize(as_stream(stream), x, q, scale, M, int(K), activation),
+                    "convrot_quantize_act");
+}
+
+int xpuint8_convrot_quantize_act(const void* x, int8_t* q, float* scale, int64_t M, int64_t K,
+                                 int32_t activation) {
+    return finish(xpuint8_convrot_quantize_act_stream(nullptr, x, q, scale, M, K, activation),
+                  "convrot_quantize_act");
+}
+
+// ------------------------------------------------------------------ rotate
+int xpuint8_convrot_rotate_bf16_stream(const void* stream, const void* x, void* xr, int64_t M,
+                                       int64_t K) {
+    XPU_TRY(check_rows(M, K));
+    XPU_NONNULL(x); XPU_NONNULL(xr);
+    XPU_TRY(ensure_device());
+    return launched(rotate_bf16(as_stream(stream), x, xr, M, int(K)), "convrot_rotate_bf16");
+}
+
+int xpuint8_convrot_rotate_bf16(const void* x, void* xr, int64_t M, int64_t K) {
+    return finish(xpuint8_convrot_rotate_bf16_stream(nullptr, x, xr, M, K), "convrot_rotate_bf16");
+}
+
+// ---------------------------------------------------------- dequant weight
+int xpuint8_dequant_weight_stream(const void* stream, const void* w8, const float* w_scale,
+                                  void* out, int64_t N, int64_t K) {
+    if (N <= 0 || K <= 0) return fail(2, "N and K must be positive");
+    XPU_TRY(check_rows(N, K));
+    XPU_NONNULL(w8); XPU_NONNULL(w_scale); XPU_NONNULL(out);
+    XPU_TRY(ensure_device());
+    return launched(dequant_weight(as_stream(stream), static_cast<const int8_t*>(w8), w_scale, out,
+                                   N, int(K)),
+                    "dequant_weight");
+}
+
+int xpuint8_dequant_weight(const void* w8, const float* w_scale, void* out, int64_t N, int64_t K) {
+    return finish(xpuint8_dequant_weight_stream(nullptr, w8, w_scale, out, N, K), "dequant_weight");
+}
+
+// ---------------------------------------------------------------- dequant
+int xpuint8_dequant_epilogue_slice_stream(const void* stream, const int32_t* acc, void* out,
+                                          const float* x_scale, const float* w_scale,
+                                          const float* bias, int64_t M, int64_t N,
+                                          int64_t acc_row_stride) {
+    if (M <= 0 || N <= 0 || N % 16 != 0 || acc_row_stride < N)
+        return fail(2, "M, N must be positive, N a multiple of 16, acc_row_stride >= N");
+    XPU_TRY(check_epilogue(M, N));
+    if (acc_row_stride % 4 != 0)
+        return fail(2, "acc_row_stride must be a multiple of 4 (16-byte rows)");
+    XPU_NONNULL(acc); XPU_NONNULL(out); XPU_NONNULL(x_scale); XPU_NONNULL(w_scale);
+    XPU_ALIGNED_OPT(bias);
+    XPU_TRY(ensure_device());
+    return launched(dequant_epilogue(as_stream(stream), acc, acc_row_stride, out, x_scale, w_scale,
+                                     bias, M, N),
+                    "dequant_epilogue");
+}
+
+int xpuint8_dequant_epilogue_stream(const void* stream, const int32_t* acc, void* out,
+                                    const float* x_scale, const float* w_scale, const float* bias,
+                                    int64_t M, int64_t N) {
+    XPU_TRY(check_epilogue(M, N));
+    return xpuint8_dequant_epilogue_slice_stream(stream, acc, out, x_scale, w_scale, bias, M, N, N);
+}
+
+int xpuint8_dequant_epilogue(const int32_t* acc, void* out, const float* x_scale,
+                             const float* w_scale, const float* bias, int64_t M, int64_t N) {
+    return finish(xpuint8_dequant_epilogue_stream(nullptr, acc, out, x_scale, w_scale, bias, M, N),
+                  "dequant_epilogue");
+}
+
+int xpuint8_dequant_epilogue_slice(const int32_t* acc, void* out, const float* x_scale,
+                                   const float* w_scale, const float* bias, int64_t M, int64_t N,
+                                   int64_t acc_row_stride) {
+    return finish(xpuint8_dequant_epilogue_slice_stream(nullptr, acc, out, x_scale, w_scale, bias,
+                                                        M, N, acc_row_stride),
+                  "dequant_epilogue_slice");
+}
+
+// -------------------------------------------------- dequant+act+quantize
+int xpuint8_dequant_act_quantize_stream(const void* stream, const void* acc, int8_t* q,
+                                        float* scale, const float* x_scale, const float* w_scale,
+                                        int64_t M, int64_t K, int32_t activation) {
+    if (activation != 3 && activation != 4 && activation != 5)
+        return fail(6, "dequant_act_quantize supports activation 3 (situ), 4 (GEGLU) or "
+                       "5 (GELU-erf)");
+    XPU_TRY(check_rows(M, K));
+    XPU_NONNULL(acc); XPU_NONNULL(q); XPU_NONNULL(scale); XPU_NONNULL(x_scale);
+    XPU_NONNULL(w_scale);
+    XPU_TRY(ensure_device());
+    const int64_t ld = act_paired(activation) ? 2 * K : K;
+    return launched(dequant_act_quantize(as_stream(stream), static_cast<const int32_t*>(acc), ld,
+                                         q, scale, x_scale, w_scale, M, int(K), activation),
+                    "dequant_act_quantize");
+}
+
+int xpuint8_dequant_act_quantize(const void* acc, int8_t* q, float* scale, const float* x_scale,
+                                 const float* w_scale, int64_t M, int64_t K, int32_t activation) {
+    return finish(xpuint8_dequant_act_quantize_stream(nullptr, acc, q, scale, x_scale, w_scale, M,
+                                                      K, activation),
+                  "dequant_act_quantize");
+}
+
+// ------------------------------------------------------------------- GEMMs
+int xpuint8_int8_gemm_stream(const void* stream, const int8_t* a, const int8_t* b, int32_t* c,
+                             int64_t M, int64_t N, int64_t K) {
+    XPU_TRY(check_gemm(M, N, K));
+    XPU_NONNULL(a); XPU_NONNULL(b); XPU_NONNULL(c);
+    XPU_TRY(ensure_device());
+    return launched(gemm_i32(as_stream(stream), a, K, b, K, c, N, int(M), int(N), int(K)),
+                    "int8_gemm");
+}
+
+int xpuint8_int8_gemm_nn_stream(const void* stream, const int8_t* a, const int8_t* b, int32_t* c,
+                                int64_t M, int64_t N, int64_t K, int8_t* work) {
+    XPU_TRY(check_gemm(M, N, K));
+    XPU_NONNULL(a); XPU_NONNULL(b); XPU_NONNULL(c); XPU_NONNULL(work);
+    XPU_TRY(ensure_device());
+    hipStream_t st = as_stream(stream);
+    XPU_TRY(launched(transpose_i8(st, b, work, K, N), "int8_gemm_nn (transpose)"));
+    return launched(gemm_i32(st, a, K, work, K, c, N, int(M), int(N), int(K)), "int8_gemm_nn");
+}
+
+int xpuint8_linear_gemm_stream(const void* stream, const int8_t* xq, const float* x_scale,
+                               const int8_t* w8, const float* w_scale, const float* bias,
+                               void* out, int64_t M, int64_t N, int64_t K) {
+    XPU_TRY(check_epilogue(M, N));
+    XPU_TRY(check_gemm(M, N, K));
+    XPU_NONNULL(xq); XPU_NONNULL(x_scale); XPU_NONNULL(w8); XPU_NONNULL(w_scale);
+    XPU_NONNULL(out);
+    XPU_ALIGNED_OPT(bias);
+    XPU_TRY(ensure_device());
+    return launched(gemm_dequant(as_stream(stream), xq, K, w8, K, out, N, x_scale, w_scale, bias,
+                                 int(M), int(N), int(K)),
+                    "linear_gemm");
+}
+
+int xpuint8_dx_gemm_stream(const void* stream, const int8_t* q, const float* a, const int8_t* w8,
+                           void* dx, int64_t M, int64_t N, int64_t K, int8_t* work) {
+    // q [M,N] @ w8 [N,K] -> dx [M,K]; the contraction runs over N
+    XPU_TRY(check_gemm(M, K, N));
+    XPU_NONNULL(q); XPU_NONNULL(a); XPU_NONNULL(w8); XPU_NONNULL(dx); XPU_NONNULL(work);
+    XPU_TRY(ensure_device());
+    hipStream_t st = as_stream(stream);
+    XPU_TRY(launched(transpose_i8(st, w8, work, N, K), "dx_gemm (transpose)"));
+    return launched(gemm_dequant(st, q, N, work, N, dx, K, a, nullptr, nullptr, int(M), int(K),
+                                 int(N)),
+                    "dx_gemm");
+}
+
+// ------------------------------------------------------ prepare / row quant
+int xpuint8_prepare_weight_stream(const void* stream, const void* w, int8_t* q, float* scale,
+                                  int64_t N, int64_t K) {
+    XPU_TRY(check_rows(N, K));
+    XPU_NONNULL(w); XPU_NONNULL(q); XPU_NONNULL(scale);
+    XPU_TRY(ensure_device());
+    return launched(prepare_weight(as_stream(stream), w, q, scale, N, int(K)), "prepare_weight");
+}
+
+int xpuint8_quantize_row_stream(const void* stream, const void* x, const float* col_scale,
+                                int8_t* q, float* scale, int64_t M, int64_t N) {
+    XPU_TRY(check_epilogue(M, N));
+    if (N > kMaxK) return fail(4, "rows longer than 131072 are not supported");
+    XPU_NONNULL(x); XPU_NONNULL(q); XPU_NONNULL(scale);
+    XPU_ALIGNED_OPT(col_scale);
+    XPU_TRY(ensure_device());
+    return launched(quantize_row(as_stream(stream), x, col_scale, q, scale, M, int(N)),
+                    "quantize_row");
+}
+
+int xpuint8_activation_table(int32_t id, uint16_t* out) {
+    if (id < 0 || id >= kNumTables) return fail(6, "table id must be 0..5");
+    XPU_NONNULL(out);
+    std::memcpy(out, host_activation_tables() + size_t(id) * kTabSize, sizeof(uint16_t) * kTabSize);
+    return 0;
+}
+
+}  // extern "C"

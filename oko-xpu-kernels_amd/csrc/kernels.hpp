@@ -1,0 +1,39 @@
+// Internal launchers (one per kernel family).  All are asynchronous on the
+// given stream, validate nothing (the C ABI in capi.hip does), and return the
+// launch status.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace xpuint8 {
+
+// rowquant.hip
+hipError_t convrot_quantize(hipStream_t st, const void* x, int8_t* q, float* scale, int64_t M,
+                            int K, int act);
+hipError_t dequant_act_quantize(hipStream_t st, const int32_t* acc, int64_t acc_ld, int8_t* q,
+                                float* scale, const float* xs, const float* ws, int64_t M, int K,
+                                int act);
+hipError_t rotate_bf16(hipStream_t st, const void* x, void* out, int64_t M, int K);
+hipError_t dequant_weight(hipStream_t st, const int8_t* w8, const float* scale, void* out,
+                          int64_t N, int K);
+hipError_t prepare_weight(hipStream_t st, const void* w, int8_t* q, float* scale, int64_t N,
+                          int K);
+hipError_t quantize_row(hipStream_t st, const void* x, const float* colscale, int8_t* q,
+                        float* scale, int64_t M, int N);
+
+// gemm_i8.hip
+hipError_t gemm_i32(hipStream_t st, const int8_t* A, int64_t lda, const int8_t* B, int64_t ldb,
+                    int32_t* C, int64_t ldc, int M, int N, int K);
+hipError_t gemm_dequant(hipStream_t st, const int8_t* A, int64_t lda, const int8_t* B, int64_t ldb,
+                        void* out, int64_t ldo, const float* xs, const float* ws, const float* bias,
+                        int M, int N, int K);
+hipError_t dequant_epilogue(hipStream_t st, const int32_t* acc, int64_t acc_ld, void* out,
+                            const float* xs, const float* ws, const float* bias, int64_t M,
+                            int64_t N);
+hipError_t transpose_i8(hipStream_t st, const int8_t* in, int8_t* out, int64_t R, int64_t C);
+
+// tables.hip: the host copy of the activation tables (activations.hpp)
+const uint16_t* host_activation_tables();
+
+}  // namespace xpuint8

@@ -1,0 +1,646 @@
+"""The INT8 API on ROCm tensors: weight preparation, the linear, the accumulator
+paths, the FFN and the backward.
+
+The counterpart of the reference's ``python/xpu_kernels/int8/ops.py`` (line
+numbers cited per function): the same names, arguments, error types and
+message substrings, with every kernel -- including the GEMMs and the chains the
+reference left to torch -- running in ``libxpuint8.so`` on the caller's
+current HIP stream.  Nothing here synchronises, and nothing falls back to a
+torch or CPU implementation: without the library every kernel call raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Optional
+
+import torch
+
+from .._capture import is_capturing
+from ._lib import (
+    ACTIVATIONS,
+    PAIRED_ACTIVATIONS,
+    _c,
+    _err,
+    _flat2d,
+    _lib,
+    _ptr,
+    _stream,
+    load,
+)
+
+_NULL = ctypes.c_void_p(0)
+
+
+def _opt(t):
+    return _NULL if t is None else _ptr(t)
+
+
+def rotate(x):
+    """ConvRot rotation only: bf16 [.., K] in, bf16 [.., K] out (ops.py:26-37)."""
+    lib = _lib()
+    x2, shape = _flat2d(x)
+    out = torch.empty_like(x2)
+    m, k = x2.shape
+    rc = lib.xpuint8_convrot_rotate_bf16_stream(_stream(x.device), _ptr(x2), _ptr(out), m, k)
+    if rc != 0:
+        _err(lib, "rotate")
+    return out.reshape(shape)
+
+
+def quantize(x):
+    """Rotate and quantize an activation: bf16 [.., K] -> (int8 [.., K], fp32 [..])
+    (ops.py:40-52)."""
+    lib = _lib()
+    x2, shape = _flat2d(x)
+    m, k = x2.shape
+    q = torch.empty((m, k), device=x.device, dtype=torch.int8)
+    scale = torch.empty((m,), device=x.device, dtype=torch.float32)
+    rc = lib.xpuint8_convrot_quantize_stream(_stream(x.device), _ptr(x2), _ptr(q), _ptr(scale),
+                                             m, k)
+    if rc != 0:
+        _err(lib, "quantize")
+    return q.reshape(*shape[:-1], k), scale.reshape(shape[:-1])
+
+
+def quantize_act(x, activation: str):
+    """Rotate+quantize with an activation fused into the load (ops.py:55-80).
+
+    ``gelu_tanh``/``gelu_erf`` consume [.., K]; ``swiglu``, ``situ`` and
+    ``geglu_erf`` consume [.., 2K]; the result is [.., K].
+    """
+    lib = _lib()
+    x2, shape = _flat2d(x)
+    m, k2 = x2.shape
+    act = ACTIVATIONS[activation]
+    k = k2 // 2 if activation in PAIRED_ACTIVATIONS else k2
+    q = torch.empty((m, k), device=x.device, dtype=torch.int8)
+    scale = torch.empty((m,), device=x.device, dtype=torch.float32)
+    rc = lib.xpuint8_convrot_quantize_act_stream(_stream(x.device), _ptr(x2), _ptr(q),
+                                                 _ptr(scale), m, k, act)
+    if rc != 0:
+        _err(lib, "quantize_act")
+    return q.reshape(*shape[:-1], k), scale.reshape(shape[:-1])
+
+
+def prepare_weight(w, group: int = 256):
+    """Prepare an INT8 weight for :func:`linear` (ops.py:83-100).
+
+    ``w`` is bf16 or fp32 [N, K] in the unrotated orientation.  Returns
+    ``(int8 [N, K], fp32 [N])``.  One kernel, bit-identical to the reference's
+    torch chain: rotate to bf16, the bf16 row absmax floored at bf16(1e-30),
+    ``s = amax / 127`` and ``round(wr / s)`` with an IEEE division.
+    """
+    if w.shape[1] % group:
+        raise ValueError(f"K={w.shape[1]} is not a multiple of the group size {group}")
+    lib = _lib()
+    w2 = _c(w.detach().to(device=w.device, dtype=torch.bfloat16))
+    n, k = w2.shape
+    q = torch.empty((n, k), device=w.device, dtype=torch.int8)
+    scale = torch.empty((n,), device=w.device, dtype=torch.float32)
+    rc = lib.xpuint8_prepare_weight_stream(_stream(w.device), _ptr(w2), _ptr(q), _ptr(scale), n, k)
+    if rc != 0:
+        _err(lib, "prepare_weight")
+    return q, scale
+
+
+def prepare_weight_fused(w, group: int = 256):
+    """The ConvRot quantizer applied to the weight (ops.py:103-124): the rotated
+    values stay fp32 (no bf16 round before the absmax), so it differs from
+    :func:`prepare_weight` in the last bit of some codes -- a different function
+    on purpose."""
+    if w.shape[1] % group:
+        raise ValueError(f"K={w.shape[1]} is not a multiple of the group size {group}")
+    return quantize(w.detach().to(device=w.device, dtype=torch.bfloat16).contiguous())
+
+
+def dequant_weight(w8, w_scale):
+    """The unrotated bf16 weight behind an INT8 ConvRot weight (ops.py:127-166):
+    ``rotate(bf16(w8 * s))`` in one kernel, bit-identical to
+    :func:`dequant_weight_torch`."""
+    if w8.dtype != torch.int8:
+        raise TypeError(f"w8 must be int8, got {w8.dtype}")
+    if w8.dim() != 2 or w8.shape[1] % 256 or w_scale.numel() not in (1, w8.shape[0]):
+        raise TypeError(f"w8 must be int8 [N, K] with K % 256 == 0 and a [N] or scalar "
+                        f"scale; got {tuple(w8.shape)} and {w_scale.numel()} scales")
+    lib = _lib()
+    w8c = _c(w8)
+    scale = expand_scale(w_scale.detach(), w8.shape[0], w8.device)
+    out = torch.empty(w8.shape, dtype=torch.bfloat16, device=w8.device)
+    rc = lib.xpuint8_dequant_weight_stream(_stream(w8.device), _ptr(w8c), _ptr(scale), _ptr(out),
+                                           w8.shape[0], w8.shape[1])
+    if rc != 0:
+        _err(lib, "dequant_weight")
+    return out
+
+
+def dequant_weight_torch(w8, w_scale):
+    """The weight dequantization as a torch chain -- the definition
+    (ops.py:169-191): fp32 multiply, bf16 round, then the rotation undone."""
+    if w8.dtype != torch.int8:
+        raise TypeError(f"w8 must be int8, got {w8.dtype}")
+    if is_capturing():
+        raise RuntimeError(
+            "dequant_weight() materializes a full-precision copy of the weight; inside a "
+            "device-graph capture it would be captured and re-computed on every replay. "
+            "Call it before capturing, or use the int8 backward "
+            "(xpu_kernels.int8_linear(..., mode='int8')), which needs no copy at all.")
+    w = w8.to(torch.float32) * w_scale.to(torch.float32).reshape(-1, 1)
+    return rotate(w.to(torch.bfloat16))
+
+
+def linear_dx(dy, w):
+    """``dL/dx = dy [.., N] @ w [N, K]`` for an unrotated weight (ops.py:194-204)."""
+    if dy.shape[-1] != w.shape[0]:
+        raise ValueError(f"dy has {dy.shape[-1]} columns but w has {w.shape[0]} rows")
+    return dy @ w
+
+
+def linear_dw(dy, x):
+    """``dL/dW = dy [.., N]^T @ x [.., K] -> [N, K]`` (ops.py:207-238).
+
+    The contraction runs over the batch (token) dimension, so the batch dims
+    must agree.
+    """
+    if dy.shape[-2] != x.shape[-2]:
+        raise ValueError(
+            f"dy has {dy.shape[-2]} rows but x has {x.shape[-2]}: the batch "
+            f"dims must match for dy^T @ x")
+    return dy.reshape(-1, dy.shape[-1]).transpose(0, 1) @ x.reshape(-1, x.shape[-1])
+
+
+class _Int8LinearFn(torch.autograd.Function):
+    """The INT8 linear as an autograd op (ops.py:241-289): forward is
+    :func:`linear`; backward is dbias plus dx through :func:`linear_dx_int8`
+    (``mode="int8"``) or :func:`linear_dx` on the dequantized weight
+    (``mode="dense"``).  The frozen int8 weight gets no gradient."""
+
+    @staticmethod
+    def forward(ctx, x, w8, w_scale, bias, mode):
+        ctx.save_for_backward(w8, w_scale)
+        ctx.mode = mode
+        ctx.input_dtype = x.dtype
+        return linear(x, w8, w_scale, bias)
+
+    @staticmethod
+    def backward(ctx, dy):
+        w8, w_scale = ctx.saved_tensors
+        dbias = dy.sum(dim=0) if ctx.needs_input_grad[3] else None
+        dy = dy.to(torch.bfloat16)
+        if ctx.mode == "int8":
+            dx = linear_dx_int8(dy, w8, w_scale)
+        elif ctx.mode == "dense":
+            dx = linear_dx(dy, dequant_weight(w8, w_scale))
+        else:
+            raise ValueError(f"unknown backward mode {ctx.mode!r}; use 'dense' or 'int8'")
+        return dx.to(ctx.input_dtype), None, None, dbias, None
+
+
+def int8_linear(x, w8, w_scale, bias=None, *, mode="dense"):
+    """The INT8 linear, differentiable (ops.py:292-317).  ``mode`` is
+    ``"dense"`` (dequantized weight in the backward) or ``"int8"`` (weight stays
+    int8, ``dy`` is row-quantized)."""
+    if mode not in ("dense", "int8"):
+        raise ValueError(f"unknown backward mode {mode!r}; use 'dense' or 'int8'")
+    return _Int8LinearFn.apply(x, w8, w_scale, bias, mode)
+
+
+def quantize_row_torch(x):
+    """The per-row quantizer as a torch chain -- the definition (ops.py:320-330)."""
+    xf = x.to(torch.float32)
+    scale = (xf.abs().amax(dim=-1, keepdim=True) / 127.0).clamp_min(1e-30)
+    q = torch.round(xf / scale).clamp_(-127, 127).to(torch.int8)
+    return q.contiguous(), scale.squeeze(-1).contiguous()
+
+
+def quantize_row(x, col_scale=None):
+    """Per-row symmetric int8 quantization, no rotation: bf16 [.., N] ->
+    (int8 [.., N], fp32 [..]) (ops.py:333-350), bit-identical to
+    :func:`quantize_row_torch`.  ``col_scale`` ([N], optional) first replaces
+    the row by ``bf16(x * bf16(col_scale))``, the product linear_dx_int8 needs."""
+    lib = _lib()
+    x2, shape = _flat2d(x)
+    m, n = x2.shape
+    if n % 16:
+        raise TypeError(f"quantize_row needs a multiple of 16 columns, got {n}")
+    cs = None if col_scale is None else expand_scale(col_scale, n, x.device)
+    q = torch.empty((m, n), device=x.device, dtype=torch.int8)
+    scale = torch.empty((m,), device=x.device, dtype=torch.float32)
+    rc = lib.xpuint8_quantize_row_stream(_stream(x.device), _ptr(x2), _opt(cs), _ptr(q),
+                                         _ptr(scale), m, n)
+    if rc != 0:
+        _err(lib, "quantize_row")
+    return q.reshape(*shape[:-1], n), scale.reshape(shape[:-1])
+
+
+def linear_dx_int8(dy, w8, w_scale):
+    """``dL/dx`` against the weight still in int8 (ops.py:353-377):
+    ``d = bf16(dy) * bf16(ws)``, row-quantized, ``acc = q @ w8`` (int32), then
+    ``bf16(acc * a[m])`` and the rotation undone."""
+    lib = _lib()
+    n, k = int(w8.shape[0]), int(w8.shape[1])
+    d2 = _c(dy.to(torch.bfloat16).reshape(-1, n))
+    m = d2.shape[0]
+    q, a = quantize_row(d2, w_scale)
+    work = torch.empty((k * n,), device=dy.device, dtype=torch.int8)
+    dx = torch.empty((m, k), device=dy.device, dtype=torch.bfloat16)
+    w8c = _c(w8)
+    rc = lib.xpuint8_dx_gemm_stream(_stream(dy.device), _ptr(q), _ptr(a), _ptr(w8c), _ptr(dx),
+                                    m, n, k, _ptr(work))
+    if rc != 0:
+        _err(lib, "linear_dx_int8")
+    return rotate(dx).reshape(*dy.shape[:-1], k)
+
+
+def expand_scale(scale, n, device=None):
+    """A flat fp32 ``[n]`` scale, broadcasting a per-tensor scalar (ops.py:380-408).
+    Returns ``scale`` itself when it already is a flat fp32 [n] tensor on the
+    device."""
+    if not isinstance(scale, torch.Tensor):
+        if not isinstance(scale, (float, int)):
+            raise TypeError(f"scale must be a tensor or a python float, "
+                            f"got {type(scale).__name__}")
+        if device is None:
+            raise TypeError("a python-scalar scale needs an explicit device")
+        return torch.full((n,), float(scale), device=device, dtype=torch.float32)
+    if (scale.dtype == torch.float32 and scale.dim() == 1 and scale.numel() == n
+            and scale.is_contiguous() and (device is None or scale.device == device)
+            and scale.data_ptr() % 16 == 0):
+        return scale
+    s = scale.reshape(-1).to(device=device or scale.device, dtype=torch.float32)
+    if s.numel() == 1 and n != 1:
+        s = s.expand(n)
+    return _c(s)
+
+
+def _dims(x, w8, act):
+    m = 1
+    for d in x.shape[:-1]:
+        m *= int(d)
+    return m, int(w8.shape[0]), int(w8.shape[1])
+
+
+def unsupported_reason(x, w8, w_scale, act=None):
+    """Why this call cannot use the fused kernels, or ``None`` if it can
+    (ops.py:418-476).  :func:`linear` raises exactly this message."""
+    if not isinstance(x, torch.Tensor) or not isinstance(w8, torch.Tensor):
+        return "activation and weight must be torch tensors"
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        return (f"activation dtype {x.dtype} is not bfloat16 or float32 "
+                f"(the kernels consume bf16)")
+    if w8.dtype != torch.int8 or w8.dim() != 2:
+        return f"weight must be an int8 [N, K] tensor, got {w8.dtype} {tuple(w8.shape)}"
+    if act is not None and act not in ACTIVATIONS:
+        return (f"unknown activation {act!r}; expected None or one of "
+                f"{', '.join(sorted(ACTIVATIONS))}")
+    k = int(w8.shape[1])
+    want = k * 2 if act in PAIRED_ACTIVATIONS else k
+    if x.shape[-1] != want:
+        return (f"activation has {x.shape[-1]} columns but this weight wants "
+                f"{want} (K={k}{' with two halves' if want != k else ''})")
+    if k % 256:
+        return f"K={k} is not a multiple of the ConvRot group size (256)"
+    if w8.shape[0] % 16:
+        return (f"N={w8.shape[0]} is not a multiple of 16; the dequant epilogue "
+                f"reads the output 16 columns at a time and would drop the tail")
+    if isinstance(w_scale, torch.Tensor):
+        if not w_scale.is_floating_point():
+            return (f"weight scale dtype {w_scale.dtype} is not floating point; "
+                    f"a per-channel scale is amax/127")
+        if w_scale.dim() > 2:
+            return (f"weight scale has {w_scale.dim()} dims; expected a scalar, "
+                    f"[N] or [N, 1]")
+        if w_scale.numel() not in (1, w8.shape[0]):
+            return (f"weight scale has {w_scale.numel()} values; expected 1 or "
+                    f"N={w8.shape[0]}")
+    elif not isinstance(w_scale, (float, int)):
+        return "weight scale must be a tensor or a python float"
+    if load() is None:
+        return "libxpuint8.so is not available (see xpu_kernels.int8._lib)"
+    if x.device.type != "cuda":
+        return f"activation is on {x.device}; the kernels need a GPU (ROCm) tensor"
+    if w8.device != x.device:
+        return (f"weight is on {w8.device} but the activation is on {x.device}; "
+                f"the kernels take raw pointers into one stream")
+    return None
+
+
+def int_mm(a, b):
+    """``torch._int_mm`` semantics on the library's MFMA GEMM: int8 a [M, K] @
+    int8 b [K, N] -> int32 [M, N].  ``b`` given as ``w8.t()`` (a transposed view
+    of a contiguous [N, K] weight) takes the NT kernel directly; a contiguous
+    [K, N] ``b`` is transposed into a scratch buffer first."""
+    lib = _lib()
+    if a.dtype != torch.int8 or b.dtype != torch.int8 or a.dim() != 2 or b.dim() != 2:
+        raise TypeError("int_mm takes two 2-D int8 tensors")
+    m, k = a.shape
+    if b.shape[0] != k:
+        raise ValueError(f"K mismatch: a has {k} columns, b has {b.shape[0]} rows")
+    n = b.shape[1]
+    a = _c(a)
+    c = torch.empty((m, n), device=a.device, dtype=torch.int32)
+    st = _stream(a.device)
+    if b.t().is_contiguous() and b.data_ptr() % 16 == 0:
+        rc = lib.xpuint8_int8_gemm_stream(st, _ptr(a), _ptr(b.t()), _ptr(c), m, n, k)
+    else:
+        b = _c(b)
+        work = torch.empty((k * n,), device=a.device, dtype=torch.int8)
+        rc = lib.xpuint8_int8_gemm_nn_stream(st, _ptr(a), _ptr(b), _ptr(c), m, n, k, _ptr(work))
+    if rc != 0:
+        _err(lib, "int_mm")
+    return c
+
+
+def dequant(acc, x_scale, w_scale, bias=None):
+    """bf16 dequant of an int32 [M, N] accumulator (ops.py:479-497)."""
+    lib = _lib()
+    if acc.dim() != 2 or acc.dtype != torch.int32:
+        raise TypeError("acc must be an int32 [M, N] tensor")
+    m, n = acc.shape
+    acc = _c(acc)
+    out = torch.empty((m, n), device=acc.device, dtype=torch.bfloat16)
+    xs, ws = expand_scale(x_scale, m, acc.device), expand_scale(w_scale, n, acc.device)
+    b = None if bias is None else expand_scale(bias, n, acc.device)
+    rc = lib.xpuint8_dequant_epilogue_stream(_stream(acc.device), _ptr(acc), _ptr(out), _ptr(xs),
+                                             _ptr(ws), _opt(b), m, n)
+    if rc != 0:
+        _err(lib, "dequant")
+    return out
+
+
+def dequant_slice(acc, x_scale, w_scale, bias=None):
+    """As :func:`dequant`, for a [M, N] column slice of a wider accumulator,
+    read in place through its row stride (ops.py:500-525)."""
+    lib = _lib()
+    if acc.dim() != 2 or acc.dtype != torch.int32:
+        raise TypeError("acc must be an int32 [M, N] tensor")
+    if acc.stride(1) != 1 or acc.stride(0) % 4 or acc.data_ptr() % 16:
+        acc = acc.contiguous() if acc.stride(1) != 1 else acc
+        if acc.stride(0) % 4 or acc.data_ptr() % 16:
+            acc = acc.clone()
+    m, n = acc.shape
+    out = torch.empty((m, n), device=acc.device, dtype=torch.bfloat16)
+    xs, ws = expand_scale(x_scale, m, acc.device), expand_scale(w_scale, n, acc.device)
+    b = None if bias is None else expand_scale(bias, n, acc.device)
+    rc = lib.xpuint8_dequant_epilogue_slice_stream(_stream(acc.device), _ptr(acc), _ptr(out),
+                                                   _ptr(xs), _ptr(ws), _opt(b), m, n,
+                                                   acc.stride(0))
+    if rc != 0:
+        _err(lib, "dequant_slice")
+    return out
+
+
+def dequant_act_quantize(acc, x_scale, w_scale, activation="situ"):
+    """Dequant, activate, rotate and quantize an up-projection accumulator
+    (ops.py:528-568): int32 [M, 2K] (paired) or [M, K] -> (int8 [M, K], fp32 [M])."""
+    lib = _lib()
+    act_id = ACTIVATIONS[activation]
+    paired = activation in PAIRED_ACTIVATIONS
+    if acc.dim() != 2 or acc.dtype != torch.int32:
+        raise TypeError("acc must be an int32 [M, N] tensor")
+    m, n = acc.shape
+    if paired:
+        if n % 2:
+            raise TypeError(f"acc must be an int32 [M, 2K] tensor for {activation}, "
+                            f"got {n} columns")
+        k = n // 2
+    else:
+        k = n
+    acc = _c(acc)
+    q = torch.empty((m, k), device=acc.device, dtype=torch.int8)
+    scale = torch.empty((m,), device=acc.device, dtype=torch.float32)
+    xs = expand_scale(x_scale, m, acc.device)
+    ws = expand_scale(w_scale, n, acc.device)
+    rc = lib.xpuint8_dequant_act_quantize_stream(_stream(acc.device), _ptr(acc), _ptr(q),
+                                                 _ptr(scale), _ptr(xs), _ptr(ws), m, k, act_id)
+    if rc != 0:
+        _err(lib, "dequant_act_quantize")
+    return q, scale
+
+
+def linear_acc(x, w8, w_scale, act: Optional[str] = None):
+    """The GEMM without the output dequant: ``(int32 [M, N], fp32 [M])``
+    (ops.py:571-588)."""
+    if act is None:
+        xq, xs = quantize(x)
+    else:
+        xq, xs = quantize_act(x, act)
+    if w8.dtype != torch.int8 or w8.dim() != 2:
+        raise TypeError("w8 must be an int8 [N, K] tensor")
+    if xq.shape[-1] != w8.shape[1]:
+        raise ValueError(f"K mismatch: activation {xq.shape[-1]} vs weight {w8.shape[1]}")
+    acc = int_mm(xq.reshape(-1, xq.shape[-1]), w8.contiguous().t())
+    return acc, xs.reshape(-1)
+
+
+def linear(x, w8, w_scale, bias=None, act: Optional[str] = None, residual=None,
+           residual_scale=None, return_acc: bool = False):
+    """INT8 ConvRot linear: bf16/fp32 [.., K] -> bf16/fp32 [.., N] (ops.py:591-646).
+
+    Two kernels: rotate+quantize of ``x`` (with ``act`` fused into its load),
+    then the MFMA GEMM with the dequant (+bias) epilogue fused into its store.
+    ``residual``/``residual_scale`` apply ``residual + residual_scale * out``;
+    ``return_acc`` returns ``(int32 [M, N], fp32 [M], fp32 [N])`` instead.
+    """
+    reason = unsupported_reason(x, w8, w_scale, act)
+    if reason is not None:
+        raise TypeError(reason)
+    if return_acc and (bias is not None or residual is not None):
+        raise ValueError("return_acc skips the epilogue, so bias and residual "
+                         "cannot be applied")
+    m, n, k = _dims(x, w8, act)
+    input_dtype = x.dtype
+    x2 = x.reshape(m, -1)
+    if x2.dtype != torch.bfloat16:
+        x2 = x2.to(dtype=torch.bfloat16)
+    if not x2.is_contiguous():
+        x2 = x2.contiguous()
+
+    if act is None:
+        xq, xs = quantize(x2)
+    else:
+        xq, xs = quantize_act(x2, act)
+    w8c = _c(w8)
+    if return_acc:
+        acc = int_mm(xq, w8c.t())
+        return acc, xs.reshape(-1), expand_scale(w_scale, n, acc.device)
+
+    lib = _lib()
+    ws = expand_scale(w_scale, n, x.device)
+    b = None if bias is None else expand_scale(bias, n, x.device)
+    out = torch.empty((m, n), device=x.device, dtype=torch.bfloat16)
+    rc = lib.xpuint8_linear_gemm_stream(_stream(x.device), _ptr(xq), _ptr(xs), _ptr(w8c),
+                                        _ptr(ws), _opt(b), _ptr(out), m, n, k)
+    if rc != 0:
+        _err(lib, "linear")
+    if residual is not None:
+        residual = residual.reshape(m, n).to(
+            out.dtype if input_dtype == torch.bfloat16 else input_dtype)
+        if input_dtype != torch.bfloat16:
+            out = out.to(dtype=input_dtype)
+        out = torch.addcmul(residual, out, residual_scale)
+    out = out.reshape(*x.shape[:-1], n)
+    return out if input_dtype == torch.bfloat16 else out.to(dtype=input_dtype)
+
+
+def ffn(x, up_w8, up_scale, down_w8, down_scale, down_bias=None, act="situ"):
+    """``act(up(x)) @ down.T`` (ops.py:649-719).  ``up_w8`` is [2*ffn, K]
+    (``[hidden | gate]``) for a paired activation and [ffn, K] for
+    ``gelu_erf``; ``down_w8`` is [K, ffn].  The up projection is unbiased."""
+    if act not in ACTIVATIONS:
+        raise TypeError(f"unknown activation {act!r}; "
+                        f"known: {', '.join(sorted(ACTIVATIONS))}")
+    if act not in ("situ", "geglu_erf", "gelu_erf"):
+        raise TypeError(f"the fused FFN supports situ, geglu_erf and gelu_erf, "
+                        f"not {act!r}")
+    paired = act in PAIRED_ACTIVATIONS
+    reason = unsupported_reason(x, up_w8, up_scale, None)
+    if reason is not None:
+        raise TypeError(reason)
+    m, n, k = _dims(x, up_w8, None)
+    if paired and n % 2:
+        raise TypeError(f"up-projection N={n} must be 2*ffn for the {act} activation")
+    inner = n // 2 if paired else n
+    if inner % 256 or inner % 16:
+        raise TypeError(f"the FFN's inner width {inner} must be a multiple of "
+                        f"256 (and of 16) for the fused {act} epilogue")
+    if down_w8.dtype != torch.int8 or down_w8.dim() != 2:
+        raise TypeError(f"down weight must be an int8 [K, ffn] tensor, got "
+                        f"{down_w8.dtype} {tuple(down_w8.shape)}")
+    if tuple(down_w8.shape) != (k, inner):
+        raise TypeError(f"down weight is {tuple(down_w8.shape)}, expected {(k, inner)}")
+    if down_w8.device != x.device:
+        raise TypeError(f"down weight is on {down_w8.device} but the activation "
+                        f"is on {x.device}")
+    if isinstance(down_scale, torch.Tensor):
+        if down_scale.dtype != torch.float32 or down_scale.dim() > 2:
+            raise TypeError("down weight scale must be a float32 scalar or [K]")
+        if down_scale.numel() not in (1, k):
+            raise TypeError(f"down weight scale has {down_scale.numel()} values; "
+                            f"expected 1 or K={k}")
+    elif not isinstance(down_scale, (float, int)):
+        raise TypeError("down weight scale must be a tensor or a python float")
+
+    device = x.device
+    input_dtype = x.dtype
+    x2 = x.reshape(m, k)
+    if x2.dtype != torch.bfloat16:
+        x2 = x2.to(dtype=torch.bfloat16)
+    if not x2.is_contiguous():
+        x2 = x2.contiguous()
+
+    xq, xs = quantize(x2)
+    acc = int_mm(xq, up_w8.contiguous().t())
+    q2, xs2 = dequant_act_quantize(acc, xs, expand_scale(up_scale, n, device), act)
+    lib = _lib()
+    dw8 = _c(down_w8)
+    ds = expand_scale(down_scale, k, device)
+    b = None if down_bias is None else expand_scale(down_bias, k, device)
+    out = torch.empty((m, k), device=device, dtype=torch.bfloat16)
+    rc = lib.xpuint8_linear_gemm_stream(_stream(device), _ptr(q2), _ptr(xs2), _ptr(dw8),
+                                        _ptr(ds), _opt(b), _ptr(out), m, k, inner)
+    if rc != 0:
+        _err(lib, "ffn")
+    out = out.reshape(*x.shape[:-1], k)
+    return out if input_dtype == torch.bfloat16 else out.to(dtype=input_dtype)
+
+
+def ffn_situ(x, up_w8, up_scale, down_w8, down_scale, down_bias=None):
+    """:func:`ffn` with MossImage's activation (ops.py:722-727)."""
+    return ffn(x, up_w8, up_scale, down_w8, down_scale, down_bias, act="situ")
+
+
+class TrainableInt8Linear(torch.nn.Module):
+    """A linear whose bf16 parameter is quantized on every forward with
+    :func:`prepare_weight_fused` (straight-through; ops.py:730-789)."""
+
+    def __init__(self, weight, bias=None, *, backward="ste"):
+        super().__init__()
+        if weight.dtype not in (torch.bfloat16, torch.float32):
+            raise TypeError(f"the weight must be bfloat16 or float32, got {weight.dtype}")
+        if backward not in ("ste", "dense"):
+            raise ValueError(f"unknown backward mode {backward!r}; use 'ste' or 'dense'")
+        self.weight = torch.nn.Parameter(weight.detach())
+        self.bias = None if bias is None else torch.nn.Parameter(
+            bias.detach().to(self.weight.dtype))
+        self.backward = backward
+
+    @classmethod
+    def from_linear(cls, mod, *, backward="ste"):
+        return cls(mod.weight.detach(), getattr(mod, "bias", None), backward=backward)
+
+    def forward(self, x):
+        return _TrainableInt8LinearFn.apply(x, self.weight, self.bias, self.backward)
+
+    def extra_repr(self):
+        return (f"{tuple(self.weight.shape)}, backward={self.backward}, "
+                f"bias={self.bias is not None}")
+
+
+class _TrainableInt8LinearFn(torch.autograd.Function):
+    """The autograd op behind :class:`TrainableInt8Linear` (ops.py:792-824)."""
+
+    @staticmethod
+    def forward(ctx, x, weight, bias, mode):
+        w8, ws = prepare_weight_fused(weight)
+        y = linear(x, w8, ws, bias)
+        ctx.save_for_backward(x, weight, w8, ws)
+        ctx.mode = mode
+        ctx.has_bias = bias is not None
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, weight, w8, ws = ctx.saved_tensors
+        dy = dy.reshape(-1, dy.shape[-1])
+        x2 = x.reshape(-1, x.shape[-1])
+        w = dequant_weight(w8, ws) if ctx.mode == "dense" else weight
+        dx = dy.to(w.dtype) @ w
+        dw = linear_dw(dy.to(torch.bfloat16), x2.to(torch.bfloat16))
+        db = dy.sum(dim=0) if ctx.has_bias else None
+        if dw.dtype != weight.dtype:
+            dw = dw.to(weight.dtype)
+        return (dx.reshape(x.shape[:-1] + (dx.shape[-1],)), dw, db, None)
+
+
+class Int8Linear(torch.nn.Module):
+    """Drop-in ``nn.Linear`` replacement with prepared weights (ops.py:831-902)."""
+
+    def __init__(self, w8, w_scale, bias=None, *, backward="dense"):
+        super().__init__()
+        self.register_buffer("w8", w8.detach())
+        self.register_buffer("w_scale", w_scale.detach().to(torch.float32))
+        self.bias = None if bias is None else torch.nn.Parameter(
+            bias.detach().to(torch.float32), requires_grad=False)
+        if backward not in ("dense", "int8"):
+            raise ValueError(f"unknown backward mode {backward!r}; use 'dense' or 'int8'")
+        self.backward = backward
+
+    @classmethod
+    def from_linear(cls, mod, *, backward="dense"):
+        q, scale = prepare_weight(mod.weight.detach())
+        return cls(q, scale, getattr(mod, "bias", None), backward=backward)
+
+    def forward(self, x):
+        return int8_linear(x, self.w8, self.w_scale, self.bias, mode=self.backward)
+
+    def dense_weight(self, refresh=False):
+        """The unrotated bf16 weight, dequantized once and cached; refused inside
+        a device-graph capture (ops.py:868-894)."""
+        cached = getattr(self, "_dense", None)
+        if cached is None or refresh:
+            if is_capturing():
+                raise RuntimeError(
+                    "Int8Linear.dense_weight() materializes a second, full-precision copy "
+                    "of the weight; inside a device-graph capture it would be captured and "
+                    "re-computed on every replay. Call it before capturing.")
+            cached = dequant_weight(self.w8, self.w_scale)
+            self._dense = cached
+        return cached
+
+    def dx(self, dy):
+        return linear_dx(dy, self.dense_weight())
+
+    def extra_repr(self):
+        n, k = self.w8.shape
+        return f"in_features={k}, out_features={n}, bias={self.bias is not None}"

@@ -1,0 +1,278 @@
+"""Parity of every HIP entry point with the CPU oracle, on the GPU.
+
+Bar: bit-exact for integer, int8 and index results and for the int32
+accumulators; bit-exact for bf16 outputs too (the kernels reproduce the
+oracle's fp32 operation order), with the reference's own tolerances checked
+separately against reference/convrot_linear.py's chain (int8 code flips
+<= 1e-4 of elements, bf16 rel-err <= 1e-2).  Shapes cover tiny, ragged, the
+two-pass long-row path, and the benchmark configurations at full size.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from gpu_util import activation, bits, from_bits, mismatch, npy, weight
+from xpu_kernels import int8
+
+pytestmark = pytest.mark.gpu
+
+
+# ------------------------------------------------------------------ GEMM
+@pytest.mark.parametrize("m,n,k", [(1, 16, 256), (32, 32, 64), (33, 48, 272), (128, 128, 1280),
+                                   (300, 1040, 1280), (77, 4096, 4096)])
+def test_int8_gemm_exact(dev, m, n, k):
+    rng = np.random.default_rng(m * 7 + n + k)
+    a = rng.integers(-127, 128, (m, k), dtype=np.int8)
+    b = rng.integers(-127, 128, (n, k), dtype=np.int8)
+    got = npy(int8.int_mm(torch.from_numpy(a).to(dev), torch.from_numpy(b).to(dev).t()))
+    want = O.int_mm(a, b)
+    assert np.array_equal(got, want), mismatch(got, want)
+
+
+def test_int8_gemm_extremes(dev):
+    k = 8192
+    a = np.full((64, k), -127, np.int8)
+    b = np.full((64, k), -127, np.int8)
+    b[1::2] = 127
+    got = npy(int8.int_mm(torch.from_numpy(a).to(dev), torch.from_numpy(b).to(dev).t()))
+    assert np.array_equal(got, O.int_mm(a, b))
+
+
+@pytest.mark.parametrize("m,n,k", [(40, 48, 96), (256, 512, 1280)])
+def test_int8_gemm_nn_exact(dev, m, n, k):
+    rng = np.random.default_rng(5)
+    a = rng.integers(-127, 128, (m, k), dtype=np.int8)
+    b = rng.integers(-127, 128, (k, n), dtype=np.int8)          # row-major [K, N]
+    got = npy(int8.int_mm(torch.from_numpy(a).to(dev), torch.from_numpy(b).to(dev)))
+    assert np.array_equal(got, O.int_mm(a, np.ascontiguousarray(b.T)))
+
+
+def test_int8_gemm_full_size_c3(dev):
+    rng = np.random.default_rng(11)
+    a = rng.integers(-127, 128, (4096, 1280), dtype=np.int8)
+    b = rng.integers(-127, 128, (10240, 1280), dtype=np.int8)
+    got = npy(int8.int_mm(torch.from_numpy(a).to(dev), torch.from_numpy(b).to(dev).t()))
+    assert np.array_equal(got, O.int_mm(a, b))
+
+
+# ------------------------------------------------------- rotate / quantize
+QSHAPES = [(1, 256), (7, 1280), (64, 5120), (33, 8192), (5, 3072), (3, 10240), (2, 16384)]
+
+
+@pytest.mark.parametrize("m,k", QSHAPES)
+def test_convrot_quantize_exact(dev, m, k):
+    x = activation(m, k, seed=m + k)
+    q, s = int8.quantize(x.to(dev))
+    wq, ws = O.convrot_quantize(bits(x))
+    assert np.array_equal(npy(s).view(np.uint32), ws.view(np.uint32)), mismatch(npy(s), ws)
+    assert np.array_equal(npy(q), wq), mismatch(npy(q), wq)
+
+
+def test_convrot_quantize_full_size_c2(dev):
+    x = activation(4096, 5120, seed=0)
+    q, s = int8.quantize(x.to(dev))
+    wq, ws = O.convrot_quantize(bits(x))
+    assert np.array_equal(npy(s).view(np.uint32), ws.view(np.uint32))
+    assert np.array_equal(npy(q), wq), mismatch(npy(q), wq)
+    # against the reference oracle's division chain: tie flips only
+    v = O.hadamard256(O.bf16_to_f32(bits(x)))
+    qd = np.clip(np.rint(v / ws[:, None]), -127, 127).astype(np.int8)
+    d = np.abs(npy(q).astype(np.int16) - qd)
+    assert d.max() <= 1 and (d > 0).mean() <= 1e-4
+
+
+def test_quantize_special_rows(dev):
+    x = np.zeros((4, 512), dtype=np.float32)
+    x[1] = 0.5
+    x[2] = -3.0
+    x[3, 7] = 1e-35                       # a lone tiny value
+    xb = O.f32_to_bf16(x)
+    q, s = int8.quantize(from_bits(xb, dev))
+    wq, ws = O.convrot_quantize(xb)
+    assert np.array_equal(npy(q), wq) and np.array_equal(npy(s), ws)
+
+
+@pytest.mark.parametrize("act", [1, 2, 3, 4, 5])
+@pytest.mark.parametrize("m,k", [(9, 1280), (16, 5120)])
+def test_quantize_act_exact(dev, act, m, k):
+    name = {v: kk for kk, v in int8.ACTIVATIONS.items()}[act]
+    width = 2 * k if act in O.PAIRED else k
+    x = activation(m, width, seed=act * 100 + m, scale=1.5)
+    q, s = int8.quantize_act(x.to(dev), name)
+    wq, ws = O.quantize_act(bits(x), act)
+    assert np.array_equal(npy(s), ws), mismatch(npy(s), ws)
+    assert np.array_equal(npy(q), wq), mismatch(npy(q), wq)
+
+
+@pytest.mark.parametrize("m,k", [(1, 256), (13, 1280), (64, 5120), (3, 20480)])
+def test_rotate_exact(dev, m, k):
+    x = activation(m, k, seed=k)
+    got = bits(int8.rotate(x.to(dev)))
+    want = O.rotate_bf16(bits(x))
+    assert np.array_equal(got, want), mismatch(got, want)
+
+
+@pytest.mark.parametrize("n,k", [(16, 256), (48, 1280), (10240, 1280)])
+def test_prepare_weight_exact(dev, n, k):
+    w = weight(n, k, seed=n)
+    if n == 48:
+        w[3] = 0
+        w[5] = 1e-31
+    q, s = int8.prepare_weight(w.to(dev))
+    wq, ws = O.prepare_weight(bits(w))
+    assert np.array_equal(npy(s).view(np.uint32), ws.view(np.uint32)), mismatch(npy(s), ws)
+    assert np.array_equal(npy(q), wq), mismatch(npy(q), wq)
+
+
+def test_prepare_weight_fused_is_the_quantizer(dev):
+    w = weight(64, 1280)
+    q, s = int8.prepare_weight_fused(w.to(dev))
+    wq, ws = O.prepare_weight_fused(bits(w))
+    assert np.array_equal(npy(q), wq) and np.array_equal(npy(s), ws)
+
+
+@pytest.mark.parametrize("n,k", [(32, 512), (5120, 1280)])
+def test_dequant_weight_exact(dev, n, k):
+    w8, ws = O.prepare_weight(bits(weight(n, k)))
+    got = bits(int8.dequant_weight(torch.from_numpy(w8).to(dev), torch.from_numpy(ws).to(dev)))
+    want = O.dequant_weight(w8, ws)
+    assert np.array_equal(got, want), mismatch(got, want)
+
+
+@pytest.mark.parametrize("m,n", [(1, 16), (8, 64), (33, 1040), (4096, 5120)])
+def test_quantize_row_exact(dev, m, n):
+    dy = activation(m, n, seed=m, scale=1e-3, n_out=0)
+    q, s = int8.quantize_row(dy.to(dev))
+    wq, ws = O.quantize_row(bits(dy))
+    assert np.array_equal(npy(s).view(np.uint32), ws.view(np.uint32))
+    assert np.array_equal(npy(q), wq), mismatch(npy(q), wq)
+    qt, st = int8.quantize_row_torch(dy.to(dev))
+    assert torch.equal(q, qt) and torch.equal(s, st)
+
+
+def test_quantize_row_ties(dev):
+    tie = torch.tensor([[127.0, 254.0, -254.0, 63.0] + [0.0] * 12], dtype=torch.bfloat16)
+    q, s = int8.quantize_row(tie.to(dev))
+    assert npy(q)[0, :4].tolist() == [64, 127, -127, 32] and float(s[0]) == 2.0
+
+
+def test_quantize_row_column_scaled(dev):
+    dy = activation(64, 1280, seed=9, scale=1e-3, n_out=0)
+    wsc = (torch.rand(1280, generator=torch.Generator().manual_seed(3)) * 1e-3).float()
+    q, s = int8.quantize_row(dy.to(dev), wsc.to(dev))
+    d = O.f32_to_bf16(O.bf16_to_f32(bits(dy)) * O.bf16_round(npy(wsc))[None, :])
+    wq, ws = O.quantize_row(d)
+    assert np.array_equal(npy(q), wq) and np.array_equal(npy(s), ws)
+
+
+# ------------------------------------------------------------- epilogues
+@pytest.mark.parametrize("bias", [False, True])
+def test_dequant_and_slice_exact(dev, bias):
+    rng = np.random.default_rng(2)
+    acc = rng.integers(-2**22, 2**22, (37, 96)).astype(np.int32)
+    xs = rng.uniform(1e-3, 1e-1, 37).astype(np.float32)
+    ws = rng.uniform(1e-4, 1e-2, 96).astype(np.float32)
+    b = rng.standard_normal(96).astype(np.float32) if bias else None
+    t = lambda a: torch.from_numpy(a).to(dev)
+    got = bits(int8.dequant(t(acc), t(xs), t(ws), None if b is None else t(b)))
+    want = O.dequant(acc, xs, ws, b)
+    assert np.array_equal(got, want), mismatch(got, want)
+    wide = t(np.concatenate([acc, acc[:, :32]], axis=1))
+    sl = bits(int8.dequant_slice(wide[:, :96], t(xs), t(ws), None if b is None else t(b)))
+    assert np.array_equal(sl, want)
+
+
+@pytest.mark.parametrize("act", [3, 4, 5])
+def test_dequant_act_quantize_exact(dev, act):
+    m, k = 24, 1280
+    n = 2 * k if act in O.PAIRED else k
+    rng = np.random.default_rng(act)
+    acc = rng.integers(-300000, 300000, (m, n)).astype(np.int32)
+    xs = rng.uniform(1e-3, 3e-2, m).astype(np.float32)
+    ws = rng.uniform(1e-4, 1e-3, n).astype(np.float32)
+    name = {v: kk for kk, v in int8.ACTIVATIONS.items()}[act]
+    t = lambda a: torch.from_numpy(a).to(dev)
+    q, s = int8.dequant_act_quantize(t(acc), t(xs), t(ws), name)
+    wq, wsc = O.dequant_act_quantize(acc, xs, ws, act)
+    assert np.array_equal(npy(s), wsc) and np.array_equal(npy(q), wq), mismatch(npy(q), wq)
+
+
+# -------------------------------------------------------- linear / ffn / dx
+def test_linear_exact_c1(dev):
+    """Config 1's shapes and recipe (8 outlier channels x20)."""
+    x = activation(1024, 1280, seed=0, n_out=8, mult=20.0)
+    w = weight(1280, 1280, seed=1)
+    bias = weight(1, 1280, seed=2, std=0.01)[0]
+    w8, ws = int8.prepare_weight(w.to(dev))
+    y = int8.linear(x.to(dev), w8, ws, bias.to(dev))
+    want = O.linear(bits(x), npy(w8), npy(ws), O.bf16_to_f32(bits(bias)))
+    assert np.array_equal(bits(y), want), mismatch(bits(y), want)
+    # the reference oracle (reference/convrot_linear.py) fed the rotated activation
+    ref = O.convrot_int8_linear(O.hadamard256(O.bf16_to_f32(bits(x))), npy(w8), npy(ws),
+                                bits(bias))
+    yf, rf = O.bf16_to_f32(bits(y)).astype(np.float64), O.bf16_to_f32(ref).astype(np.float64)
+    assert np.linalg.norm(yf - rf) / np.linalg.norm(rf) < 1e-2
+
+
+def test_linear_full_size_c3(dev):
+    x = activation(4096, 1280, seed=0)
+    w = weight(10240, 1280, seed=1)
+    bias = weight(1, 10240, seed=2, std=0.01)[0]
+    w8, ws = int8.prepare_weight(w.to(dev))
+    y = int8.linear(x.to(dev), w8, ws, bias.to(dev))
+    want = O.linear(bits(x), npy(w8), npy(ws), O.bf16_to_f32(bits(bias)))
+    assert np.array_equal(bits(y), want), mismatch(bits(y), want)
+    acc, xs = int8.linear_acc(x.to(dev), w8, ws)
+    same = int8.dequant(acc, xs, ws, bias.to(dev))
+    assert torch.equal(same.view(torch.int16), y.view(torch.int16))
+
+
+def test_linear_shapes_and_dtypes(dev):
+    x = activation(2 * 3 * 5, 512, seed=3).reshape(2, 3, 5, 512)
+    w = weight(48, 512)
+    w8, ws = int8.prepare_weight(w.to(dev))
+    y = int8.linear(x.to(dev), w8, ws)
+    assert y.shape == (2, 3, 5, 48) and y.dtype == torch.bfloat16
+    y32 = int8.linear(x.float().to(dev), w8, ws)
+    assert y32.dtype == torch.float32 and torch.equal(y32, y.float())
+    want = O.linear(bits(x.reshape(30, 512)), npy(w8), npy(ws))
+    assert np.array_equal(bits(y.reshape(30, 48)), want)
+
+
+def test_ffn_geglu_exact(dev):
+    m, k, inner = 512, 1280, 1280
+    x = activation(m, k, seed=4)
+    up8, ups = int8.prepare_weight(weight(2 * inner, k, seed=5).to(dev))
+    dn8, dns = int8.prepare_weight(weight(k, inner, seed=6).to(dev))
+    db = weight(1, k, seed=7, std=0.01)[0].float()
+    y = int8.ffn(x.to(dev), up8, ups, dn8, dns, db.to(dev), act="geglu_erf")
+    want = O.ffn(bits(x), npy(up8), npy(ups), npy(dn8), npy(dns), npy(db), act=4)
+    assert np.array_equal(bits(y), want), mismatch(bits(y), want)
+
+
+def test_linear_dx_int8_exact(dev):
+    m, n, k = 512, 1280, 1280
+    dy = activation(m, n, seed=8, scale=1e-3, n_out=0)
+    w8, ws = int8.prepare_weight(weight(n, k, seed=9).to(dev))
+    dx = int8.linear_dx_int8(dy.to(dev), w8, ws)
+    want = O.linear_dx_int8(bits(dy), npy(w8), npy(ws))
+    assert np.array_equal(bits(dx), want), mismatch(bits(dx), want)
+
+
+def test_int8_linear_autograd(dev):
+    x = activation(256, 512, seed=10).to(dev).float().requires_grad_(True)
+    w = weight(64, 512, seed=11).to(dev)
+    bias = torch.zeros(64, device=dev, requires_grad=True)
+    w8, ws = int8.prepare_weight(w)
+    dy = torch.randn(256, 64, generator=torch.Generator().manual_seed(0)).to(dev)
+    for mode in ("int8", "dense"):
+        x.grad = None
+        bias.grad = None
+        y = int8.int8_linear(x, w8, ws, bias, mode=mode)
+        y.backward(dy)
+        exact = dy @ w.float()
+        rel = ((x.grad - exact).norm() / exact.norm()).item()
+        assert rel < 0.05, (mode, rel)
+        assert torch.allclose(bias.grad, dy.sum(0))

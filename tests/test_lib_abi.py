@@ -1,0 +1,97 @@
+"""The C ABI without a GPU: the library loads, exports every function
+include/xpuint8.h declares, and rejects bad arguments with the documented
+codes and messages before touching a device (the reference's return-code
+convention, src/xpuint8.cpp:733-776, 999-1002)."""
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from xpu_kernels.int8 import _lib as L
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "xpuint8.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(xpuint8_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    path = L.library_path()
+    assert path is not None, "libxpuint8.so is not built (run __graft_entry__.build())"
+    return L.open_library(path)
+
+
+def test_every_declared_symbol_is_exported_and_bound(lib):
+    names = _declared()
+    assert len(names) >= 25
+    sigs = L._signatures()
+    for n in names:
+        assert hasattr(lib, n), n
+        assert n in sigs, f"{n} has no ctypes signature in _lib.py"
+    assert set(sigs) == set(names)
+
+
+def test_group_size(lib):
+    assert lib.xpuint8_convrot_groupsize() == 256
+
+
+P = ctypes.c_void_p(0x1000)   # never dereferenced: validation runs first
+Z = ctypes.c_void_p(0)
+
+
+def _rc(lib, fn, *args):
+    rc = getattr(lib, fn)(*args)
+    return rc, lib.xpuint8_last_error().decode()
+
+
+@pytest.mark.parametrize("fn,args,code,substr", [
+    ("xpuint8_convrot_quantize_stream", (Z, P, P, P, 4, 384), 3, "256"),
+    ("xpuint8_convrot_quantize_stream", (Z, P, P, P, 0, 512), 2, "positive"),
+    ("xpuint8_convrot_quantize_stream", (Z, Z, P, P, 4, 512), 6, "null"),
+    ("xpuint8_convrot_quantize_act_stream", (Z, P, P, P, 4, 512, 9), 6, "activation"),
+    ("xpuint8_convrot_rotate_bf16_stream", (Z, P, P, 4, 100), 3, "256"),
+    ("xpuint8_dequant_epilogue_stream", (Z, P, P, P, P, Z, 4, 24), 2, "16"),
+    ("xpuint8_dequant_epilogue_slice_stream", (Z, P, P, P, P, Z, 4, 32, 16), 2, "stride"),
+    ("xpuint8_dequant_act_quantize_stream", (Z, P, P, P, P, P, 4, 512, 1), 6, "activation"),
+    ("xpuint8_dequant_weight_stream", (Z, P, P, P, 0, 512), 2, "positive"),
+    ("xpuint8_int8_gemm_stream", (Z, P, P, P, 4, 32, 24), 2, "16"),
+    ("xpuint8_int8_gemm_stream", (Z, P, P, P, 4, 32, 1 << 20), 4, "131072"),
+    ("xpuint8_int8_gemm_nn_stream", (Z, P, P, P, 4, 32, 32, Z), 6, "null"),
+    ("xpuint8_linear_gemm_stream", (Z, P, P, P, P, Z, P, 4, 24, 512), 2, "16"),
+    ("xpuint8_dx_gemm_stream", (Z, P, P, P, P, 4, 24, 512, P), 2, "16"),
+    ("xpuint8_prepare_weight_stream", (Z, P, P, P, 16, 300), 3, "256"),
+    ("xpuint8_quantize_row_stream", (Z, P, Z, P, P, 4, 20), 2, "16"),
+    ("xpuint8_activation_table", (7, P), 6, "0..5"),
+])
+def test_argument_errors_are_reported_without_a_device(lib, fn, args, code, substr):
+    rc, msg = _rc(lib, fn, *args)
+    assert rc == code and substr in msg, (rc, msg)
+
+
+def test_errors_are_per_thread(lib):
+    import threading
+    rc, _ = _rc(lib, "xpuint8_convrot_quantize_stream", Z, P, P, P, 4, 384)
+    seen = {}
+
+    def other():
+        lib.xpuint8_dequant_epilogue_stream(Z, P, P, P, P, Z, 4, 24)
+        seen["msg"] = lib.xpuint8_last_error().decode()
+
+    t = threading.Thread(target=other)
+    t.start()
+    t.join()
+    assert "16" in seen["msg"]
+    assert "256" in lib.xpuint8_last_error().decode()
+
+
+@pytest.mark.skipif(torch.cuda.is_available(), reason="checks the no-device path")
+def test_init_without_a_device_fails_cleanly(lib):
+    rc = lib.xpuint8_init()
+    assert rc == 1 and "device" in lib.xpuint8_last_error().decode().lower()
