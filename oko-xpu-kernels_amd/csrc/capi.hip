@@ -35,6 +35,7 @@ constexpr int kMaxDevices = 64;
 std::mutex g_mutex;
 std::string g_device_name[kMaxDevices];
 const uint16_t* g_tab_dev[kMaxDevices] = {};
+int g_cus[kMaxDevices] = {};
 std::atomic<bool> g_ready[kMaxDevices] = {};
 
 // Per-device set-up: architecture check and table upload.  Returns 0 or an
@@ -61,6 +62,7 @@ int ensure_device() {
     if (e != hipSuccess)
         return fail(5, std::string("uploading the activation tables: ") + hipGetErrorString(e));
     g_tab_dev[dev] = static_cast<const uint16_t*>(sym);
+    g_cus[dev] = prop.multiProcessorCount;
     g_device_name[dev] = prop.name;
     g_ready[dev].store(true, std::memory_order_release);
     return 0;
@@ -101,7 +103,7 @@ int check_epilogue(int64_t M, int64_t N) {
 
 int check_gemm(int64_t M, int64_t N, int64_t K) {
     if (M <= 0 || N <= 0 || K <= 0) return fail(2, "M, N and K must be positive");
-    if (K % 16 != 0) return fail(2, "K must be a multiple of 16");
+    if (K % 16 != 0 || N % 16 != 0) return fail(2, "K and N must be multiples of 16");
     if (K > kMaxK) return fail(4, "K must be <= 131072 (int32 accumulator range)");
     if (M > kMaxGemmM || N > kMaxDim) return fail(4, "M must be <= 8388480 and N < 2^31");
     return 0;
@@ -129,6 +131,13 @@ int act_ok(int32_t act) {
 }
 
 }  // namespace
+
+int device_cus() {
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    const int n = (dev >= 0 && dev < kMaxDevices) ? g_cus[dev] : 0;
+    return n > 0 ? n : 256;
+}
 
 const uint16_t* activation_tables() {
     int dev = 0;

@@ -1,16 +1,29 @@
-// int8 x int8 -> int32 GEMM on CDNA4 MFMA (v_mfma_i32_32x32x32_i8), with the
-// accumulator consumed in-register by an epilogue: int32 store, or the
+// int8 x int8 -> int32 GEMM on CDNA4 MFMA (v_mfma_i32_16x16x64_i8), with the
+// accumulator consumed in registers by a fused epilogue: int32 store, or the
 // ConvRot dequant  bf16(float(acc) * (ws[n] * xs[m]) + bias[n])
-// (src/xpuint8.cpp:692-710) fused into the store.
+// (src/xpuint8.cpp:692-710) applied on the way out.
 //
-// C[m, n] = sum_k A[m, k] * B[n, k]   (A int8 [M, K], B int8 [N, K], both
-// K-contiguous: the "NT" form of torch._int_mm(a, b.t()) that the reference's
-// linear calls, python/xpu_kernels/int8/ops.py:634).
+//   C[m, n] = sum_k X[m, k] * W[n, k]      X int8 [M, K], W int8 [N, K]
 //
-// Block tile BM x BN, K step BK, 256 threads = 4 waves in a 2 x 2 grid; a wave
-// owns a (BM/2) x (BN/2) tile of 32 x 32 MFMA blocks.  A and B tiles are staged
-// through LDS (row pitch BK+16 bytes, conflict-free 16-byte reads), double
-// buffered with register prefetch of the next K step.
+// the "NT" product torch._int_mm(x, w.t()) of the reference's linear
+// (python/xpu_kernels/int8/ops.py:634).
+//
+// Layout.  Each MFMA computes a 16 x 16 block D = W_blk * X_blk^T with the
+// weight rows as the MFMA "A" operand, so lane l ends up holding
+// D[n0 + 4*(l/16) + i][m0 + l%16], i = 0..3: four consecutive output columns
+// of one row -- one 8-byte bf16 store (or one 16-byte int32 store) per block.
+// The operand layout is lane l -> row l%16, bytes [16*(l/16), +16) of the
+// 64-byte K step, for both operands; any K permutation shared by the two
+// operands gives the same integer dot products.
+//
+// Tiling.  A block of WGM x WGN waves owns a BM x BN output tile; a wave owns
+// (BM/WGM) x (BN/WGN), TM x TN MFMA blocks.  The X and W K-slices (BK = 64
+// bytes per row) stream into a ring of STAGES LDS buffers with direct
+// global->LDS loads (global_load_lds_dwordx4, no VGPR staging), issued
+// STAGES-1 steps ahead of the MFMAs; each step waits only for its own loads
+// (an explicit vmcnt) and one s_barrier.  Tiles are ordered so that each of
+// the 8 XCDs (blockIdx % 8) works on a compact rectangle of the output,
+// keeping its X rows and W rows in its own L2.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -18,135 +31,398 @@ namespace xpuint8 {
 namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
-typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v2f __attribute__((ext_vector_type(2)));
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
 
+// s_waitcnt immediate that waits for vmcnt <= n only (gfx9 encoding: vmcnt in
+// bits 3:0 and 15:14; expcnt 6:4 and lgkmcnt 11:8 left at their maxima).
+__host__ __device__ constexpr int vmcnt_imm(int n) {
+    return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8);
+}
+
+// Two fp32 -> packed bf16 (round to nearest even; v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v2f{lo, hi}, v2bf));
+}
+
+// ----------------------------------------------------------------- epilogues
+// Called once per 16x16 block with the lane's four values: row m, columns
+// n..n+3 (n % 4 == 0, the whole block lies inside [0, N)).
 struct EpiI32 {
+    static constexpr bool kStaged = false;
     int32_t* c;
     int64_t ldc;
-    __device__ __forceinline__ void operator()(int i, int j, int v) const { c[int64_t(i) * ldc + j] = v; }
+    __device__ __forceinline__ void operator()(int m, int n, const v4i& v) const {
+        *reinterpret_cast<v4i*>(c + int64_t(m) * ldc + n) = v;
+    }
 };
 
-// The dequant epilogue; ws == nullptr means a unit column scale (1.0f * xs is xs).
+// bf16(float(acc) * (ws[n] * xs[m]) + bias[n]); ws == nullptr is a unit column
+// scale (1.0f * xs[m] == xs[m]), bias may be null.
 struct EpiDequant {
+    static constexpr bool kStaged = true;
     uint16_t* out;
     int64_t ldo;
     const float* xs;
     const float* ws;
     const float* bias;
-    __device__ __forceinline__ void operator()(int i, int j, int v) const {
-        const float w = ws ? ws[j] : 1.0f;
-        float r = float(v) * (w * xs[i]);
-        if (bias) r = r + bias[j];
-        out[int64_t(i) * ldo + j] = uint16_t(f32_to_bf16_bits(r));
+    // per-row and per-column operands, loaded before any conversion so that
+    // their memory latency is paid once per tile
+    struct Col { float4 w, b; };
+    __device__ __forceinline__ float row(int m) const { return xs[m]; }
+    __device__ __forceinline__ Col col(int n) const {
+        Col c;
+        c.w = ws ? *reinterpret_cast<const float4*>(ws + n) : make_float4(1.f, 1.f, 1.f, 1.f);
+        c.b = bias ? *reinterpret_cast<const float4*>(bias + n) : make_float4(0.f, 0.f, 0.f, 0.f);
+        return c;
+    }
+    // the four bf16 results of one row, columns n..n+3, packed
+    __device__ __forceinline__ uint2 convert(const v4i& v, float x, const Col& c) const {
+        float r0 = float(v[0]) * (c.w.x * x), r1 = float(v[1]) * (c.w.y * x);
+        float r2 = float(v[2]) * (c.w.z * x), r3 = float(v[3]) * (c.w.w * x);
+        if (bias) {
+            r0 = r0 + c.b.x; r1 = r1 + c.b.y; r2 = r2 + c.b.z; r3 = r3 + c.b.w;
+        }
+        uint2 o;
+        o.x = cvt_pk_bf16(r0, r1);
+        o.y = cvt_pk_bf16(r2, r3);
+        return o;
+    }
+    // eight finished bf16 values, row m, columns n..n+7
+    __device__ __forceinline__ void store16(int m, int n, const uint4& v) const {
+        *reinterpret_cast<uint4*>(out + int64_t(m) * ldo + n) = v;
+    }
+    __device__ __forceinline__ void operator()(int m, int n, const v4i& v) const {
+        const uint2 o = convert(v, row(m), col(n));
+        *reinterpret_cast<uint2*>(out + int64_t(m) * ldo + n) = o;
     }
 };
 
-template <int BM, int BN, int BK, class Epi>
-__global__ __launch_bounds__(256) void gemm_i8_kernel(const int8_t* __restrict__ A, int64_t lda,
-                                                     const int8_t* __restrict__ B, int64_t ldb,
-                                                     int M, int N, int K, Epi epi) {
-    constexpr int PITCH = BK + 16;
-    constexpr int WTM = BM / 2, WTN = BN / 2;
-    constexpr int TM = WTM / 32, TN = WTN / 32;
-    constexpr int CPR = BK / 16;                 // 16-byte chunks per tile row
-    constexpr int A_CH = BM * CPR / 256, B_CH = BN * CPR / 256;
-    static_assert(A_CH * 256 == BM * CPR && B_CH * 256 == BN * CPR, "tile/thread mismatch");
-    __shared__ __attribute__((aligned(16))) int8_t sA[2][BM * PITCH];
-    __shared__ __attribute__((aligned(16))) int8_t sB[2][BN * PITCH];
+// ----------------------------------------------------------------- kernel
+// 16 zero bytes: the DMA source of operand chunks beyond K (a load cannot be
+// predicated into zeros, so it reads these instead).
+__device__ __attribute__((aligned(16))) int8_t g_zero16[16];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+// LDS layout of one stage: (BM + BN) / 16 blocks of 1 KB, X blocks first.  A
+// block holds 16 rows x 64 bytes; the 16-byte chunk c of row r sits at
+// position c ^ ((r >> 1) & 3), so that the 16 rows read together by one
+// quarter-wave land on distinct banks.  One block is exactly what one
+// global_load_lds_dwordx4 writes (lane l -> bytes [16l, 16l+16)).
+__device__ __forceinline__ int swz(int r, int c) { return c ^ ((r >> 1) & 3); }
 
-    int4 ra[A_CH], rb[B_CH];
-    auto gload = [&](int k0) {
-#pragma unroll
-        for (int i = 0; i < A_CH; ++i) {
-            const int c = tid + i * 256, r = c / CPR, kc = (c % CPR) * 16;
-            const int gm = m0 + r;
-            ra[i] = (gm < M && k0 + kc < K)
-                        ? *reinterpret_cast<const int4*>(A + int64_t(gm) * lda + k0 + kc)
-                        : make_int4(0, 0, 0, 0);
-        }
-#pragma unroll
-        for (int i = 0; i < B_CH; ++i) {
-            const int c = tid + i * 256, r = c / CPR, kc = (c % CPR) * 16;
-            const int gn = n0 + r;
-            rb[i] = (gn < N && k0 + kc < K)
-                        ? *reinterpret_cast<const int4*>(B + int64_t(gn) * ldb + k0 + kc)
-                        : make_int4(0, 0, 0, 0);
-        }
-    };
-    auto sstore = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < A_CH; ++i) {
-            const int c = tid + i * 256, r = c / CPR, kc = (c % CPR) * 16;
-            *reinterpret_cast<int4*>(&sA[buf][r * PITCH + kc]) = ra[i];
-        }
-#pragma unroll
-        for (int i = 0; i < B_CH; ++i) {
-            const int c = tid + i * 256, r = c / CPR, kc = (c % CPR) * 16;
-            *reinterpret_cast<int4*>(&sB[buf][r * PITCH + kc]) = rb[i];
-        }
-    };
-
-    v16i acc[TM][TN];
-#pragma unroll
-    for (int a = 0; a < TM; ++a)
-#pragma unroll
-        for (int b = 0; b < TN; ++b) acc[a][b] = v16i{0};
-
-    const int KT = (K + BK - 1) / BK;
-    gload(0);
-    sstore(0);
-    __syncthreads();
-    for (int kt = 0; kt < KT; ++kt) {
-        const int cur = kt & 1;
-        if (kt + 1 < KT) gload((kt + 1) * BK);
-#pragma unroll
-        for (int kk = 0; kk < BK / 32; ++kk) {
-            v4i af[TM], bf[TN];
-            const int koff = kk * 32 + (lane >> 5) * 16;
-#pragma unroll
-            for (int a = 0; a < TM; ++a)
-                af[a] = *reinterpret_cast<const v4i*>(
-                    &sA[cur][(wm * WTM + a * 32 + (lane & 31)) * PITCH + koff]);
-#pragma unroll
-            for (int b = 0; b < TN; ++b)
-                bf[b] = *reinterpret_cast<const v4i*>(
-                    &sB[cur][(wn * WTN + b * 32 + (lane & 31)) * PITCH + koff]);
-#pragma unroll
-            for (int a = 0; a < TM; ++a)
-#pragma unroll
-                for (int b = 0; b < TN; ++b)
-                    acc[a][b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[a], bf[b], acc[a][b], 0, 0, 0);
-        }
-        if (kt + 1 < KT) sstore(cur ^ 1);
-        __syncthreads();
-    }
-
-    // 32x32 accumulator layout: register r of lane l holds
-    // row 8*(r/4) + 4*(l/32) + r%4, column l%32.
-#pragma unroll
-    for (int a = 0; a < TM; ++a)
-#pragma unroll
-        for (int b = 0; b < TN; ++b)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int i = m0 + wm * WTM + a * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                const int j = n0 + wn * WTN + b * 32 + (lane & 31);
-                if (i < M && j < N) epi(i, j, acc[a][b][r]);
-            }
+// One 16-byte global -> LDS DMA per lane (global_load_lds_dwordx4): lane l's
+// bytes land at ldst + 16*l; ldst must be the same for the whole wave.
+__device__ __forceinline__ void dma16(const int8_t* gsrc, int8_t* ldst) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_global_load_lds(gsrc, (__attribute__((address_space(3))) void*)ldst, 16, 0,
+                                     0);
+#endif
 }
 
-template <class Epi>
-hipError_t launch_gemm(hipStream_t st, const int8_t* A, int64_t lda, const int8_t* B, int64_t ldb,
-                       int M, int N, int K, const Epi& epi) {
-    constexpr int BM = 128, BN = 128, BK = 64;
-    const dim3 grid(unsigned((N + BN - 1) / BN), unsigned((M + BM - 1) / BM));
-    hipLaunchKernelGGL((gemm_i8_kernel<BM, BN, BK, Epi>), grid, dim3(256), 0, st, A, lda, B, ldb,
-                       M, N, K, epi);
+template <int BM, int BN, int WGM, int WGN, int STAGES, class Epi>
+__global__ __launch_bounds__(WGM * WGN * 64) void gemm_i8_kernel(
+    const int8_t* __restrict__ X, int64_t ldx, const int8_t* __restrict__ W, int64_t ldw, int M,
+    int N, int K, int tiles_m, int tiles_n, Epi epi) {
+    constexpr int BK = 64;
+    constexpr int NWAVES = WGM * WGN;
+    constexpr int WM = BM / WGM, WN = BN / WGN;
+    constexpr int TM = WM / 16, TN = WN / 16;
+    static_assert(WM % 16 == 0 && WN % 16 == 0, "wave tile must be whole MFMA blocks");
+    constexpr int XB = BM / 16, WB = BN / 16, NB = XB + WB;      // 1 KB blocks per stage
+    constexpr int PER_WAVE = (NB + NWAVES - 1) / NWAVES;       // DMA instructions per wave
+    constexpr int STAGE_BYTES = NB * 1024;
+    __shared__ __attribute__((aligned(1024))) int8_t smem[STAGES * STAGE_BYTES];
+
+    const int tiles = tiles_m * tiles_n;
+    int t = blockIdx.x;
+    if (tiles % 8 == 0) t = (t % 8) * (tiles / 8) + t / 8;
+    constexpr int GROUP = 8;
+    const int band = t / (GROUP * tiles_n);
+    const int first_m = band * GROUP;
+    const int gm = min(tiles_m - first_m, GROUP);
+    const int in_band = t - band * GROUP * tiles_n;
+    const int tile_m = first_m + in_band % gm;
+    const int tile_n = in_band / gm;
+    const int m0 = tile_m * BM, n0 = tile_n * BN;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave / WGN, wn = wave % WGN;
+
+    // This lane's DMA sources: block j of a stage covers rows 16*(j' ) .. of X
+    // (j < XB) or of W; lane l brings row l/4, chunk swz(l/4, l%4) of it.
+    const int lr = lane >> 2;
+    const int lc = swz(lr, lane & 3) * 16;
+    const int8_t* src[PER_WAVE];
+    int nblk = 0;
+#pragma unroll
+    for (int i = 0; i < PER_WAVE; ++i) {
+        const int j = wave + i * NWAVES;
+        if (j < NB) ++nblk;
+        if (j < XB) {
+            const int r = min(m0 + 16 * j + lr, M - 1);
+            src[i] = X + int64_t(r) * ldx + lc;
+        } else {
+            const int r = min(n0 + 16 * (j - XB) + lr, N - 1);
+            src[i] = W + int64_t(r) * ldw + lc;
+        }
+    }
+    auto issue = [&](int stage_buf, int k0) {
+#pragma unroll
+        for (int i = 0; i < PER_WAVE; ++i) {
+            const int j = wave + i * NWAVES;
+            if (j < NB) {
+                const int8_t* p = (k0 + lc < K) ? src[i] + k0 : g_zero16;
+                dma16(p, smem + stage_buf * STAGE_BYTES + j * 1024);
+            }
+        }
+    };
+
+    v4i acc[TN][TM];
+#pragma unroll
+    for (int a = 0; a < TN; ++a)
+#pragma unroll
+        for (int b = 0; b < TM; ++b) acc[a][b] = v4i{0, 0, 0, 0};
+
+    // operand read offset inside a block: row l%16, chunk l/16
+    const int frag = (lane & 15) * 64 + swz(lane & 15, lane >> 4) * 16;
+    const int KT = (K + BK - 1) / BK;
+#pragma unroll
+    for (int s = 0; s < STAGES - 1; ++s)
+        if (s < KT) issue(s, s * BK);
+
+    for (int kt = 0; kt < KT; ++kt) {
+        // this wave's loads of step kt are done once at most the later
+        // (STAGES - 2) steps' loads are outstanding; then every wave's are
+        const int later = min(KT - 1 - kt, STAGES - 2);
+        if (nblk == PER_WAVE) {
+            if (later >= 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * PER_WAVE));
+            else if (later == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(PER_WAVE));
+            else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        } else {
+            if (later >= 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * (PER_WAVE - 1)));
+            else if (later == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(PER_WAVE - 1));
+            else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        }
+        __builtin_amdgcn_s_barrier();
+        // the buffer refilled now was consumed at step kt-1, before this barrier
+        if (kt + STAGES - 1 < KT) issue((kt + STAGES - 1) % STAGES, (kt + STAGES - 1) * BK);
+        const int8_t* sb = smem + (kt % STAGES) * STAGE_BYTES;
+        v4i wf[TN];
+#pragma unroll
+        for (int a = 0; a < TN; ++a)
+            wf[a] = *reinterpret_cast<const v4i*>(sb + (XB + wn * (WN / 16) + a) * 1024 + frag);
+#pragma unroll
+        for (int b = 0; b < TM; ++b) {
+            const v4i xf = *reinterpret_cast<const v4i*>(sb + (wm * (WM / 16) + b) * 1024 + frag);
+#pragma unroll
+            for (int a = 0; a < TN; ++a)
+                acc[a][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[a], xf, acc[a][b], 0, 0, 0);
+        }
+    }
+
+    // lane l of block (a, b): row m0 + wm*WM + 16b + l%16, columns n .. n+3 with
+    // n = n0 + wn*WN + 16a + 4*(l/16)
+    const int mrow = m0 + wm * WM + (lane & 15);
+    const int ncol = n0 + wn * WN + 4 * (lane >> 4);
+#pragma unroll
+    for (int b = 0; b < TM; ++b) {
+        const int m = mrow + 16 * b;
+        if (m >= M) continue;
+#pragma unroll
+        for (int a = 0; a < TN; ++a) {
+            const int n = ncol + 16 * a;
+            if (n < N) epi(m, n, acc[a][b]);
+        }
+    }
+}
+
+// ------------------------------------------------------------ large tiles
+// A BM x BN tile per block of 4 waves in a WGM x WGN grid, two blocks per CU
+// (so one block's prologue and epilogue overlap the other's main loop); a
+// wave owns (BM/WGM) x (BN/WGN) = TM x TN MFMA blocks.  K runs in 64-byte
+// steps through a ring of STAGES LDS stages filled by direct global->LDS
+// loads issued STAGES-1 steps ahead; the stage is padded to a multiple of
+// 4 KB so every wave issues the same number of loads.  A step reads the
+// wave's TM + TN fragments right after its barrier and runs TM * TN MFMAs on
+// them; the other block's waves keep the matrix core busy meanwhile.
+template <int BM, int BN, int WGM, int WGN, int STAGES, bool KTAIL, class Epi>
+__global__ __launch_bounds__(256, 2) void gemm_i8_big_kernel(
+    const int8_t* __restrict__ X, int64_t ldx, const int8_t* __restrict__ W, int64_t ldw, int M,
+    int N, int K, int tiles_m, int tiles_n, Epi epi) {
+    static_assert(WGM * WGN == 4, "four waves");
+    constexpr int BK = 64;
+    constexpr int WM = BM / WGM, WN = BN / WGN, TM = WM / 16, TN = WN / 16;
+    constexpr int XB = BM / 16, WB = BN / 16;
+    constexpr int PER_WAVE = (XB + WB + 3) / 4;                 // DMA per wave per step
+    constexpr int STAGE_BYTES = 4 * PER_WAVE * 1024;
+    constexpr int RING = STAGES * STAGE_BYTES;
+    constexpr int STG_ROWS = 32;                                // epilogue rows per pass
+    static_assert(!Epi::kStaged || 4 * STG_ROWS * 256 <= RING, "staging fits in the ring");
+    static_assert(TM % 2 == 0, "epilogue passes of 32 rows");
+    __shared__ __attribute__((aligned(1024))) int8_t smem[RING];
+
+    const int tiles = tiles_m * tiles_n;
+    int t = blockIdx.x;
+    if (tiles % 8 == 0) t = (t % 8) * (tiles / 8) + t / 8;
+    constexpr int GROUP = 8;
+    const int band = t / (GROUP * tiles_n);
+    const int first_m = band * GROUP;
+    const int gm = min(tiles_m - first_m, GROUP);
+    const int in_band = t - band * GROUP * tiles_n;
+    const int m0 = (first_m + in_band % gm) * BM, n0 = (in_band / gm) * BN;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave / WGN, wn = wave % WGN;
+
+    // DMA: wave w brings blocks w, w+4, ... of every step; blocks 0..XB-1 are
+    // X rows, XB..XB+WB-1 W rows, the rest padding (a repeat of the last W
+    // block into slots nobody reads).  Lane l: row l/4, chunk swz(l/4, l%4).
+    // Sources are 32-bit byte offsets from the X / W bases (the launcher only
+    // picks this kernel when both operands span < 2^31 bytes).
+    const int lr = lane >> 2;
+    const int lc = swz(lr, lane & 3) * 16;
+    int off[PER_WAVE];
+#pragma unroll
+    for (int i = 0; i < PER_WAVE; ++i) {
+        const int j = min(wave + 4 * i, XB + WB - 1);
+        if (j < XB) off[i] = min(m0 + 16 * j + lr, M - 1) * int(ldx) + lc;
+        else off[i] = min(n0 + 16 * (j - XB) + lr, N - 1) * int(ldw) + lc;
+    }
+    auto issue = [&](int buf, int k0) {
+#pragma unroll
+        for (int i = 0; i < PER_WAVE; ++i) {
+            const int8_t* p = (wave + 4 * i < XB ? X : W) + (off[i] + k0);
+            if (KTAIL && k0 + lc >= K) p = g_zero16;
+            dma16(p, smem + buf * STAGE_BYTES + (wave + 4 * i) * 1024);
+        }
+    };
+
+    const int frag = (lane & 15) * 64 + swz(lane & 15, lane >> 4) * 16;
+    const int xoff = (wm * TM) * 1024 + frag;
+    const int woff = (XB + wn * TN) * 1024 + frag;
+
+    v4i acc[TN][TM];
+#pragma unroll
+    for (int a = 0; a < TN; ++a)
+#pragma unroll
+        for (int b = 0; b < TM; ++b) acc[a][b] = v4i{0, 0, 0, 0};
+
+    const int KT = (K + BK - 1) / BK;
+#pragma unroll
+    for (int s = 0; s < STAGES - 1; ++s)
+        if (s < KT) issue(s, s * BK);
+#pragma clang loop unroll(disable)
+    for (int kt = 0; kt < KT; ++kt) {
+        // step kt's loads are done once only the later groups may be pending
+        const int later = min(KT - 1 - kt, STAGES - 2);
+        if (later >= 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * PER_WAVE));
+        else if (later == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(PER_WAVE));
+        else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        __builtin_amdgcn_s_barrier();
+        // the buffer refilled now was read at step kt-1, before this barrier
+        if (kt + STAGES - 1 < KT) issue((kt + STAGES - 1) % STAGES, (kt + STAGES - 1) * BK);
+        const int8_t* sb = smem + (kt % STAGES) * STAGE_BYTES;
+        v4i wf[TN], xf[TM];
+#pragma unroll
+        for (int i = 0; i < TN; ++i) wf[i] = *reinterpret_cast<const v4i*>(sb + woff + i * 1024);
+#pragma unroll
+        for (int i = 0; i < TM; ++i) xf[i] = *reinterpret_cast<const v4i*>(sb + xoff + i * 1024);
+#pragma unroll
+        for (int b = 0; b < TM; ++b)
+#pragma unroll
+            for (int a = 0; a < TN; ++a)
+                acc[a][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[a], xf[b], acc[a][b], 0, 0, 0);
+    }
+
+    if constexpr (Epi::kStaged) {
+        // bf16 results through this wave's part of the (now idle) ring, 32 rows
+        // per pass: 256-byte rows of 16-byte chunks, chunk c of row r at
+        // c ^ (r & 15); each row leaves as contiguous 16-byte stores.
+        constexpr int CH = WN / 8;                                 // live chunks per row
+        static_assert(CH <= 16 && (STG_ROWS * CH) % 64 == 0, "staging shape");
+        float xrow[TM];
+        typename Epi::Col ccol[TN];
+#pragma unroll
+        for (int b = 0; b < TM; ++b)
+            xrow[b] = epi.row(min(m0 + wm * WM + 16 * b + (lane & 15), M - 1));
+#pragma unroll
+        for (int a = 0; a < TN; ++a)
+            ccol[a] = epi.col(min(n0 + wn * WN + 16 * a + 4 * (lane >> 4), N - 4));
+        __builtin_amdgcn_s_barrier();                              // ring no longer read
+        int8_t* stg = smem + wave * (STG_ROWS * 256);
+#pragma unroll
+        for (int pass = 0; pass < TM / 2; ++pass) {
+#pragma unroll
+            for (int bb = 0; bb < 2; ++bb) {
+                const int b = 2 * pass + bb;
+                const int r = 16 * bb + (lane & 15);
+#pragma unroll
+                for (int a = 0; a < TN; ++a) {
+                    const int c = 16 * a + 4 * (lane >> 4);
+                    const uint2 v = epi.convert(acc[a][b], xrow[b], ccol[a]);
+                    *reinterpret_cast<uint2*>(stg + r * 256 + (((c >> 3) ^ (r & 15)) << 4) +
+                                              (c & 7) * 2) = v;
+                }
+            }
+            __builtin_amdgcn_s_waitcnt(0xC07F);                   // lgkmcnt(0)
+#pragma unroll
+            for (int i = 0; i < (STG_ROWS * CH) / 64; ++i) {
+                const int flat = i * 64 + lane;
+                const int r = flat / CH, c = flat % CH;
+                const uint4 v = *reinterpret_cast<const uint4*>(stg + r * 256 + ((c ^ (r & 15)) << 4));
+                const int m = m0 + wm * WM + 32 * pass + r, n = n0 + wn * WN + 8 * c;
+                if (m < M && n < N) epi.store16(m, n, v);
+            }
+            __builtin_amdgcn_s_waitcnt(0xC07F);                   // reads done before reuse
+        }
+    } else {
+        const int mrow = m0 + wm * WM + (lane & 15);
+        const int ncol = n0 + wn * WN + 4 * (lane >> 4);
+#pragma unroll
+        for (int b = 0; b < TM; ++b) {
+            const int m = mrow + 16 * b;
+            if (m >= M) continue;
+#pragma unroll
+            for (int a = 0; a < TN; ++a) {
+                const int n = ncol + 16 * a;
+                if (n < N) epi(m, n, acc[a][b]);
+            }
+        }
+    }
+}
+
+template <int BM, int BN, int WGM, int WGN, int STAGES, class Epi>
+hipError_t launch_cfg(hipStream_t st, const int8_t* X, int64_t ldx, const int8_t* W, int64_t ldw,
+                      int M, int N, int K, const Epi& epi) {
+    const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
+    hipLaunchKernelGGL((gemm_i8_kernel<BM, BN, WGM, WGN, STAGES, Epi>), dim3(unsigned(tm * tn)),
+                       dim3(WGM * WGN * 64), 0, st, X, ldx, W, ldw, M, N, K, tm, tn, epi);
     return hipGetLastError();
+}
+
+// Tile choice: the large tile (256 x 320, 8 waves of 128 x 80) whenever it
+// still gives every CU work; otherwise the small one (128 x 128, 4 waves of
+// 64 x 64).
+template <class Epi>
+hipError_t launch_gemm(hipStream_t st, const int8_t* X, int64_t ldx, const int8_t* W, int64_t ldw,
+                       int M, int N, int K, const Epi& epi) {
+    constexpr int BM = 256, BN = 160, STAGES = 2;
+    const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
+    const bool fits32 = int64_t(M) * ldx < (int64_t(1) << 31) && int64_t(N) * ldw < (int64_t(1) << 31);
+    if (int64_t(tm) * tn >= 192 && fits32) {
+        if (K % 64 == 0)
+            hipLaunchKernelGGL((gemm_i8_big_kernel<BM, BN, 2, 2, STAGES, false, Epi>),
+                               dim3(unsigned(tm * tn)), dim3(256), 0, st, X, ldx, W, ldw, M, N, K,
+                               tm, tn, epi);
+        else
+            hipLaunchKernelGGL((gemm_i8_big_kernel<BM, BN, 2, 2, STAGES, true, Epi>),
+                               dim3(unsigned(tm * tn)), dim3(256), 0, st, X, ldx, W, ldw, M, N, K,
+                               tm, tn, epi);
+        return hipGetLastError();
+    }
+    return launch_cfg<128, 128, 2, 2, 4>(st, X, ldx, W, ldw, M, N, K, epi);
 }
 
 // ------------------------------------------------------- standalone dequant
@@ -176,8 +452,8 @@ __global__ __launch_bounds__(256) void dequant_kernel(const int32_t* __restrict_
                 const float4 b = pb[j];
                 r0 = r0 + b.x; r1 = r1 + b.y; r2 = r2 + b.z; r3 = r3 + b.w;
             }
-            o[2 * j] = pack_bf16x2(r0, r1);
-            o[2 * j + 1] = pack_bf16x2(r2, r3);
+            o[2 * j] = cvt_pk_bf16(r0, r1);
+            o[2 * j + 1] = cvt_pk_bf16(r2, r3);
         }
         uint4* po = reinterpret_cast<uint4*>(out + m * N + c);
         po[0] = make_uint4(o[0], o[1], o[2], o[3]);

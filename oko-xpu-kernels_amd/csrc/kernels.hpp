@@ -33,6 +33,9 @@ hipError_t dequant_epilogue(hipStream_t st, const int32_t* acc, int64_t acc_ld, 
                             int64_t N);
 hipError_t transpose_i8(hipStream_t st, const int8_t* in, int8_t* out, int64_t R, int64_t C);
 
+// capi.hip: compute units of the current device (persistent grids)
+int device_cus();
+
 // tables.hip: the host copy of the activation tables (activations.hpp)
 const uint16_t* host_activation_tables();
 

@@ -148,8 +148,13 @@ def test_quantize_row_exact(dev, m, n):
     wq, ws = O.quantize_row(bits(dy))
     assert np.array_equal(npy(s).view(np.uint32), ws.view(np.uint32))
     assert np.array_equal(npy(q), wq), mismatch(npy(q), wq)
+    # torch's chain run *on the GPU* divides by the python scalar 127 through a
+    # reciprocal, so its scale can be one ulp off the CPU chain (the oracle):
+    # agreement there is to within that ulp and one code unit
     qt, st = int8.quantize_row_torch(dy.to(dev))
-    assert torch.equal(q, qt) and torch.equal(s, st)
+    ds = np.abs(npy(s).view(np.int32).astype(np.int64) - npy(st).view(np.int32))
+    assert ds.max() <= 1
+    assert (npy(q).astype(np.int16) - npy(qt)).__abs__().max() <= 1
 
 
 def test_quantize_row_ties(dev):
