@@ -34,6 +34,22 @@ for p in (ROOT, os.path.join(ROOT, "oko-xpu-kernels_amd")):
 
 PEAK_INT8_TOPS = 5000.0          # MI355X dense int8 MFMA, TOP/s
 PEAK_HBM_GBPS = 8000.0           # MI355X HBM3E, GB/s
+CALIB_BYTES = 256 << 20          # size of the --calibrate-copy kernel's input and output
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemm_i8_dequant_c3_traffic.md")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the config-3 GEMM, as measured by the two
+    rocprofv3 counter passes summarised in TRAFFIC_FILE (the line
+    ``traffic_bytes_per_launch: N``); None when that summary is absent."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.strip().startswith("traffic_bytes_per_launch:"):
+                    return int(float(line.split(":", 1)[1]))
+    except OSError:
+        pass
+    return None
 
 
 def log(*a):
@@ -110,6 +126,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--only-main", action="store_true", help="config 3 only (for profiling)")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="first run an elementwise int8 kernel over 256 MiB (reads and writes "
+                         "exactly 256 MiB) so counter runs can scale FETCH_SIZE/WRITE_SIZE")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path "
@@ -123,6 +142,13 @@ def main():
         raise SystemExit(f"libxpuint8 unavailable: {L._ERR}")
     dev = torch.device("cuda", 0)
     K, W = args.steps, args.warmup
+    if args.calibrate_copy:
+        src = torch.ones(CALIB_BYTES, dtype=torch.int8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        del src, dst
 
     # ---------------------------------------------------------- config 3
     M, Kd, N = 4096, 1280, 10240
@@ -214,7 +240,7 @@ def main():
                    "M": M, "K": Kd, "N": N, "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": round(gemm_tops, 2), "peak": PEAK_INT8_TOPS,
                      "unit": "TOP/s", "frac": round(gemm_tops / PEAK_INT8_TOPS, 4),
-                     "traffic": None,
+                     "traffic": measured_traffic(),
                      "kernel": "gemm_i8 with dequant epilogue (2*M*N*K int ops per launch)"},
         "extra": extra,
     }
