@@ -123,11 +123,13 @@ int xpuint8_int8_gemm_nn_stream(const void *stream, const int8_t *a, const int8_
 /* The linear's GEMM with the dequant epilogue fused into its store:
  * out[m,n] = bf16(float(sum_k xq[m,k] w8[n,k]) * (w_scale[n] * x_scale[m]) + bias[n]),
  * bit-identical to xpuint8_int8_gemm_stream followed by
- * xpuint8_dequant_epilogue_stream.  bias may be NULL; N % 16 == 0.
+ * xpuint8_dequant_epilogue_stream.  bias may be NULL; it is fp32[N] when
+ * bias_bf16 == 0 and bf16[N] when bias_bf16 == 1 (widened exactly, as the
+ * reference's bias.float()).  N % 16 == 0.
  * Replaces torch._int_mm + dequant at python/xpu_kernels/int8/ops.py:634-638. */
 int xpuint8_linear_gemm_stream(const void *stream, const int8_t *xq, const float *x_scale,
-                               const int8_t *w8, const float *w_scale, const float *bias,
-                               void *out, int64_t M, int64_t N, int64_t K);
+                               const int8_t *w8, const float *w_scale, const void *bias,
+                               int32_t bias_bf16, void *out, int64_t M, int64_t N, int64_t K);
 
 /* linear_dx_int8's GEMM: dx[m,k] = bf16(float(sum_n q[m,n] w8[n,k]) * a[m]),
  * the NN product with the row-scale epilogue.  `work` holds w8^T (K*N bytes).

@@ -311,16 +311,19 @@ int xpuint8_int8_gemm_nn_stream(const void* stream, const int8_t* a, const int8_
 }
 
 int xpuint8_linear_gemm_stream(const void* stream, const int8_t* xq, const float* x_scale,
-                               const int8_t* w8, const float* w_scale, const float* bias,
-                               void* out, int64_t M, int64_t N, int64_t K) {
+                               const int8_t* w8, const float* w_scale, const void* bias,
+                               int32_t bias_bf16, void* out, int64_t M, int64_t N, int64_t K) {
     XPU_TRY(check_epilogue(M, N));
     XPU_TRY(check_gemm(M, N, K));
     XPU_NONNULL(xq); XPU_NONNULL(x_scale); XPU_NONNULL(w8); XPU_NONNULL(w_scale);
     XPU_NONNULL(out);
     XPU_ALIGNED_OPT(bias);
+    if (bias_bf16 != 0 && bias_bf16 != 1) return fail(2, "bias_bf16 must be 0 or 1");
     XPU_TRY(ensure_device());
-    return launched(gemm_dequant(as_stream(stream), xq, K, w8, K, out, N, x_scale, w_scale, bias,
-                                 int(M), int(N), int(K)),
+    const float* b32 = bias_bf16 ? nullptr : static_cast<const float*>(bias);
+    const uint16_t* b16 = bias_bf16 ? static_cast<const uint16_t*>(bias) : nullptr;
+    return launched(gemm_dequant(as_stream(stream), xq, K, w8, K, out, N, x_scale, w_scale, b32,
+                                 b16, int(M), int(N), int(K)),
                     "linear_gemm");
 }
 
@@ -332,7 +335,7 @@ int xpuint8_dx_gemm_stream(const void* stream, const int8_t* q, const float* a, 
     XPU_TRY(ensure_device());
     hipStream_t st = as_stream(stream);
     XPU_TRY(launched(transpose_i8(st, w8, work, N, K), "dx_gemm (transpose)"));
-    return launched(gemm_dequant(st, q, N, work, N, dx, K, a, nullptr, nullptr, int(M), int(K),
+    return launched(gemm_dequant(st, q, N, work, N, dx, K, a, nullptr, nullptr, nullptr, int(M), int(K),
                                  int(N)),
                     "dx_gemm");
 }

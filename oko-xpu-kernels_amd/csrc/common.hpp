@@ -25,12 +25,13 @@ constexpr int kWave = 64;
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 
-// 16-byte streaming loads (read once: non-temporal hint).
-__device__ __forceinline__ u32x4 load16_nt(const void* p) {
-    return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+// 16-byte loads.  (A non-temporal hint measured slower on MI355X for these
+// read-once streams: 5.5 vs 6.3 TB/s.)
+__device__ __forceinline__ u32x4 load16(const void* p) {
+    return *reinterpret_cast<const u32x4*>(p);
 }
-__device__ __forceinline__ i32x4 load16_nt_i(const void* p) {
-    return __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(p));
+__device__ __forceinline__ i32x4 load16_i(const void* p) {
+    return *reinterpret_cast<const i32x4*>(p);
 }
 
 // ----------------------------------------------------------------- bf16 <-> f32
@@ -52,7 +53,11 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 }
 
 // ------------------------------------------------------------ lane exchange
-// quad_perm DPP: xor 1 = [1,0,3,2] = 0xB1, xor 2 = [2,3,0,1] = 0x4E.
+// DPP controls used here, each a lane xor inside a row of 16 lanes:
+// quad_perm [1,0,3,2] = 0xB1 (xor 1), quad_perm [2,3,0,1] = 0x4E (xor 2),
+// row_half_mirror = 0x141 (lane i <- 7-i in each half row: xor 7),
+// row_mirror = 0x140 (lane i <- 15-i: xor 15).
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppXor7 = 0x141, kDppXor15 = 0x140;
 template <int CTRL>
 __device__ __forceinline__ float dpp(float x) {
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xF, 0xF, true));
@@ -89,24 +94,42 @@ __device__ __forceinline__ void hadamard_inreg(float (&v)[16]) {
     for (int c = 0; c < 4; ++c) h4_chain(v[c], v[c + 4], v[c + 8], v[c + 12]);
 }
 
-// Axes 2 and 3: lane L of a 16-lane group holds register w = L.  The 4-point
-// butterfly over lanes {L, L^m1, L^m2, L^m1^m2} as the reference's bfly_xor
-// (src/xpuint8.cpp:441-448): A = v + v[L^m1]; B = v - v[L^m1];
-// out = A + B[L^m2], bit-identical to bfly4 (src/xpuint8.cpp:279-285).
+// Lane -> register assignment.  The 16 lanes of a group hold its 16
+// registers w = i2 + 4*i3 (register w = group elements [16w, 16w+16)); lane
+// sl holds register lane_w(sl), chosen so that the four lanes differing only
+// in digit i2 are {L, L^1, L^2, L^3} and the four differing only in digit i3
+// are {L, L^7, L^15, L^8}.  Both butterflies then use single-instruction DPP
+// lane xors (1, 2 and 7, 15), which fold into the adds, instead of LDS-pipe
+// swizzles.  sl = i2 ^ 7*(i3&1) ^ 15*(i3>>1), inverted:
+//   i3 = gray(sl >> 2), i2 = (sl & 3) ^ (3 if i3 is 1 or 2).
+__device__ __forceinline__ int lane_w(int sl) {
+    const int hi = sl >> 2;
+    const int i3 = hi ^ (hi >> 1);
+    const int i2 = (sl & 3) ^ ((hi & 1) ? 3 : 0);
+    return i2 + 4 * i3;
+}
+
+// Axes 2 and 3.  The 4-point butterfly over lanes {L, L^m1, L^m2, L^m1^m2}
+// as the reference's bfly_xor (src/xpuint8.cpp:441-448): A = v + v[L^m1];
+// B = v - v[L^m1]; out = A + B[L^m2].  With the lane holding index
+// j = c1 + 2*c2 of the 4-point set (c1, c2 its m1, m2 components) this is
+// bit-identical to bfly4 (src/xpuint8.cpp:279-285) for any masks m1, m2:
+// each output is the same two IEEE additions of the same operands, up to
+// commutation and the exact negation x + (b - a) == x - (a - b).
 __device__ __forceinline__ void hadamard_xlane(float (&v)[16]) {
 #pragma unroll
-    for (int t = 0; t < 16; ++t) {           // axis 2: xor 1, xor 2 (DPP quad_perm)
-        const float p = dpp<0xB1>(v[t]);
+    for (int t = 0; t < 16; ++t) {           // axis 2: lane xor 1, xor 2
+        const float p = dpp<kDppXor1>(v[t]);
         const float A = v[t] + p;
         const float B = v[t] - p;
-        v[t] = A + dpp<0x4E>(B);
+        v[t] = A + dpp<kDppXor2>(B);
     }
 #pragma unroll
-    for (int t = 0; t < 16; ++t) {           // axis 3: xor 4, xor 8 (ds_swizzle)
-        const float p = swz_xor<4>(v[t]);
+    for (int t = 0; t < 16; ++t) {           // axis 3: lane xor 7, xor 15
+        const float p = dpp<kDppXor7>(v[t]);
         const float A = v[t] + p;
         const float B = v[t] - p;
-        v[t] = A + swz_xor<8>(B);
+        v[t] = A + dpp<kDppXor15>(B);
     }
 }
 
@@ -118,12 +141,21 @@ __device__ __forceinline__ void hadamard16_unscaled(float (&v)[16]) {
 
 // --------------------------------------------------------------- reductions
 __device__ __forceinline__ float wave_max(float x) {
-    x = fmaxf(x, dpp<0xB1>(x));
-    x = fmaxf(x, dpp<0x4E>(x));
-    x = fmaxf(x, swz_xor<4>(x));
-    x = fmaxf(x, swz_xor<8>(x));
+    x = fmaxf(x, dpp<kDppXor1>(x));
+    x = fmaxf(x, dpp<kDppXor2>(x));
+    x = fmaxf(x, dpp<kDppXor7>(x));
+    x = fmaxf(x, dpp<kDppXor15>(x));
     x = fmaxf(x, swz_xor<16>(x));
     x = fmaxf(x, __shfl_xor(x, 32));
+    return x;
+}
+
+// Max over the 16 lanes of an aligned segment (lanes 16j..16j+15).
+__device__ __forceinline__ float segment_max(float x) {
+    x = fmaxf(x, dpp<kDppXor1>(x));
+    x = fmaxf(x, dpp<kDppXor2>(x));
+    x = fmaxf(x, dpp<kDppXor7>(x));
+    x = fmaxf(x, dpp<kDppXor15>(x));
     return x;
 }
 

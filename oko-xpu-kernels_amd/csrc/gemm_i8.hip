@@ -65,7 +65,8 @@ struct EpiDequant {
     int64_t ldo;
     const float* xs;
     const float* ws;
-    const float* bias;
+    const float* bias;       // fp32 bias, or
+    const uint16_t* bias16;  // bf16 bias (widened exactly), or neither
     // per-row and per-column operands, loaded before any conversion so that
     // their memory latency is paid once per tile
     struct Col { float4 w, b; };
@@ -73,14 +74,21 @@ struct EpiDequant {
     __device__ __forceinline__ Col col(int n) const {
         Col c;
         c.w = ws ? *reinterpret_cast<const float4*>(ws + n) : make_float4(1.f, 1.f, 1.f, 1.f);
-        c.b = bias ? *reinterpret_cast<const float4*>(bias + n) : make_float4(0.f, 0.f, 0.f, 0.f);
+        if (bias) {
+            c.b = *reinterpret_cast<const float4*>(bias + n);
+        } else if (bias16) {
+            const uint2 u = *reinterpret_cast<const uint2*>(bias16 + n);
+            c.b = make_float4(bf16lo(u.x), bf16hi(u.x), bf16lo(u.y), bf16hi(u.y));
+        } else {
+            c.b = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
         return c;
     }
     // the four bf16 results of one row, columns n..n+3, packed
     __device__ __forceinline__ uint2 convert(const v4i& v, float x, const Col& c) const {
         float r0 = float(v[0]) * (c.w.x * x), r1 = float(v[1]) * (c.w.y * x);
         float r2 = float(v[2]) * (c.w.z * x), r3 = float(v[3]) * (c.w.w * x);
-        if (bias) {
+        if (bias || bias16) {
             r0 = r0 + c.b.x; r1 = r1 + c.b.y; r2 = r2 + c.b.z; r3 = r3 + c.b.w;
         }
         uint2 o;
@@ -444,7 +452,7 @@ __global__ __launch_bounds__(256) void dequant_kernel(const int32_t* __restrict_
         uint32_t o[8];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const i32x4 a = load16_nt_i(pa + 4 * j);
+            const i32x4 a = load16_i(pa + 4 * j);
             const float4 w = pw[j];
             float r0 = float(a.x) * (w.x * x), r1 = float(a.y) * (w.y * x);
             float r2 = float(a.z) * (w.z * x), r3 = float(a.w) * (w.w * x);
@@ -489,9 +497,9 @@ hipError_t gemm_i32(hipStream_t st, const int8_t* A, int64_t lda, const int8_t* 
 
 hipError_t gemm_dequant(hipStream_t st, const int8_t* A, int64_t lda, const int8_t* B, int64_t ldb,
                         void* out, int64_t ldo, const float* xs, const float* ws, const float* bias,
-                        int M, int N, int K) {
+                        const uint16_t* bias16, int M, int N, int K) {
     return launch_gemm(st, A, lda, B, ldb, M, N, K,
-                       EpiDequant{static_cast<uint16_t*>(out), ldo, xs, ws, bias});
+                       EpiDequant{static_cast<uint16_t*>(out), ldo, xs, ws, bias, bias16});
 }
 
 hipError_t dequant_epilogue(hipStream_t st, const int32_t* acc, int64_t acc_ld, void* out,

@@ -27,7 +27,7 @@ hipError_t gemm_i32(hipStream_t st, const int8_t* A, int64_t lda, const int8_t* 
                     int32_t* C, int64_t ldc, int M, int N, int K);
 hipError_t gemm_dequant(hipStream_t st, const int8_t* A, int64_t lda, const int8_t* B, int64_t ldb,
                         void* out, int64_t ldo, const float* xs, const float* ws, const float* bias,
-                        int M, int N, int K);
+                        const uint16_t* bias16, int M, int N, int K);
 hipError_t dequant_epilogue(hipStream_t st, const int32_t* acc, int64_t acc_ld, void* out,
                             const float* xs, const float* ws, const float* bias, int64_t M,
                             int64_t N);

@@ -2,15 +2,14 @@
 // fused dequant+activation), rotate only, the gradient row quantizer, the
 // weight preparation and the weight dequantization.
 //
-// Work decomposition (all kernels): a wave64 owns one row.  A "slot" is 1024
-// consecutive elements of the row: 64 lanes x 16 elements, i.e. four 256-point
-// ConvRot groups with 16 lanes per group, lane L of a group holding elements
-// [16L, 16L+16) -- the register/lane assignment of the reference's sub-group
-// kernel (src/xpuint8.cpp:406-438).  The whole row stays in registers (SLOTS x
-// 16 floats per lane), the row absmax is a wave reduction (no LDS, no
-// barrier), then the row is quantized and stored with one 16-byte store per
-// slot.  Rows longer than kMaxSlots*1024 use the two-pass variant, which
-// re-reads the row (from L2) to quantize it.
+// Lane assignment (all kernels): a 256-point ConvRot group is held by 16
+// lanes, each holding one 16-element register of it (elements [16w, 16w+16)
+// in lane L for w = lane_w(L), a permutation of the reference sub-group
+// kernel's w = L, src/xpuint8.cpp:406-438, that keeps every cross-lane
+// butterfly on DPP).  Row kernels
+// keep the whole row in registers across as many 16-lane segments as it needs
+// (rowquant_seg_kernel); rows too long for that use the two-pass variant, one
+// wave per row, which re-reads the row (from L2) to quantize it.
 #include "common.hpp"
 #include "kernels.hpp"
 #include "activations.hpp"
@@ -21,19 +20,27 @@ namespace {
 constexpr int kRowsPerBlock = 4;     // 4 waves = 4 rows per 256-thread block
 
 // ------------------------------------------------------------------ loaders
-// A loader fills v[16] with the pre-rotation values of elements
-// [col, col+16) of a row, as bf16-valued floats.
+// A loader produces the pre-rotation values of elements [col, col+16) of a
+// row, as bf16-valued floats, in two steps: fetch() issues the memory reads
+// and returns them raw, expand() turns them into floats.  Kernels that
+// pipeline rows call fetch() for the next row before working on the current
+// one, so the reads stay in flight during the arithmetic.
 
 struct LoadBF16 {
     const uint16_t* x;
     int64_t ld;
-    __device__ __forceinline__ void operator()(int64_t row, int col, float (&v)[16]) const {
+    struct Raw { u32x4 a, b; };
+    __device__ __forceinline__ Raw fetch(int64_t row, int col) const {
         const uint16_t* p = x + row * ld + col;
-        const u32x4 a = load16_nt(p);
-        const u32x4 b = load16_nt(p + 8);
-        const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        return Raw{load16(p), load16(p + 8)};
+    }
+    __device__ __forceinline__ void expand(const Raw& r, float (&v)[16]) const {
+        const uint32_t w[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
 #pragma unroll
         for (int j = 0; j < 8; ++j) { v[2 * j] = bf16lo(w[j]); v[2 * j + 1] = bf16hi(w[j]); }
+    }
+    __device__ __forceinline__ void operator()(int64_t row, int col, float (&v)[16]) const {
+        expand(fetch(row, col), v);
     }
 };
 
@@ -45,18 +52,28 @@ struct LoadAct {
     int64_t ld;
     int64_t half;
     const uint16_t* tab;   // activation tables (activations.hpp)
-    __device__ __forceinline__ void operator()(int64_t row, int col, float (&v)[16]) const {
+    struct Raw { LoadBF16::Raw a, b; };
+    __device__ __forceinline__ Raw fetch(int64_t row, int col) const {
+        Raw r;
+        r.a = LoadBF16{x, ld}.fetch(row, col);
+        if constexpr (act_paired(ACT)) r.b = LoadBF16{x + half, ld}.fetch(row, col);
+        return r;
+    }
+    __device__ __forceinline__ void expand(const Raw& r, float (&v)[16]) const {
         float a[16];
-        LoadBF16{x, ld}(row, col, a);
+        LoadBF16{x, ld}.expand(r.a, a);
         if constexpr (act_paired(ACT)) {
             float b[16];
-            LoadBF16{x + half, ld}(row, col, b);
+            LoadBF16{x, ld}.expand(r.b, b);
 #pragma unroll
             for (int t = 0; t < 16; ++t) v[t] = activate<ACT>(tab, a[t], b[t]);
         } else {
 #pragma unroll
             for (int t = 0; t < 16; ++t) v[t] = activate<ACT>(tab, a[t], 0.f);
         }
+    }
+    __device__ __forceinline__ void operator()(int64_t row, int col, float (&v)[16]) const {
+        expand(fetch(row, col), v);
     }
 };
 
@@ -75,7 +92,7 @@ struct LoadDequantAct {
         const float4* q = reinterpret_cast<const float4*>(ws + c0);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const i32x4 a = load16_nt_i(p + 4 * j);
+            const i32x4 a = load16_i(p + 4 * j);
             const float4 w = q[j];
             o[4 * j + 0] = bf16_round(float(a.x) * (w.x * xsr));
             o[4 * j + 1] = bf16_round(float(a.y) * (w.y * xsr));
@@ -97,6 +114,17 @@ struct LoadDequantAct {
             for (int t = 0; t < 16; ++t) v[t] = activate<ACT>(tab, h[t], 0.f);
         }
     }
+    // (not pipelined: the raw form would be 32 registers of accumulators)
+    struct Raw { float v[16]; };
+    __device__ __forceinline__ Raw fetch(int64_t row, int col) const {
+        Raw r;
+        (*this)(row, col, r.v);
+        return r;
+    }
+    __device__ __forceinline__ void expand(const Raw& r, float (&v)[16]) const {
+#pragma unroll
+        for (int t = 0; t < 16; ++t) v[t] = r.v[t];
+    }
 };
 
 // bf16(bf16(dy) * bf16(ws[n])): the column-scaled gradient of linear_dx_int8
@@ -106,19 +134,32 @@ struct LoadColScaled {
     const uint16_t* x;
     int64_t ld;
     const float* colscale;   // may be null: plain bf16 rows
-    __device__ __forceinline__ void operator()(int64_t row, int col, float (&v)[16]) const {
-        LoadBF16{x, ld}(row, col, v);
+    struct Raw { LoadBF16::Raw x; float4 c[4]; };
+    __device__ __forceinline__ Raw fetch(int64_t row, int col) const {
+        Raw r;
+        r.x = LoadBF16{x, ld}.fetch(row, col);
         if (colscale) {
             const float4* q = reinterpret_cast<const float4*>(colscale + col);
 #pragma unroll
+            for (int j = 0; j < 4; ++j) r.c[j] = q[j];
+        }
+        return r;
+    }
+    __device__ __forceinline__ void expand(const Raw& r, float (&v)[16]) const {
+        LoadBF16{x, ld}.expand(r.x, v);
+        if (colscale) {
+#pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const float4 w = q[j];
+                const float4 w = r.c[j];
                 v[4 * j + 0] = bf16_round(v[4 * j + 0] * bf16_round(w.x));
                 v[4 * j + 1] = bf16_round(v[4 * j + 1] * bf16_round(w.y));
                 v[4 * j + 2] = bf16_round(v[4 * j + 2] * bf16_round(w.z));
                 v[4 * j + 3] = bf16_round(v[4 * j + 3] * bf16_round(w.w));
             }
         }
+    }
+    __device__ __forceinline__ void operator()(int64_t row, int col, float (&v)[16]) const {
+        expand(fetch(row, col), v);
     }
 };
 
@@ -127,15 +168,20 @@ struct LoadDequantWeight {
     const int8_t* w8;
     int64_t ld;
     const float* scale;
-    __device__ __forceinline__ void operator()(int64_t row, int col, float (&v)[16]) const {
-        const int4 a = *reinterpret_cast<const int4*>(w8 + row * ld + col);
-        const float s = scale[row];
-        const uint32_t w[4] = {uint32_t(a.x), uint32_t(a.y), uint32_t(a.z), uint32_t(a.w)};
+    struct Raw { int4 a; float s; };
+    __device__ __forceinline__ Raw fetch(int64_t row, int col) const {
+        return Raw{*reinterpret_cast<const int4*>(w8 + row * ld + col), scale[row]};
+    }
+    __device__ __forceinline__ void expand(const Raw& r, float (&v)[16]) const {
+        const uint32_t w[4] = {uint32_t(r.a.x), uint32_t(r.a.y), uint32_t(r.a.z), uint32_t(r.a.w)};
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
             const int8_t b = int8_t((w[j >> 2] >> (8 * (j & 3))) & 0xFF);
-            v[j] = bf16_round(float(b) * s);
+            v[j] = bf16_round(float(b) * r.s);
         }
+    }
+    __device__ __forceinline__ void operator()(int64_t row, int col, float (&v)[16]) const {
+        expand(fetch(row, col), v);
     }
 };
 
@@ -183,48 +229,92 @@ __device__ __forceinline__ uint4 quant16(const float (&u)[16], float s, float in
     return r;
 }
 
-template <bool ROT, int MODE>
+// Running max of |u| over 16 raw values (unscaled Hadamard sums when ROT).
 __device__ __forceinline__ float absmax16(const float (&u)[16], float m) {
 #pragma unroll
-    for (int t = 0; t < 16; ++t) {
-        float x = ROT ? u[t] * 0.0625f : u[t];
-        if (MODE == kPrepare) x = bf16_round(x);
-        m = fmaxf(m, fabsf(x));
-    }
+    for (int t = 0; t < 16; ++t) m = fmaxf(m, fabsf(u[t]));
     return m;
 }
 
-// One wave per row, the whole row in registers.
-template <int SLOTS, bool ROT, int MODE, class Loader>
-__global__ __launch_bounds__(256) void rowquant_kernel(Loader load, int8_t* __restrict__ q,
-                                                      float* __restrict__ scale, int64_t M,
-                                                      int K) {
-    const int lane = threadIdx.x & 63;
-    const int64_t row = int64_t(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6);
-    if (row >= M) return;                       // whole wave leaves together
-    float v[SLOTS][16];
+// The row max of the values the quantizer sees, from the max of the raw
+// ones: f(max|u|) == max f(|u|) for the monotone non-decreasing
+// f(u) = u/16 (ROT) and bf16 rounding (kPrepare), so one application suffices.
+template <bool ROT, int MODE>
+__device__ __forceinline__ float finish_max(float raw) {
+    float x = ROT ? raw * 0.0625f : raw;
+    if (MODE == kPrepare) x = bf16_round(x);
+    return x;
+}
+
+// Segmented row kernel.  A segment is 16 lanes holding P (1 or 2) whole
+// 256-groups of one row (lane L of the segment holds register lane_w(L) of
+// each of its groups); a row is S = G/P consecutive segments and a block is
+// R whole rows, so R*S*16 threads (rounded up to whole waves with idle
+// padding segments).  The row is register-resident (16P floats per lane):
+// the group maxima are reduced inside the segment with DPP, combined across
+// the row's segments with one LDS atomic max per segment, and the row is
+// then quantized from registers and stored with one 16-byte store per group.
+//
+// Lanes with no row of their own (padding segments, rows past M) load a valid
+// row anyway (row M-1), so the loads need no branch; they publish nothing and
+// store nothing.  When FULL (K % 256 == 0, every rotating kernel) no column
+// is masked either; otherwise columns past K read as zeros.
+constexpr int kMaxSegments = 64;     // 1024 threads
+
+// s_barrier after this wave's LDS operations have completed, without waiting
+// for its outstanding global loads (which __syncthreads() would).  The
+// "memory" clobber keeps the compiler from moving memory operations across.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+template <int P, bool ROT, int MODE, bool FULL, class Loader>
+__global__ __launch_bounds__(1024) void rowquant_seg_kernel(Loader load, int8_t* __restrict__ q,
+                                                           float* __restrict__ scale, int64_t M,
+                                                           int K, int S, int R, int s_mul) {
+    __shared__ uint32_t row_max[kMaxSegments];
+    const int seg = threadIdx.x >> 4;
+    const int sl = threadIdx.x & 15;
+    const int r = (seg * s_mul) >> 12;           // seg / S (exact for seg, S <= 64)
+    const int sg = seg - r * S;                  // segment within the row
+    const int64_t row = int64_t(blockIdx.x) * R + r;
+    const bool live = r < R && row < M;
+    const int64_t row_ld = row < M ? row : M - 1;
+    int col[P];
+    typename Loader::Raw raw[P];
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        col[p] = (sg * P + p) * kGroup + lane_w(sl) * 16;
+        if constexpr (FULL) {
+            raw[p] = load.fetch(row_ld, col[p]);
+        } else {
+            raw[p] = typename Loader::Raw{};
+            if (col[p] < K) raw[p] = load.fetch(row_ld, col[p]);
+        }
+    }
+    if (threadIdx.x < R) row_max[threadIdx.x] = 0u;
+    lds_barrier();                               // the zeros land before any max
+    float v[P][16];
     float m = 0.f;
 #pragma unroll
-    for (int s = 0; s < SLOTS; ++s) {
-        const int col = s * 1024 + lane * 16;
-        if (col < K) {
-            load(row, col, v[s]);
-        } else {
-#pragma unroll
-            for (int t = 0; t < 16; ++t) v[s][t] = 0.f;
-        }
-        if constexpr (ROT) hadamard16_unscaled(v[s]);   // every lane takes part
-        m = absmax16<ROT, MODE>(v[s], m);
+    for (int p = 0; p < P; ++p) {
+        load.expand(raw[p], v[p]);
+        if constexpr (ROT) hadamard16_unscaled(v[p]);
+        m = absmax16(v[p], m);
     }
-    const float rowmax = wave_max(m);
-    const float sc = row_scale(MODE, rowmax);
+    m = segment_max(m);
+    // m >= 0 (never NaN), so its bit pattern orders like its value
+    if (live && sl == 0) atomicMax(&row_max[r], __float_as_uint(m));
+    lds_barrier();
+    if (!live) return;
+    const float rowmax = __uint_as_float(row_max[r]);
+    const float sc = row_scale(MODE, finish_max<ROT, MODE>(rowmax));
     const float inv = 1.0f / sc;
-    if (lane == 0) scale[row] = sc;
+    if (sg == 0 && sl == 0) scale[row] = sc;
 #pragma unroll
-    for (int s = 0; s < SLOTS; ++s) {
-        const int col = s * 1024 + lane * 16;
-        const uint4 r = quant16<ROT, MODE>(v[s], sc, inv);
-        if (col < K) *reinterpret_cast<uint4*>(q + row * K + col) = r;
+    for (int p = 0; p < P; ++p) {
+        const uint4 w = quant16<ROT, MODE>(v[p], sc, inv);
+        if (FULL || col[p] < K) *reinterpret_cast<uint4*>(q + row * K + col[p]) = w;
     }
 }
 
@@ -241,22 +331,22 @@ __global__ __launch_bounds__(256) void rowquant_2pass_kernel(Loader load, int8_t
     float m = 0.f;
     for (int s = 0; s < slots; ++s) {
         float v[16];
-        const int col = s * 1024 + lane * 16;
+        const int col = s * 1024 + (lane >> 4) * kGroup + lane_w(lane & 15) * 16;
         if (col < K) load(row, col, v);
         else {
 #pragma unroll
             for (int t = 0; t < 16; ++t) v[t] = 0.f;
         }
         if constexpr (ROT) hadamard16_unscaled(v);
-        m = absmax16<ROT, MODE>(v, m);
+        m = absmax16(v, m);
     }
-    const float rowmax = wave_max(m);
+    const float rowmax = finish_max<ROT, MODE>(wave_max(m));
     const float sc = row_scale(MODE, rowmax);
     const float inv = 1.0f / sc;
     if (lane == 0) scale[row] = sc;
     for (int s = 0; s < slots; ++s) {
         float v[16];
-        const int col = s * 1024 + lane * 16;
+        const int col = s * 1024 + (lane >> 4) * kGroup + lane_w(lane & 15) * 16;
         if (col < K) load(row, col, v);
         else {
 #pragma unroll
@@ -268,69 +358,105 @@ __global__ __launch_bounds__(256) void rowquant_2pass_kernel(Loader load, int8_t
     }
 }
 
+// Launch shape of the segmented kernel for a row of G groups: P = 1 (one
+// group per lane; measured fastest on MI355X at K = 5120, ahead of P = 2 and
+// of several rows per block) unless G > kMaxSegments, then P = 2 for even G;
+// S = G/P; then R rows per block with R*S a multiple of 4 (whole waves) near
+// 16 segments (256 threads) or, when that would exceed kMaxSegments, one row
+// padded to whole waves.  nseg is the block's segment count.  Returns false
+// when no P fits (rows longer than 128 groups, or odd and longer than 64).
+inline bool seg_shape(int G, int& P, int& S, int& R, int& nseg) {
+    P = (G > kMaxSegments && G % 2 == 0) ? 2 : 1;
+    S = G / P;
+    if (S > kMaxSegments) return false;
+    int rmin = 4;
+    while (rmin > 1 && (S * (rmin / 2)) % 4 == 0) rmin /= 2;
+    if (rmin * S <= kMaxSegments) {
+        R = rmin;
+        while (R * 2 * S <= 16) R *= 2;
+        nseg = R * S;
+    } else {
+        R = 1;
+        nseg = (S + 3) & ~3;
+    }
+    return true;
+}
+
+template <int P, bool ROT, int MODE, bool FULL, class Loader>
+void launch_seg(hipStream_t st, const Loader& ld, int8_t* q, float* scale, int64_t M, int K,
+                int S, int R, int nseg) {
+    const dim3 grid(unsigned((M + R - 1) / R)), block(unsigned(nseg * 16));
+    const int s_mul = (4096 + S - 1) / S;
+    hipLaunchKernelGGL((rowquant_seg_kernel<P, ROT, MODE, FULL, Loader>), grid, block, 0, st, ld,
+                       q, scale, M, K, S, R, s_mul);
+}
+
 template <bool ROT, int MODE, class Loader>
 hipError_t launch_rowquant(hipStream_t st, const Loader& ld, int8_t* q, float* scale, int64_t M,
                            int K) {
-    const dim3 grid(unsigned((M + kRowsPerBlock - 1) / kRowsPerBlock)), block(256);
-    const int slots = (K + 1023) / 1024;
-    switch (slots) {
-#define XPU_SLOT(n)                                                                     \
-    case n:                                                                             \
-        hipLaunchKernelGGL((rowquant_kernel<n, ROT, MODE, Loader>), grid, block, 0, st, \
-                           ld, q, scale, M, K);                                         \
-        break;
-        XPU_SLOT(1) XPU_SLOT(2) XPU_SLOT(3) XPU_SLOT(4) XPU_SLOT(5) XPU_SLOT(6) XPU_SLOT(7)
-        XPU_SLOT(8)
-#undef XPU_SLOT
-        default:
-            hipLaunchKernelGGL((rowquant_2pass_kernel<ROT, MODE, Loader>), grid, block, 0, st,
-                               ld, q, scale, M, K);
+    const int G = (K + kGroup - 1) / kGroup;
+    int P, S, R, nseg;
+    if (seg_shape(G, P, S, R, nseg)) {
+        if constexpr (ROT) {     // rotating entry points guarantee K % 256 == 0
+            if (P == 2) launch_seg<2, ROT, MODE, true>(st, ld, q, scale, M, K, S, R, nseg);
+            else        launch_seg<1, ROT, MODE, true>(st, ld, q, scale, M, K, S, R, nseg);
+        } else {
+            const bool full = K % kGroup == 0;
+            if (P == 2) {
+                if (full) launch_seg<2, ROT, MODE, true>(st, ld, q, scale, M, K, S, R, nseg);
+                else      launch_seg<2, ROT, MODE, false>(st, ld, q, scale, M, K, S, R, nseg);
+            } else {
+                if (full) launch_seg<1, ROT, MODE, true>(st, ld, q, scale, M, K, S, R, nseg);
+                else      launch_seg<1, ROT, MODE, false>(st, ld, q, scale, M, K, S, R, nseg);
+            }
+        }
+    } else {
+        const dim3 grid(unsigned((M + kRowsPerBlock - 1) / kRowsPerBlock)), block(256);
+        hipLaunchKernelGGL((rowquant_2pass_kernel<ROT, MODE, Loader>), grid, block, 0, st, ld, q,
+                           scale, M, K);
     }
     return hipGetLastError();
 }
 
 // ------------------------------------------------------------ rotate only
-// Every 256-group is independent, so the tensor is a flat list of groups;
-// a wave takes four groups (one slot) at a time.
+// Every 256-group is independent, so the tensor is a flat list of M*K/256
+// groups (K % 256 == 0); a 16-lane segment rotates one group at a time, a
+// block's 16 segments take 16 consecutive groups per grid-stride step.
 template <class Loader>
 __global__ __launch_bounds__(256) void rotate_kernel(Loader load, uint16_t* __restrict__ out,
                                                      int64_t M, int K) {
-    const int lane = threadIdx.x & 63;
-    const int64_t slots_per_row = (K + 1023) / 1024;
-    const int64_t total = M * slots_per_row;
-    const int64_t wave = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
-    const int64_t nwaves = int64_t(gridDim.x) * 4;
-    for (int64_t w = wave; w < total; w += nwaves) {
-        const int64_t row = w / slots_per_row;
-        const int col = int(w - row * slots_per_row) * 1024 + lane * 16;
+    const int sl = threadIdx.x & 15;
+    const int64_t G = K / kGroup;
+    const int64_t total = M * G;
+    for (int64_t g = int64_t(blockIdx.x) * 16 + (threadIdx.x >> 4); g < total;
+         g += int64_t(gridDim.x) * 16) {
+        const int64_t row = g / G;
+        const int col = int(g - row * G) * kGroup + lane_w(sl) * 16;
         float v[16];
-        if (col < K) load(row, col, v);
-        else {
-#pragma unroll
-            for (int t = 0; t < 16; ++t) v[t] = 0.f;
-        }
+        load(row, col, v);
         hadamard16_unscaled(v);
-        if (col < K) {
-            uint4 a, b;
-            a.x = pack_bf16x2(v[0] * 0.0625f, v[1] * 0.0625f);
-            a.y = pack_bf16x2(v[2] * 0.0625f, v[3] * 0.0625f);
-            a.z = pack_bf16x2(v[4] * 0.0625f, v[5] * 0.0625f);
-            a.w = pack_bf16x2(v[6] * 0.0625f, v[7] * 0.0625f);
-            b.x = pack_bf16x2(v[8] * 0.0625f, v[9] * 0.0625f);
-            b.y = pack_bf16x2(v[10] * 0.0625f, v[11] * 0.0625f);
-            b.z = pack_bf16x2(v[12] * 0.0625f, v[13] * 0.0625f);
-            b.w = pack_bf16x2(v[14] * 0.0625f, v[15] * 0.0625f);
-            uint4* p = reinterpret_cast<uint4*>(out + row * K + col);
-            p[0] = a;
-            p[1] = b;
-        }
+        uint4 a, b;
+        a.x = pack_bf16x2(v[0] * 0.0625f, v[1] * 0.0625f);
+        a.y = pack_bf16x2(v[2] * 0.0625f, v[3] * 0.0625f);
+        a.z = pack_bf16x2(v[4] * 0.0625f, v[5] * 0.0625f);
+        a.w = pack_bf16x2(v[6] * 0.0625f, v[7] * 0.0625f);
+        b.x = pack_bf16x2(v[8] * 0.0625f, v[9] * 0.0625f);
+        b.y = pack_bf16x2(v[10] * 0.0625f, v[11] * 0.0625f);
+        b.z = pack_bf16x2(v[12] * 0.0625f, v[13] * 0.0625f);
+        b.w = pack_bf16x2(v[14] * 0.0625f, v[15] * 0.0625f);
+        uint4* p = reinterpret_cast<uint4*>(out + row * K + col);
+        p[0] = a;
+        p[1] = b;
     }
 }
 
+// The loop exit can differ between the segments of a wave on the last step;
+// that is safe because the butterfly only exchanges lanes inside a segment
+// (DPP quad_perm and ds_swizzle xor 4/8), whose 16 lanes always share g.
 template <class Loader>
 hipError_t launch_rotate(hipStream_t st, const Loader& ld, uint16_t* out, int64_t M, int K) {
-    const int64_t waves = M * ((K + 1023) / 1024);
-    int64_t blocks = (waves + 3) / 4;
+    const int64_t groups = M * (K / kGroup);
+    int64_t blocks = (groups + 15) / 16;
     if (blocks > 65536) blocks = 65536;
     hipLaunchKernelGGL((rotate_kernel<Loader>), dim3(unsigned(blocks)), dim3(256), 0, st, ld,
                        out, M, K);

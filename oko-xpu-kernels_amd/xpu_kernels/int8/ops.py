@@ -273,6 +273,20 @@ def expand_scale(scale, n, device=None):
     return _c(s)
 
 
+def _bias_arg(bias, n, device):
+    """(tensor or None, bias_bf16 flag) for the fused GEMM epilogue: a flat
+    contiguous bf16 [n] bias on the device goes in as it is (the kernel widens
+    it exactly, as ``bias.float()`` does), anything else through
+    ``expand_scale`` as fp32."""
+    if bias is None:
+        return None, 0
+    if (isinstance(bias, torch.Tensor) and bias.dtype == torch.bfloat16 and bias.dim() == 1
+            and bias.numel() == n and bias.is_contiguous() and bias.device == device
+            and bias.data_ptr() % 16 == 0):
+        return bias, 1
+    return expand_scale(bias, n, device), 0
+
+
 def _dims(x, w8, act):
     m = 1
     for d in x.shape[:-1]:
@@ -467,10 +481,10 @@ def linear(x, w8, w_scale, bias=None, act: Optional[str] = None, residual=None,
 
     lib = _lib()
     ws = expand_scale(w_scale, n, x.device)
-    b = None if bias is None else expand_scale(bias, n, x.device)
+    b, b16 = _bias_arg(bias, n, x.device)
     out = torch.empty((m, n), device=x.device, dtype=torch.bfloat16)
     rc = lib.xpuint8_linear_gemm_stream(_stream(x.device), _ptr(xq), _ptr(xs), _ptr(w8c),
-                                        _ptr(ws), _opt(b), _ptr(out), m, n, k)
+                                        _ptr(ws), _opt(b), b16, _ptr(out), m, n, k)
     if rc != 0:
         _err(lib, "linear")
     if residual is not None:
@@ -535,10 +549,10 @@ def ffn(x, up_w8, up_scale, down_w8, down_scale, down_bias=None, act="situ"):
     lib = _lib()
     dw8 = _c(down_w8)
     ds = expand_scale(down_scale, k, device)
-    b = None if down_bias is None else expand_scale(down_bias, k, device)
+    b, b16 = _bias_arg(down_bias, k, device)
     out = torch.empty((m, k), device=device, dtype=torch.bfloat16)
     rc = lib.xpuint8_linear_gemm_stream(_stream(device), _ptr(q2), _ptr(xs2), _ptr(dw8),
-                                        _ptr(ds), _opt(b), _ptr(out), m, k, inner)
+                                        _ptr(ds), _opt(b), b16, _ptr(out), m, k, inner)
     if rc != 0:
         _err(lib, "ffn")
     out = out.reshape(*x.shape[:-1], k)

@@ -58,7 +58,8 @@ def test_int8_gemm_full_size_c3(dev):
 
 
 # ------------------------------------------------------- rotate / quantize
-QSHAPES = [(1, 256), (7, 1280), (64, 5120), (33, 8192), (5, 3072), (3, 10240), (2, 16384)]
+QSHAPES = [(1, 256), (7, 1280), (64, 5120), (33, 8192), (5, 3072), (3, 10240), (2, 16384),
+           (5, 4352), (3, 16896), (2, 32768), (2, 33792), (2, 66560), (3, 16640)]
 
 
 @pytest.mark.parametrize("m,k", QSHAPES)
@@ -214,6 +215,9 @@ def test_linear_exact_c1(dev):
     y = int8.linear(x.to(dev), w8, ws, bias.to(dev))
     want = O.linear(bits(x), npy(w8), npy(ws), O.bf16_to_f32(bits(bias)))
     assert np.array_equal(bits(y), want), mismatch(bits(y), want)
+    # a bf16 bias is read by the epilogue directly, an fp32 one as it is: same bits
+    y32 = int8.linear(x.to(dev), w8, ws, bias.float().to(dev))
+    assert np.array_equal(bits(y32), want)
     # the reference oracle (reference/convrot_linear.py) fed the rotated activation
     ref = O.convrot_int8_linear(O.hadamard256(O.bf16_to_f32(bits(x))), npy(w8), npy(ws),
                                 bits(bias))

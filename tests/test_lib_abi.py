@@ -64,7 +64,8 @@ def _rc(lib, fn, *args):
     ("xpuint8_int8_gemm_stream", (Z, P, P, P, 4, 32, 24), 2, "16"),
     ("xpuint8_int8_gemm_stream", (Z, P, P, P, 4, 32, 1 << 20), 4, "131072"),
     ("xpuint8_int8_gemm_nn_stream", (Z, P, P, P, 4, 32, 32, Z), 6, "null"),
-    ("xpuint8_linear_gemm_stream", (Z, P, P, P, P, Z, P, 4, 24, 512), 2, "16"),
+    ("xpuint8_linear_gemm_stream", (Z, P, P, P, P, Z, 0, P, 4, 24, 512), 2, "16"),
+    ("xpuint8_linear_gemm_stream", (Z, P, P, P, P, Z, 2, P, 4, 32, 512), 2, "bias_bf16"),
     ("xpuint8_dx_gemm_stream", (Z, P, P, P, P, 4, 24, 512, P), 2, "16"),
     ("xpuint8_prepare_weight_stream", (Z, P, P, P, 16, 300), 3, "256"),
     ("xpuint8_quantize_row_stream", (Z, P, Z, P, P, 4, 20), 2, "16"),
