@@ -40,4 +40,17 @@ PINNING = {
                     "(mismatches bounded, each <=1 bf16 ulp); float64 closed form",
     "linear": "composition; float64 x@W.T within INT8 error; "
               "reference convrot_linear.py restatement (<=1e-4 code flips)",
+    "dequant_weight": "torch chain (w8.float()*s).bf16 then the pinned rotation; "
+                      "round trip to W within the int8 step",
+    "linear_dx_int8": "torch chain of ops.py:366-377 (bf16 mul, torch._int_mm); "
+                      "float64 dy@W within INT8 error",
+    "linear_dw": "torch float64 matmul",
+    "activate": "torch bf16 eager chains (gelu_tanh, silu*u, situ, h*gelu(g), gelu) "
+                "within 1 bf16 ulp on <0.5% of elements; float64 closed forms "
+                "(test_oracle_activations); tanh_fast vs float64 tanh on all bf16",
+    "quantize_act": "convrot_quantize of the torch chain's activation, bit for bit "
+                    "on rows where the activations agree",
+    "dequant_act / dequant_act_quantize": "torch chain bf16(acc*(ws*xs)) then the "
+                                          "activation; quantize of it on equal rows",
+    "ffn": "float64 down(geglu(up(x)))+b with the unquantized weights",
 }
