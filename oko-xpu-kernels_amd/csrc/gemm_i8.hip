@@ -410,9 +410,11 @@ hipError_t launch_cfg(hipStream_t st, const int8_t* X, int64_t ldx, const int8_t
     return hipGetLastError();
 }
 
-// Tile choice: the large tile (256 x 320, 8 waves of 128 x 80) whenever it
-// still gives every CU work; otherwise the small one (128 x 128, 4 waves of
-// 64 x 64).
+// Tile choice: the large tile (256 x 160, 4 waves of 128 x 80, two blocks per
+// CU, two LDS stages: the fastest of the 256x128/128x256/256x192/128x160
+// shapes and stage counts measured at M=4096, K=1280, N=10240) whenever it
+// gives at least 192 tiles and its 32-bit DMA offsets fit; otherwise the
+// small one (128 x 128, 4 waves of 64 x 64, four stages).
 template <class Epi>
 hipError_t launch_gemm(hipStream_t st, const int8_t* X, int64_t ldx, const int8_t* W, int64_t ldw,
                        int M, int N, int K, const Epi& epi) {
