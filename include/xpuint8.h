@@ -131,6 +131,21 @@ int xpuint8_linear_gemm_stream(const void *stream, const int8_t *xq, const float
                                const int8_t *w8, const float *w_scale, const void *bias,
                                int32_t bias_bf16, void *out, int64_t M, int64_t N, int64_t K);
 
+/* The FFN's up-projection with the dequant and the activation fused into the
+ * GEMM's store:
+ *   d_j[m,n] = bf16(float(sum_k xq[m,k] w8[j*N+n,k]) * (w_scale[j*N+n] * x_scale[m]))
+ *   out[m,n] = act(d_0, d_1)      bf16 [M,N]
+ * for the paired activations 3 (situ: hidden, gate) and 4 (GEGLU: hidden,
+ * gate), whose w8 is [2N, K] = [first half | second half]; for 5 (GELU-erf)
+ * w8 is [N, K] and out = gelu(d_0).  `out` quantized by
+ * xpuint8_convrot_quantize_stream equals xpuint8_dequant_act_quantize_stream
+ * of the int32 accumulator, bit for bit, without the accumulator round trip.
+ * N % 16 == 0, K % 16 == 0.  Replaces torch._int_mm + the load side of
+ * dequant_act_quantize in ffn (python/xpu_kernels/int8/ops.py:714-715). */
+int xpuint8_ffn_up_stream(const void *stream, const int8_t *xq, const float *x_scale,
+                          const int8_t *w8, const float *w_scale, void *out, int64_t M, int64_t N,
+                          int64_t K, int32_t activation);
+
 /* linear_dx_int8's GEMM: dx[m,k] = bf16(float(sum_n q[m,n] w8[n,k]) * a[m]),
  * the NN product with the row-scale epilogue.  `work` holds w8^T (K*N bytes).
  * Replaces torch._int_mm(q, w8) + dequant(acc, a, ones) at

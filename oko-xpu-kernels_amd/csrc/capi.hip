@@ -327,6 +327,22 @@ int xpuint8_linear_gemm_stream(const void* stream, const int8_t* xq, const float
                     "linear_gemm");
 }
 
+int xpuint8_ffn_up_stream(const void* stream, const int8_t* xq, const float* x_scale,
+                          const int8_t* w8, const float* w_scale, void* out, int64_t M, int64_t N,
+                          int64_t K, int32_t activation) {
+    if (activation != 3 && activation != 4 && activation != 5)
+        return fail(6, "ffn_up supports activation 3 (situ), 4 (GEGLU) or 5 (GELU-erf)");
+    const int64_t rows = act_paired(activation) ? 2 * N : N;   // weight rows
+    XPU_TRY(check_epilogue(M, N));
+    XPU_TRY(check_gemm(M, rows, K));
+    XPU_NONNULL(xq); XPU_NONNULL(x_scale); XPU_NONNULL(w8); XPU_NONNULL(w_scale);
+    XPU_NONNULL(out);
+    XPU_TRY(ensure_device());
+    return launched(gemm_act(as_stream(stream), xq, K, w8, K, out, N, x_scale, w_scale, int(M),
+                             int(N), int(K), activation),
+                    "ffn_up");
+}
+
 int xpuint8_dx_gemm_stream(const void* stream, const int8_t* q, const float* a, const int8_t* w8,
                            void* dx, int64_t M, int64_t N, int64_t K, int8_t* work) {
     // q [M,N] @ w8 [N,K] -> dx [M,K]; the contraction runs over N

@@ -24,6 +24,7 @@
 // (an explicit vmcnt) and one s_barrier.  Tiles are ordered so that each of
 // the 8 XCDs (blockIdx % 8) works on a compact rectangle of the output,
 // keeping its X rows and W rows in its own L2.
+#include "activations.hpp"
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -48,8 +49,14 @@ __device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {
 // ----------------------------------------------------------------- epilogues
 // Called once per 16x16 block with the lane's four values: row m, columns
 // n..n+3 (n % 4 == 0, the whole block lies inside [0, N)).
+//
+// kPaired epilogues consume two accumulators per output element: the product
+// with weight row n (first half) and with row half + n (second half), e.g.
+// the FFN's hidden and gate columns; the kernel then interleaves the two
+// halves' weight rows block by block so both land in the same lane.
 struct EpiI32 {
     static constexpr bool kStaged = false;
+    static constexpr bool kPaired = false;
     int32_t* c;
     int64_t ldc;
     __device__ __forceinline__ void operator()(int m, int n, const v4i& v) const {
@@ -61,6 +68,7 @@ struct EpiI32 {
 // scale (1.0f * xs[m] == xs[m]), bias may be null.
 struct EpiDequant {
     static constexpr bool kStaged = true;
+    static constexpr bool kPaired = false;
     uint16_t* out;
     int64_t ldo;
     const float* xs;
@@ -105,6 +113,62 @@ struct EpiDequant {
         *reinterpret_cast<uint2*>(out + int64_t(m) * ldo + n) = o;
     }
 };
+
+// The FFN up-projection's epilogue: dequant, then the activation, written as
+// bf16 (src/xpuint8.cpp:238-261, the load side of the reference's fused
+// dequant+activation+quantize kernel, moved into the GEMM's store):
+//   d = bf16(float(acc) * (ws[n] * xs[m]))   for each half
+//   out[m, n] = act(d_first, d_second)         (activations.hpp)
+// bit-identical to what the fused quantizer forms in registers, so quantizing
+// `out` afterwards gives its exact codes.
+template <int ACT>
+struct EpiAct {
+    static constexpr bool kStaged = true;
+    static constexpr bool kPaired = act_paired(ACT);
+    uint16_t* out;
+    int64_t ldo;
+    const float* xs;
+    const float* ws;          // per weight row: [2 * half] paired, [N] otherwise
+    int half;                 // row offset of the second half (paired)
+    const uint16_t* tab;      // device activation tables
+    struct Col { float4 w; };
+    __device__ __forceinline__ float row(int m) const { return xs[m]; }
+    __device__ __forceinline__ Col col(int n) const {
+        return Col{*reinterpret_cast<const float4*>(ws + n)};
+    }
+    __device__ __forceinline__ static float deq(int a, float w, float x) {
+        return bf16_round(float(a) * (w * x));
+    }
+    __device__ __forceinline__ uint2 convert(const v4i& v, float x, const Col& c) const {
+        const float r0 = activate<ACT>(tab, deq(v[0], c.w.x, x), 0.f);
+        const float r1 = activate<ACT>(tab, deq(v[1], c.w.y, x), 0.f);
+        const float r2 = activate<ACT>(tab, deq(v[2], c.w.z, x), 0.f);
+        const float r3 = activate<ACT>(tab, deq(v[3], c.w.w, x), 0.f);
+        return make_uint2(cvt_pk_bf16(r0, r1), cvt_pk_bf16(r2, r3));
+    }
+    __device__ __forceinline__ uint2 convert2(const v4i& a, const v4i& b, float x, const Col& ca,
+                                              const Col& cb) const {
+        const float r0 = activate<ACT>(tab, deq(a[0], ca.w.x, x), deq(b[0], cb.w.x, x));
+        const float r1 = activate<ACT>(tab, deq(a[1], ca.w.y, x), deq(b[1], cb.w.y, x));
+        const float r2 = activate<ACT>(tab, deq(a[2], ca.w.z, x), deq(b[2], cb.w.z, x));
+        const float r3 = activate<ACT>(tab, deq(a[3], ca.w.w, x), deq(b[3], cb.w.w, x));
+        return make_uint2(cvt_pk_bf16(r0, r1), cvt_pk_bf16(r2, r3));
+    }
+    __device__ __forceinline__ void store16(int m, int n, const uint4& v) const {
+        *reinterpret_cast<uint4*>(out + int64_t(m) * ldo + n) = v;
+    }
+    // unstaged form (small tiles, unpaired activations only)
+    __device__ __forceinline__ void operator()(int m, int n, const v4i& v) const {
+        *reinterpret_cast<uint2*>(out + int64_t(m) * ldo + n) = convert(v, row(m), col(n));
+    }
+};
+
+// Row offset of a paired epilogue's second half (0 for the others).
+template <class Epi>
+__device__ __forceinline__ int pair_offset(const Epi& e) {
+    if constexpr (Epi::kPaired) return e.half;
+    else return 0;
+}
 
 // ----------------------------------------------------------------- kernel
 // 16 zero bytes: the DMA source of operand chunks beyond K (a load cannot be
@@ -254,6 +318,14 @@ __global__ __launch_bounds__(WGM * WGN * 64) void gemm_i8_kernel(
 // 4 KB so every wave issues the same number of loads.  A step reads the
 // wave's TM + TN fragments right after its barrier and runs TM * TN MFMAs on
 // them; the other block's waves keep the matrix core busy meanwhile.
+//
+// N is the number of output columns.  With a kPaired epilogue the tile's BN
+// weight rows are BN/2 output columns' worth of pairs: W block 2p holds rows
+// n0 + 16p .. of the first half, block 2p+1 the same rows of the second half
+// (epi.half rows further), and each wave's TN blocks are whole pairs.
+//
+// DMA sources are a per-tile base pointer (wave-uniform) plus a 32-bit offset
+// inside the tile's rows, so no operand size limit beyond K <= 2^23 / BM.
 template <int BM, int BN, int WGM, int WGN, int STAGES, bool KTAIL, class Epi>
 __global__ __launch_bounds__(256, 2) void gemm_i8_big_kernel(
     const int8_t* __restrict__ X, int64_t ldx, const int8_t* __restrict__ W, int64_t ldw, int M,
@@ -268,6 +340,10 @@ __global__ __launch_bounds__(256, 2) void gemm_i8_big_kernel(
     constexpr int STG_ROWS = 32;                                // epilogue rows per pass
     static_assert(!Epi::kStaged || 4 * STG_ROWS * 256 <= RING, "staging fits in the ring");
     static_assert(TM % 2 == 0, "epilogue passes of 32 rows");
+    constexpr bool PAIRED = Epi::kPaired;
+    static_assert(!PAIRED || (Epi::kStaged && TN % 2 == 0), "pairs are whole per wave");
+    constexpr int OUT_TN = PAIRED ? TN / 2 : TN;                // output blocks per wave
+    constexpr int WN_OUT = 16 * OUT_TN, BN_OUT = WN_OUT * WGN;  // output columns
     __shared__ __attribute__((aligned(1024))) int8_t smem[RING];
 
     const int tiles = tiles_m * tiles_n;
@@ -278,7 +354,7 @@ __global__ __launch_bounds__(256, 2) void gemm_i8_big_kernel(
     const int first_m = band * GROUP;
     const int gm = min(tiles_m - first_m, GROUP);
     const int in_band = t - band * GROUP * tiles_n;
-    const int m0 = (first_m + in_band % gm) * BM, n0 = (in_band / gm) * BN;
+    const int m0 = (first_m + in_band % gm) * BM, n0 = (in_band / gm) * BN_OUT;
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -287,21 +363,33 @@ __global__ __launch_bounds__(256, 2) void gemm_i8_big_kernel(
     // DMA: wave w brings blocks w, w+4, ... of every step; blocks 0..XB-1 are
     // X rows, XB..XB+WB-1 W rows, the rest padding (a repeat of the last W
     // block into slots nobody reads).  Lane l: row l/4, chunk swz(l/4, l%4).
-    // Sources are 32-bit byte offsets from the X / W bases (the launcher only
-    // picks this kernel when both operands span < 2^31 bytes).
+    // Rows past M or N repeat the last row (their results are never stored).
     const int lr = lane >> 2;
     const int lc = swz(lr, lane & 3) * 16;
+    const int8_t* const xbase = X + int64_t(m0) * ldx;
+    const int8_t* const wbase = W + int64_t(n0) * ldw;
+    const int8_t* const gbase = W + (int64_t(pair_offset(epi)) + n0) * ldw;
+    const int8_t* base[PER_WAVE];
     int off[PER_WAVE];
 #pragma unroll
     for (int i = 0; i < PER_WAVE; ++i) {
         const int j = min(wave + 4 * i, XB + WB - 1);
-        if (j < XB) off[i] = min(m0 + 16 * j + lr, M - 1) * int(ldx) + lc;
-        else off[i] = min(n0 + 16 * (j - XB) + lr, N - 1) * int(ldw) + lc;
+        if (j < XB) {
+            base[i] = xbase;
+            off[i] = (min(m0 + 16 * j + lr, M - 1) - m0) * int(ldx) + lc;
+        } else if constexpr (PAIRED) {
+            const int jw = j - XB;
+            base[i] = (jw & 1) ? gbase : wbase;
+            off[i] = (min(n0 + 16 * (jw >> 1) + lr, N - 1) - n0) * int(ldw) + lc;
+        } else {
+            base[i] = wbase;
+            off[i] = (min(n0 + 16 * (j - XB) + lr, N - 1) - n0) * int(ldw) + lc;
+        }
     }
     auto issue = [&](int buf, int k0) {
 #pragma unroll
         for (int i = 0; i < PER_WAVE; ++i) {
-            const int8_t* p = (wave + 4 * i < XB ? X : W) + (off[i] + k0);
+            const int8_t* p = base[i] + (off[i] + k0);
             if (KTAIL && k0 + lc >= K) p = g_zero16;
             dma16(p, smem + buf * STAGE_BYTES + (wave + 4 * i) * 1024);
         }
@@ -348,7 +436,7 @@ __global__ __launch_bounds__(256, 2) void gemm_i8_big_kernel(
         // bf16 results through this wave's part of the (now idle) ring, 32 rows
         // per pass: 256-byte rows of 16-byte chunks, chunk c of row r at
         // c ^ (r & 15); each row leaves as contiguous 16-byte stores.
-        constexpr int CH = WN / 8;                                 // live chunks per row
+        constexpr int CH = WN_OUT / 8;                             // live chunks per row
         static_assert(CH <= 16 && (STG_ROWS * CH) % 64 == 0, "staging shape");
         float xrow[TM];
         typename Epi::Col ccol[TN];
@@ -356,8 +444,13 @@ __global__ __launch_bounds__(256, 2) void gemm_i8_big_kernel(
         for (int b = 0; b < TM; ++b)
             xrow[b] = epi.row(min(m0 + wm * WM + 16 * b + (lane & 15), M - 1));
 #pragma unroll
-        for (int a = 0; a < TN; ++a)
-            ccol[a] = epi.col(min(n0 + wn * WN + 16 * a + 4 * (lane >> 4), N - 4));
+        for (int a = 0; a < TN; ++a) {
+            if constexpr (PAIRED)
+                ccol[a] = epi.col(min(n0 + wn * WN_OUT + 16 * (a >> 1) + 4 * (lane >> 4), N - 4) +
+                                  ((a & 1) ? epi.half : 0));
+            else
+                ccol[a] = epi.col(min(n0 + wn * WN + 16 * a + 4 * (lane >> 4), N - 4));
+        }
         __builtin_amdgcn_s_barrier();                              // ring no longer read
         int8_t* stg = smem + wave * (STG_ROWS * 256);
 #pragma unroll
@@ -367,9 +460,14 @@ __global__ __launch_bounds__(256, 2) void gemm_i8_big_kernel(
                 const int b = 2 * pass + bb;
                 const int r = 16 * bb + (lane & 15);
 #pragma unroll
-                for (int a = 0; a < TN; ++a) {
+                for (int a = 0; a < OUT_TN; ++a) {
                     const int c = 16 * a + 4 * (lane >> 4);
-                    const uint2 v = epi.convert(acc[a][b], xrow[b], ccol[a]);
+                    uint2 v;
+                    if constexpr (PAIRED)
+                        v = epi.convert2(acc[2 * a][b], acc[2 * a + 1][b], xrow[b], ccol[2 * a],
+                                         ccol[2 * a + 1]);
+                    else
+                        v = epi.convert(acc[a][b], xrow[b], ccol[a]);
                     *reinterpret_cast<uint2*>(stg + r * 256 + (((c >> 3) ^ (r & 15)) << 4) +
                                               (c & 7) * 2) = v;
                 }
@@ -380,7 +478,7 @@ __global__ __launch_bounds__(256, 2) void gemm_i8_big_kernel(
                 const int flat = i * 64 + lane;
                 const int r = flat / CH, c = flat % CH;
                 const uint4 v = *reinterpret_cast<const uint4*>(stg + r * 256 + ((c ^ (r & 15)) << 4));
-                const int m = m0 + wm * WM + 32 * pass + r, n = n0 + wn * WN + 8 * c;
+                const int m = m0 + wm * WM + 32 * pass + r, n = n0 + wn * WN_OUT + 8 * c;
                 if (m < M && n < N) epi.store16(m, n, v);
             }
             __builtin_amdgcn_s_waitcnt(0xC07F);                   // reads done before reuse
@@ -413,26 +511,39 @@ hipError_t launch_cfg(hipStream_t st, const int8_t* X, int64_t ldx, const int8_t
 // Tile choice: the large tile (256 x 160, 4 waves of 128 x 80, two blocks per
 // CU, two LDS stages: the fastest of the 256x128/128x256/256x192/128x160
 // shapes and stage counts measured at M=4096, K=1280, N=10240) whenever it
-// gives at least 192 tiles and its 32-bit DMA offsets fit; otherwise the
-// small one (128 x 128, 4 waves of 64 x 64, four stages).
+// gives at least 192 tiles; otherwise the small one (128 x 128, 4 waves of
+// 64 x 64, four stages).  Paired epilogues always take the large tile.
 template <class Epi>
 hipError_t launch_gemm(hipStream_t st, const int8_t* X, int64_t ldx, const int8_t* W, int64_t ldw,
                        int M, int N, int K, const Epi& epi) {
     constexpr int BM = 256, BN = 160, STAGES = 2;
-    const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
-    const bool fits32 = int64_t(M) * ldx < (int64_t(1) << 31) && int64_t(N) * ldw < (int64_t(1) << 31);
-    if (int64_t(tm) * tn >= 192 && fits32) {
+    if constexpr (Epi::kPaired) {
+        // 4 x 1 waves of 64 x 160: each wave holds five (first, second) pairs
+        const int tm = (M + BM - 1) / BM, tn = (N + BN / 2 - 1) / (BN / 2);
         if (K % 64 == 0)
-            hipLaunchKernelGGL((gemm_i8_big_kernel<BM, BN, 2, 2, STAGES, false, Epi>),
+            hipLaunchKernelGGL((gemm_i8_big_kernel<BM, BN, 4, 1, STAGES, false, Epi>),
                                dim3(unsigned(tm * tn)), dim3(256), 0, st, X, ldx, W, ldw, M, N, K,
                                tm, tn, epi);
         else
-            hipLaunchKernelGGL((gemm_i8_big_kernel<BM, BN, 2, 2, STAGES, true, Epi>),
+            hipLaunchKernelGGL((gemm_i8_big_kernel<BM, BN, 4, 1, STAGES, true, Epi>),
                                dim3(unsigned(tm * tn)), dim3(256), 0, st, X, ldx, W, ldw, M, N, K,
                                tm, tn, epi);
         return hipGetLastError();
+    } else {
+        const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
+        if (int64_t(tm) * tn >= 192) {
+            if (K % 64 == 0)
+                hipLaunchKernelGGL((gemm_i8_big_kernel<BM, BN, 2, 2, STAGES, false, Epi>),
+                                   dim3(unsigned(tm * tn)), dim3(256), 0, st, X, ldx, W, ldw, M, N,
+                                   K, tm, tn, epi);
+            else
+                hipLaunchKernelGGL((gemm_i8_big_kernel<BM, BN, 2, 2, STAGES, true, Epi>),
+                                   dim3(unsigned(tm * tn)), dim3(256), 0, st, X, ldx, W, ldw, M, N,
+                                   K, tm, tn, epi);
+            return hipGetLastError();
+        }
+        return launch_cfg<128, 128, 2, 2, 4>(st, X, ldx, W, ldw, M, N, K, epi);
     }
-    return launch_cfg<128, 128, 2, 2, 4>(st, X, ldx, W, ldw, M, N, K, epi);
 }
 
 // ------------------------------------------------------- standalone dequant
@@ -502,6 +613,19 @@ hipError_t gemm_dequant(hipStream_t st, const int8_t* A, int64_t lda, const int8
                         const uint16_t* bias16, int M, int N, int K) {
     return launch_gemm(st, A, lda, B, ldb, M, N, K,
                        EpiDequant{static_cast<uint16_t*>(out), ldo, xs, ws, bias, bias16});
+}
+
+hipError_t gemm_act(hipStream_t st, const int8_t* A, int64_t lda, const int8_t* B, int64_t ldb,
+                    void* out, int64_t ldo, const float* xs, const float* ws, int M, int N, int K,
+                    int act) {
+    uint16_t* o = static_cast<uint16_t*>(out);
+    const uint16_t* tab = activation_tables();
+    switch (act) {
+        case 3: return launch_gemm(st, A, lda, B, ldb, M, N, K, EpiAct<3>{o, ldo, xs, ws, N, tab});
+        case 4: return launch_gemm(st, A, lda, B, ldb, M, N, K, EpiAct<4>{o, ldo, xs, ws, N, tab});
+        case 5: return launch_gemm(st, A, lda, B, ldb, M, N, K, EpiAct<5>{o, ldo, xs, ws, N, tab});
+        default: return hipErrorInvalidValue;
+    }
 }
 
 hipError_t dequant_epilogue(hipStream_t st, const int32_t* acc, int64_t acc_ld, void* out,

@@ -28,6 +28,11 @@ hipError_t gemm_i32(hipStream_t st, const int8_t* A, int64_t lda, const int8_t* 
 hipError_t gemm_dequant(hipStream_t st, const int8_t* A, int64_t lda, const int8_t* B, int64_t ldb,
                         void* out, int64_t ldo, const float* xs, const float* ws, const float* bias,
                         const uint16_t* bias16, int M, int N, int K);
+// out[m, n] = act(bf16(acc(n) * ws[n] * xs[m]), bf16(acc(N + n) * ws[N + n] * xs[m])) for the
+// paired activations 3 (situ) and 4 (GEGLU), whose B has 2N rows; act 5 (GELU) takes N rows
+hipError_t gemm_act(hipStream_t st, const int8_t* A, int64_t lda, const int8_t* B, int64_t ldb,
+                    void* out, int64_t ldo, const float* xs, const float* ws, int M, int N, int K,
+                    int act);
 hipError_t dequant_epilogue(hipStream_t st, const int32_t* acc, int64_t acc_ld, void* out,
                             const float* xs, const float* ws, const float* bias, int64_t M,
                             int64_t N);

@@ -500,7 +500,16 @@ def linear(x, w8, w_scale, bias=None, act: Optional[str] = None, residual=None,
 def ffn(x, up_w8, up_scale, down_w8, down_scale, down_bias=None, act="situ"):
     """``act(up(x)) @ down.T`` (ops.py:649-719).  ``up_w8`` is [2*ffn, K]
     (``[hidden | gate]``) for a paired activation and [ffn, K] for
-    ``gelu_erf``; ``down_w8`` is [K, ffn].  The up projection is unbiased."""
+    ``gelu_erf``; ``down_w8`` is [K, ffn].  The up projection is unbiased.
+
+    Four kernels: rotate+quantize of x; the up-projection GEMM whose epilogue
+    dequantizes each half and applies the activation, writing the bf16
+    activation [M, ffn] (its hidden and gate columns are computed in the same
+    lanes); rotate+quantize of that; the down-projection GEMM with the dequant
+    (+bias) epilogue.  The codes equal the reference's fused
+    dequant+activation+quantize of the int32 accumulator bit for bit (the
+    bf16 activation is exactly the value that kernel forms), without writing
+    the [M, 2*ffn] int32 accumulator."""
     if act not in ACTIVATIONS:
         raise TypeError(f"unknown activation {act!r}; "
                         f"known: {', '.join(sorted(ACTIVATIONS))}")
@@ -543,10 +552,16 @@ def ffn(x, up_w8, up_scale, down_w8, down_scale, down_bias=None, act="situ"):
     if not x2.is_contiguous():
         x2 = x2.contiguous()
 
-    xq, xs = quantize(x2)
-    acc = int_mm(xq, up_w8.contiguous().t())
-    q2, xs2 = dequant_act_quantize(acc, xs, expand_scale(up_scale, n, device), act)
     lib = _lib()
+    xq, xs = quantize(x2)
+    uw8 = _c(up_w8)
+    us = expand_scale(up_scale, n, device)
+    v = torch.empty((m, inner), device=device, dtype=torch.bfloat16)
+    rc = lib.xpuint8_ffn_up_stream(_stream(device), _ptr(xq), _ptr(xs), _ptr(uw8), _ptr(us),
+                                   _ptr(v), m, inner, k, ACTIVATIONS[act])
+    if rc != 0:
+        _err(lib, "ffn (up projection)")
+    q2, xs2 = quantize(v)
     dw8 = _c(down_w8)
     ds = expand_scale(down_scale, k, device)
     b, b16 = _bias_arg(down_bias, k, device)

@@ -15,6 +15,7 @@ import torch
 import oracle as O
 from gpu_util import activation, bits, from_bits, mismatch, npy, weight
 from xpu_kernels import int8
+from xpu_kernels.int8 import _lib as L
 
 pytestmark = pytest.mark.gpu
 
@@ -258,6 +259,52 @@ def test_ffn_geglu_exact(dev):
     db = weight(1, k, seed=7, std=0.01)[0].float()
     y = int8.ffn(x.to(dev), up8, ups, dn8, dns, db.to(dev), act="geglu_erf")
     want = O.ffn(bits(x), npy(up8), npy(ups), npy(dn8), npy(dns), npy(db), act=4)
+    assert np.array_equal(bits(y), want), mismatch(bits(y), want)
+
+
+@pytest.mark.parametrize("act", [3, 4, 5])
+@pytest.mark.parametrize("m,inner,k", [(300, 512, 1280), (64, 1280, 1040), (512, 256, 256)])
+def test_ffn_up_epilogue_exact(dev, act, m, inner, k):
+    """The up-projection GEMM's activation epilogue against the oracle's
+    dequant_act of the int32 product (ragged M, a partial last column tile,
+    K not a multiple of 64)."""
+    rng = np.random.default_rng(act * 100 + m)
+    rows = 2 * inner if act in O.PAIRED else inner
+    xq = rng.integers(-127, 128, (m, k), dtype=np.int8)
+    w8 = rng.integers(-127, 128, (rows, k), dtype=np.int8)
+    xs = rng.uniform(0.01, 0.05, m).astype(np.float32)
+    ws = rng.uniform(1e-5, 1e-4, rows).astype(np.float32)
+    out = torch.empty((m, inner), device=dev, dtype=torch.bfloat16)
+    lib = L._lib()
+    t = [torch.from_numpy(a).to(dev) for a in (xq, xs, w8, ws)]
+    rc = lib.xpuint8_ffn_up_stream(L._stream(dev), L._ptr(t[0]), L._ptr(t[1]), L._ptr(t[2]),
+                                   L._ptr(t[3]), L._ptr(out), m, inner, k, act)
+    assert rc == 0, lib.xpuint8_last_error()
+    want = O.f32_to_bf16(O.dequant_act(O.int_mm(xq, w8), xs, ws, act))
+    assert np.array_equal(bits(out), want), mismatch(bits(out), want)
+
+
+@pytest.mark.parametrize("act", ["situ", "gelu_erf"])
+def test_ffn_other_activations_exact(dev, act):
+    m, k, inner = 272, 1280, 768
+    x = activation(m, k, seed=12)
+    rows = 2 * inner if act == "situ" else inner
+    up8, ups = int8.prepare_weight(weight(rows, k, seed=13).to(dev))
+    dn8, dns = int8.prepare_weight(weight(k, inner, seed=14).to(dev))
+    y = int8.ffn(x.to(dev), up8, ups, dn8, dns, None, act=act)
+    want = O.ffn(bits(x), npy(up8), npy(ups), npy(dn8), npy(dns), None,
+                 act=int8.ACTIVATIONS[act])
+    assert np.array_equal(bits(y), want), mismatch(bits(y), want)
+
+
+def test_ffn_full_size_c4(dev):
+    """Config 4: x [4096,1280] -> GEGLU [4096,5120] -> [4096,1280]."""
+    x = activation(4096, 1280, seed=3)
+    up8, ups = int8.prepare_weight(weight(10240, 1280, seed=4).to(dev))
+    dn8, dns = int8.prepare_weight(weight(1280, 5120, seed=5).to(dev))
+    db = weight(1, 1280, seed=6, std=0.01)[0]
+    y = int8.ffn(x.to(dev), up8, ups, dn8, dns, db.to(dev), act="geglu_erf")
+    want = O.ffn(bits(x), npy(up8), npy(ups), npy(dn8), npy(dns), O.bf16_to_f32(bits(db)), act=4)
     assert np.array_equal(bits(y), want), mismatch(bits(y), want)
 
 

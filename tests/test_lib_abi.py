@@ -66,6 +66,9 @@ def _rc(lib, fn, *args):
     ("xpuint8_int8_gemm_nn_stream", (Z, P, P, P, 4, 32, 32, Z), 6, "null"),
     ("xpuint8_linear_gemm_stream", (Z, P, P, P, P, Z, 0, P, 4, 24, 512), 2, "16"),
     ("xpuint8_linear_gemm_stream", (Z, P, P, P, P, Z, 2, P, 4, 32, 512), 2, "bias_bf16"),
+    ("xpuint8_ffn_up_stream", (Z, P, P, P, P, P, 4, 512, 512, 2), 6, "activation"),
+    ("xpuint8_ffn_up_stream", (Z, P, P, P, P, P, 4, 24, 512, 4), 2, "16"),
+    ("xpuint8_ffn_up_stream", (Z, P, P, Z, P, P, 4, 512, 512, 4), 6, "null"),
     ("xpuint8_dx_gemm_stream", (Z, P, P, P, P, 4, 24, 512, P), 2, "16"),
     ("xpuint8_prepare_weight_stream", (Z, P, P, P, 16, 300), 3, "256"),
     ("xpuint8_quantize_row_stream", (Z, P, Z, P, P, 4, 20), 2, "16"),
