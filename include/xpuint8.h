@@ -169,6 +169,13 @@ int xpuint8_prepare_weight_stream(const void *stream, const void *w, int8_t *q, 
 int xpuint8_quantize_row_stream(const void *stream, const void *x, const float *col_scale,
                                 int8_t *q, float *scale, int64_t M, int64_t N);
 
+/* The weight gradient of a linear: dw[n,k] = sum_m dy[m,n] * x[m,k], dy bf16
+ * [M,N], x bf16 [M,K], dw bf16 [N,K]; fp32 accumulation, one RNE rounding.
+ * N % 16 == 0, K % 16 == 0.  Replaces the torch matmul dy^T @ x of linear_dw
+ * (python/xpu_kernels/int8/ops.py:207-238). */
+int xpuint8_linear_dw_stream(const void *stream, const void *dy, const void *x, void *dw,
+                             int64_t M, int64_t N, int64_t K);
+
 /* Host copy of an activation table (65536 bf16 entries indexed by the bf16
  * bit pattern of the input): 0 gelu_erf, 1 gelu_tanh, 2 silu, 3 situ's
  * tanh(bf16(x/4)), 4 sigmoid, 5 situ's tanh(bf16(x/25)).  No device needed.

@@ -356,6 +356,17 @@ int xpuint8_dx_gemm_stream(const void* stream, const int8_t* q, const float* a, 
                     "dx_gemm");
 }
 
+int xpuint8_linear_dw_stream(const void* stream, const void* dy, const void* x, void* dw,
+                             int64_t M, int64_t N, int64_t K) {
+    if (M <= 0 || N <= 0 || K <= 0) return fail(2, "M, N and K must be positive");
+    if (N % 16 != 0 || K % 16 != 0) return fail(2, "N and K must be multiples of 16");
+    if (M > kMaxDim || N > kMaxDim || K > kMaxDim) return fail(4, "M, N and K must be < 2^31");
+    XPU_NONNULL(dy); XPU_NONNULL(x); XPU_NONNULL(dw);
+    XPU_TRY(ensure_device());
+    return launched(gemm_bf16_tn(as_stream(stream), dy, N, x, K, dw, K, int(M), int(N), int(K)),
+                    "linear_dw");
+}
+
 // ------------------------------------------------------ prepare / row quant
 int xpuint8_prepare_weight_stream(const void* stream, const void* w, int8_t* q, float* scale,
                                   int64_t N, int64_t K) {

@@ -1,0 +1,202 @@
+// The weight gradient of a linear on CDNA4 bf16 MFMA (v_mfma_f32_16x16x32_bf16):
+//
+//   dw[n, k] = sum_m dy[m, n] * x[m, k]      dy bf16 [R, N], x bf16 [R, K]
+//
+// fp32 accumulation, one bf16 rounding (RNE) at the store: the reference's
+// linear_dw, dy^T @ x in bf16 (python/xpu_kernels/int8/ops.py:207-238).
+//
+// Both operands are contracted along their *rows*, while an MFMA operand
+// fragment wants 8 consecutive reduction values per lane.  The tiles therefore
+// go into LDS exactly as they lie in memory (row-major, direct global->LDS
+// loads), and the fragments come out with gfx950's transposing LDS read
+// ds_read_b64_tr_b16.  Within each group of 16 lanes, lane j supplies the
+// address of 4 consecutive bf16 and lane i = 4a + b receives element b of the
+// vectors supplied by lanes a, a+4, a+8, a+12.  So when lane j points at row
+// j/4, columns 4(j%4)..+3 of a 4 x 16 block, lane i receives column i of the
+// 4 rows -- a transposed 4 x 16 read.  Two such reads (rows +0..3 and +4..7)
+// give lane l the 8 reduction values m = 8(l/16)..+7 of operand row l%16,
+// the fragment layout of the 16x16x32 MFMA.
+//
+// D = A * B with A from x (D rows = k) and B from dy (D columns = n), so lane
+// l of a 16x16 block holds D[4(l/16)+i][l%16]: four consecutive k of one dw
+// row, stored as one 8-byte write.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace xpuint8 {
+namespace {
+
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef short v8s __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v2f __attribute__((ext_vector_type(2)));
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+
+// 16 zero bytes: the DMA source for reduction rows past R.
+__device__ __attribute__((aligned(16))) int8_t g_zero_line[16];
+
+constexpr int kStepRows = 32;                // reduction rows per MFMA step
+constexpr int kRegion = kStepRows * 256;     // 32 rows x 128 bf16 columns = 8 KB
+
+// A region row is 256 bytes = 16 chunks of 16 bytes; chunk c of row r sits at
+// position c ^ 2*(r & 3).  A transposing read touches rows 8g + 4h + q
+// (q = 0..3) and two adjacent chunks per row: the four values of r & 3 move
+// the chunk pair to four different 32-byte bank groups, so the 512 bytes of
+// one read spread evenly over the banks.
+__device__ __forceinline__ int tpos(int r, int c) { return c ^ (2 * (r & 3)); }
+
+__device__ __forceinline__ void dma16(const int8_t* gsrc, int8_t* ldst) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_global_load_lds(gsrc, (__attribute__((address_space(3))) void*)ldst, 16, 0,
+                                     0);
+#endif
+}
+
+__device__ __forceinline__ v4s tr_read(const int8_t* p) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)p);
+#else
+    return v4s{};
+#endif
+}
+
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v2f{lo, hi}, v2bf));
+}
+
+// s_waitcnt immediate waiting for vmcnt <= n only.
+__host__ __device__ constexpr int vmcnt_imm(int n) {
+    return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8);
+}
+
+// One 128 (k) x 128 (n) tile per block of 4 waves (2 x 2, 64 x 64 each), two
+// blocks per CU; the reduction runs in steps of 32 rows through a ring of
+// STAGES LDS stages (x region, then dy region), filled STAGES-1 steps ahead.
+template <int STAGES>
+__global__ __launch_bounds__(256, 2) void gemm_bf16_tn_kernel(
+    const uint16_t* __restrict__ X, int64_t ldx, const uint16_t* __restrict__ Y, int64_t ldy,
+    uint16_t* __restrict__ out, int64_t ldo, int R, int K, int N, int tiles_k, int tiles_n) {
+    constexpr int BKD = 128, BND = 128;                 // D rows (k), D columns (n) per tile
+    constexpr int TM = 4, TN = 4;                       // 16x16 blocks per wave
+    constexpr int STAGE = 2 * kRegion;
+    __shared__ __attribute__((aligned(1024))) int8_t smem[STAGES * STAGE];
+
+    const int tiles = tiles_k * tiles_n;
+    int t = blockIdx.x;
+    if (tiles % 8 == 0) t = (t % 8) * (tiles / 8) + t / 8;   // each XCD a contiguous range
+    const int k0 = (t % tiles_k) * BKD, n0 = (t / tiles_k) * BND;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+
+    // DMA: a stage is 16 blocks of 1 KB (4 rows x 256 bytes): blocks 0..7 the
+    // x region, 8..15 the dy region; wave w brings blocks w, w+4, w+8, w+12.
+    // Lane l fills row 4*(b%8) + l/16, position l%16, i.e. source chunk
+    // (l%16) ^ 2*(l/16).  Columns past K / N repeat a valid chunk (their
+    // results are not stored); rows past R read zeros.
+    const int drow = lane >> 4;
+    const int dchunk = (lane & 15) ^ (2 * drow);
+    const int8_t* src[4];
+    int srow[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int b = wave + 4 * i;
+        srow[i] = 4 * (b & 7) + drow;
+        if (i < 2) {
+            const int col = min(k0 + dchunk * 8, K - 8);
+            src[i] = reinterpret_cast<const int8_t*>(X + col);
+        } else {
+            const int col = min(n0 + dchunk * 8, N - 8);
+            src[i] = reinterpret_cast<const int8_t*>(Y + col);
+        }
+    }
+    auto issue = [&](int buf, int step) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = step * kStepRows + srow[i];
+            const int64_t ld = i < 2 ? ldx : ldy;
+            const int8_t* p = row < R ? src[i] + int64_t(row) * ld * 2 : g_zero_line;
+            dma16(p, smem + buf * STAGE + (wave + 4 * i) * 1024);
+        }
+    };
+
+    // transposing-read offsets: lane l (group g, index j) reads row
+    // 8g + 4h + j/4 (h = 0, 1), 8 bytes at column 16*blk + 4*(j%4)
+    const int g = lane >> 4, j = lane & 15;
+    int roff[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) roff[h] = (8 * g + 4 * h + (j >> 2)) * 256 + 8 * (j & 1);
+    const int cpair = (j & 3) >> 1;             // chunk within the block's two
+    const int rq = j >> 2;                      // row & 3 for the swizzle
+    auto frag = [&](const int8_t* region, int blk) {
+        const int pos = ((2 * blk + cpair) ^ (2 * rq)) * 16;
+        const v4s lo = tr_read(region + roff[0] + pos);
+        const v4s hi = tr_read(region + roff[1] + pos);
+        const v8s v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        return __builtin_bit_cast(v8bf, v);
+    };
+
+    v4f acc[TN][TM];
+#pragma unroll
+    for (int a = 0; a < TN; ++a)
+#pragma unroll
+        for (int b = 0; b < TM; ++b) acc[a][b] = v4f{0.f, 0.f, 0.f, 0.f};
+
+    const int RS = (R + kStepRows - 1) / kStepRows;
+#pragma unroll
+    for (int s = 0; s < STAGES - 1; ++s)
+        if (s < RS) issue(s, s);
+#pragma clang loop unroll(disable)
+    for (int st = 0; st < RS; ++st) {
+        const int later = min(RS - 1 - st, STAGES - 2);
+        if (later >= 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(8));
+        else if (later == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(4));
+        else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        __builtin_amdgcn_s_barrier();
+        // the buffer refilled now was read at step st-1, before this barrier
+        if (st + STAGES - 1 < RS) issue((st + STAGES - 1) % STAGES, st + STAGES - 1);
+        const int8_t* sb = smem + (st % STAGES) * STAGE;
+        v8bf af[TM], bf[TN];
+#pragma unroll
+        for (int b = 0; b < TM; ++b) af[b] = frag(sb, wm * TM + b);
+#pragma unroll
+        for (int a = 0; a < TN; ++a) bf[a] = frag(sb + kRegion, wn * TN + a);
+#pragma unroll
+        for (int a = 0; a < TN; ++a)
+#pragma unroll
+            for (int b = 0; b < TM; ++b)
+                acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[b], bf[a], acc[a][b], 0, 0, 0);
+    }
+
+    // lane l of block (a, b): dw row n = n0 + 64 wn + 16a + l%16,
+    // columns k = k0 + 64 wm + 16b + 4(l/16) .. +3
+#pragma unroll
+    for (int a = 0; a < TN; ++a) {
+        const int n = n0 + wn * 64 + 16 * a + (lane & 15);
+        if (n >= N) continue;
+#pragma unroll
+        for (int b = 0; b < TM; ++b) {
+            const int k = k0 + wm * 64 + 16 * b + 4 * (lane >> 4);
+            if (k < K) {
+                const v4f v = acc[a][b];
+                *reinterpret_cast<uint2*>(out + int64_t(n) * ldo + k) =
+                    make_uint2(cvt_pk_bf16(v[0], v[1]), cvt_pk_bf16(v[2], v[3]));
+            }
+        }
+    }
+}
+
+}  // namespace
+
+hipError_t gemm_bf16_tn(hipStream_t st, const void* dy, int64_t ldy, const void* x, int64_t ldx,
+                        void* dw, int64_t ldo, int R, int N, int K) {
+    const int tiles_k = (K + 127) / 128, tiles_n = (N + 127) / 128;
+    hipLaunchKernelGGL((gemm_bf16_tn_kernel<3>), dim3(unsigned(tiles_k * tiles_n)), dim3(256), 0,
+                       st, static_cast<const uint16_t*>(x), ldx, static_cast<const uint16_t*>(dy),
+                       ldy, static_cast<uint16_t*>(dw), ldo, R, K, N, tiles_k, tiles_n);
+    return hipGetLastError();
+}
+
+}  // namespace xpuint8

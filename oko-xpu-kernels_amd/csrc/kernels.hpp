@@ -38,6 +38,10 @@ hipError_t dequant_epilogue(hipStream_t st, const int32_t* acc, int64_t acc_ld, 
                             int64_t N);
 hipError_t transpose_i8(hipStream_t st, const int8_t* in, int8_t* out, int64_t R, int64_t C);
 
+// gemm_bf16.hip: dw[n, k] = sum_m dy[m, n] * x[m, k] (bf16, fp32 accumulate)
+hipError_t gemm_bf16_tn(hipStream_t st, const void* dy, int64_t ldy, const void* x, int64_t ldx,
+                        void* dw, int64_t ldo, int R, int N, int K);
+
 // capi.hip: compute units of the current device (persistent grids)
 int device_cus();
 

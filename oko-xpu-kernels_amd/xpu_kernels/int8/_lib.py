@@ -72,6 +72,7 @@ def _signatures():
         "xpuint8_dx_gemm_stream": ([vp] * 5 + [i64] * 3 + [vp], c_int),
         "xpuint8_prepare_weight_stream": ([vp] * 4 + [i64] * 2, c_int),
         "xpuint8_quantize_row_stream": ([vp] * 5 + [i64] * 2, c_int),
+        "xpuint8_linear_dw_stream": ([vp] * 4 + [i64] * 3, c_int),
         "xpuint8_activation_table": ([i32, vp], c_int),
     }
 

@@ -166,7 +166,23 @@ def linear_dw(dy, x):
         raise ValueError(
             f"dy has {dy.shape[-2]} rows but x has {x.shape[-2]}: the batch "
             f"dims must match for dy^T @ x")
-    return dy.reshape(-1, dy.shape[-1]).transpose(0, 1) @ x.reshape(-1, x.shape[-1])
+    dy2 = dy.reshape(-1, dy.shape[-1])
+    x2 = x.reshape(-1, x.shape[-1])
+    n, k = dy2.shape[1], x2.shape[1]
+    if (dy2.dtype == torch.bfloat16 and x2.dtype == torch.bfloat16 and dy2.is_cuda
+            and x2.device == dy2.device and n % 16 == 0 and k % 16 == 0):
+        # the hand-written bf16 MFMA kernel (fp32 accumulation, like the
+        # matmul it replaces)
+        lib = _lib()
+        dy2, x2 = _c(dy2), _c(x2)
+        dw = torch.empty((n, k), device=dy2.device, dtype=torch.bfloat16)
+        rc = lib.xpuint8_linear_dw_stream(_stream(dy2.device), _ptr(dy2), _ptr(x2), _ptr(dw),
+                                          dy2.shape[0], n, k)
+        if rc != 0:
+            _err(lib, "linear_dw")
+        return dw
+    # other dtypes and shapes: the product the reference computes, in their dtype
+    return dy2.transpose(0, 1) @ x2
 
 
 class _Int8LinearFn(torch.autograd.Function):

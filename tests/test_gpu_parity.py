@@ -308,6 +308,26 @@ def test_ffn_full_size_c4(dev):
     assert np.array_equal(bits(y), want), mismatch(bits(y), want)
 
 
+@pytest.mark.parametrize("m,n,k", [(4096, 5120, 1280), (1000, 272, 208), (1, 16, 16),
+                                   (77, 1280, 4096)])
+def test_linear_dw(dev, m, n, k):
+    """dL/dW = dy^T x through the bf16 MFMA kernel, against float64: each
+    element within one bf16 rounding of the exact value plus the fp32
+    accumulation error (bounded by 2^-14 * sum |dy| |x|)."""
+    g = torch.Generator().manual_seed(m + n + k)
+    dy = (torch.randn(m, n, generator=g) * 1e-3).to(torch.bfloat16)
+    x = torch.randn(m, k, generator=g).to(torch.bfloat16)
+    dw = int8.linear_dw(dy.to(dev), x.to(dev))
+    assert dw.dtype == torch.bfloat16 and tuple(dw.shape) == (n, k)
+    ref = O.linear_dw(bits(dy), bits(x))
+    mag = np.abs(O.bf16_to_f32(bits(dy)).astype(np.float64)).T @ \
+        np.abs(O.bf16_to_f32(bits(x)).astype(np.float64))
+    got = O.bf16_to_f32(bits(dw)).astype(np.float64)
+    err = np.abs(got - ref)
+    assert np.all(err <= 2.0 ** -8 * np.abs(ref) + 2.0 ** -14 * mag), float(
+        np.max(err / (2.0 ** -8 * np.abs(ref) + 2.0 ** -14 * mag)))
+
+
 def test_linear_dx_int8_exact(dev):
     m, n, k = 512, 1280, 1280
     dy = activation(m, n, seed=8, scale=1e-3, n_out=0)

@@ -73,6 +73,8 @@ def _rc(lib, fn, *args):
     ("xpuint8_prepare_weight_stream", (Z, P, P, P, 16, 300), 3, "256"),
     ("xpuint8_quantize_row_stream", (Z, P, Z, P, P, 4, 20), 2, "16"),
     ("xpuint8_activation_table", (7, P), 6, "0..5"),
+    ("xpuint8_linear_dw_stream", (Z, P, P, P, 64, 24, 32), 2, "16"),
+    ("xpuint8_linear_dw_stream", (Z, P, Z, P, 64, 32, 32), 6, "null"),
 ])
 def test_argument_errors_are_reported_without_a_device(lib, fn, args, code, substr):
     rc, msg = _rc(lib, fn, *args)
