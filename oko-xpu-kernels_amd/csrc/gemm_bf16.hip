@@ -39,12 +39,13 @@ __device__ __attribute__((aligned(16))) int8_t g_zero_line[16];
 constexpr int kStepRows = 32;                // reduction rows per MFMA step
 constexpr int kRegion = kStepRows * 256;     // 32 rows x 128 bf16 columns = 8 KB
 
-// A region row is 256 bytes = 16 chunks of 16 bytes; chunk c of row r sits at
-// position c ^ 2*(r & 3).  A transposing read touches rows 8g + 4h + q
-// (q = 0..3) and two adjacent chunks per row: the four values of r & 3 move
-// the chunk pair to four different 32-byte bank groups, so the 512 bytes of
-// one read spread evenly over the banks.
-__device__ __forceinline__ int tpos(int r, int c) { return c ^ (2 * (r & 3)); }
+// A region row is 256 bytes = 16 chunks of 16 bytes, i.e. one pass over the
+// 64 four-byte LDS banks; chunk c of row r sits at position c ^ swz(r).  A
+// transposing read touches 16 rows, 8g + 4h + q (g, q = 0..3), and two
+// adjacent chunks (8 banks) in each: swz takes 8 distinct even values over
+// (q, g & 1), so the rows' chunk pairs cover all 64 banks twice -- the
+// minimum two cycles for the read's 512 bytes.
+__device__ __forceinline__ int swz(int r) { return 2 * ((r & 3) | (((r >> 3) & 1) << 2)); }
 
 __device__ __forceinline__ void dma16(const int8_t* gsrc, int8_t* ldst) {
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -53,12 +54,20 @@ __device__ __forceinline__ void dma16(const int8_t* gsrc, int8_t* ldst) {
 #endif
 }
 
-__device__ __forceinline__ v4s tr_read(const int8_t* p) {
-#if defined(__HIP_DEVICE_COMPILE__)
-    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)p);
-#else
-    return v4s{};
-#endif
+// The transposing read, issued as inline assembly.  Written with the builtin,
+// the compiler must assume the read may see LDS that a pending direct-to-LDS
+// load writes, and waits for *all* outstanding loads before it -- including
+// the stage just issued, which removes the pipelining.  Here the ring's own
+// vmcnt waits (before each barrier) order the loads; the reads' completion is
+// awaited by lds_wait() below before any fragment is used.
+__device__ __forceinline__ uint32_t lds_addr(const int8_t* p) {
+    return static_cast<uint32_t>(
+        reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const int8_t*)p));
+}
+__device__ __forceinline__ v4s tr_read(uint32_t addr) {
+    v4s r;
+    asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r) : "v"(addr));
+    return r;
 }
 
 __device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {
@@ -70,9 +79,9 @@ __host__ __device__ constexpr int vmcnt_imm(int n) {
     return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8);
 }
 
-// One 128 (k) x 128 (n) tile per block of 4 waves (2 x 2, 64 x 64 each), two
-// blocks per CU; the reduction runs in steps of 32 rows through a ring of
-// STAGES LDS stages (x region, then dy region), filled STAGES-1 steps ahead.
+// One 128 (k) x 128 (n) tile per block of 4 waves (2 x 2, 64 x 64 each); the
+// reduction runs in steps of 32 rows through a ring of STAGES LDS stages (x
+// region, then dy region), filled STAGES-1 steps ahead.
 template <int STAGES>
 __global__ __launch_bounds__(256, 2) void gemm_bf16_tn_kernel(
     const uint16_t* __restrict__ X, int64_t ldx, const uint16_t* __restrict__ Y, int64_t ldy,
@@ -93,17 +102,16 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_tn_kernel(
 
     // DMA: a stage is 16 blocks of 1 KB (4 rows x 256 bytes): blocks 0..7 the
     // x region, 8..15 the dy region; wave w brings blocks w, w+4, w+8, w+12.
-    // Lane l fills row 4*(b%8) + l/16, position l%16, i.e. source chunk
-    // (l%16) ^ 2*(l/16).  Columns past K / N repeat a valid chunk (their
-    // results are not stored); rows past R read zeros.
-    const int drow = lane >> 4;
-    const int dchunk = (lane & 15) ^ (2 * drow);
+    // Lane l fills row r = 4*(b%8) + l/16, position l%16, i.e. source chunk
+    // (l%16) ^ swz(r).  Columns past K / N repeat a valid chunk (their results
+    // are not stored); rows past R read zeros.
     const int8_t* src[4];
     int srow[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int b = wave + 4 * i;
-        srow[i] = 4 * (b & 7) + drow;
+        srow[i] = 4 * (b & 7) + (lane >> 4);
+        const int dchunk = (lane & 15) ^ swz(srow[i]);
         if (i < 2) {
             const int col = min(k0 + dchunk * 8, K - 8);
             src[i] = reinterpret_cast<const int8_t*>(X + col);
@@ -125,15 +133,19 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_tn_kernel(
     // transposing-read offsets: lane l (group g, index j) reads row
     // 8g + 4h + j/4 (h = 0, 1), 8 bytes at column 16*blk + 4*(j%4)
     const int g = lane >> 4, j = lane & 15;
-    int roff[2];
+    uint32_t roff[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) roff[h] = (8 * g + 4 * h + (j >> 2)) * 256 + 8 * (j & 1);
     const int cpair = (j & 3) >> 1;             // chunk within the block's two
-    const int rq = j >> 2;                      // row & 3 for the swizzle
-    auto frag = [&](const int8_t* region, int blk) {
-        const int pos = ((2 * blk + cpair) ^ (2 * rq)) * 16;
-        const v4s lo = tr_read(region + roff[0] + pos);
-        const v4s hi = tr_read(region + roff[1] + pos);
+    const int rs = swz(8 * g + (j >> 2));       // swz of the rows read (h does not change it)
+    const uint32_t sbase = lds_addr(smem);
+    // fragment halves: lo = reduction rows +0..3, hi = +4..7 of the lane's 8
+    auto frag_read = [&](uint32_t region, int blk, v4s& lo, v4s& hi) {
+        const uint32_t pos = ((2 * blk + cpair) ^ rs) * 16;
+        lo = tr_read(region + roff[0] + pos);
+        hi = tr_read(region + roff[1] + pos);
+    };
+    auto join = [](const v4s& lo, const v4s& hi) {
         const v8s v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         return __builtin_bit_cast(v8bf, v);
     };
@@ -157,12 +169,24 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_tn_kernel(
         __builtin_amdgcn_s_barrier();
         // the buffer refilled now was read at step st-1, before this barrier
         if (st + STAGES - 1 < RS) issue((st + STAGES - 1) % STAGES, st + STAGES - 1);
-        const int8_t* sb = smem + (st % STAGES) * STAGE;
+        const uint32_t sb = sbase + (st % STAGES) * STAGE;
+        v4s al[TM], ah[TM], bl[TN], bh[TN];
+#pragma unroll
+        for (int b = 0; b < TM; ++b) frag_read(sb, wm * TM + b, al[b], ah[b]);
+#pragma unroll
+        for (int a = 0; a < TN; ++a) frag_read(sb + kRegion, wn * TN + a, bl[a], bh[a]);
+        // every read has landed before any fragment is used (the operands tie
+        // the fragments to this wait, so no use can be scheduled above it)
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(al[0]), "+v"(al[1]), "+v"(al[2]), "+v"(al[3]), "+v"(ah[0]),
+                       "+v"(ah[1]), "+v"(ah[2]), "+v"(ah[3]), "+v"(bl[0]), "+v"(bl[1]),
+                       "+v"(bl[2]), "+v"(bl[3]), "+v"(bh[0]), "+v"(bh[1]), "+v"(bh[2]),
+                       "+v"(bh[3]));
         v8bf af[TM], bf[TN];
 #pragma unroll
-        for (int b = 0; b < TM; ++b) af[b] = frag(sb, wm * TM + b);
+        for (int b = 0; b < TM; ++b) af[b] = join(al[b], ah[b]);
 #pragma unroll
-        for (int a = 0; a < TN; ++a) bf[a] = frag(sb + kRegion, wn * TN + a);
+        for (int a = 0; a < TN; ++a) bf[a] = join(bl[a], bh[a]);
 #pragma unroll
         for (int a = 0; a < TN; ++a)
 #pragma unroll
@@ -193,7 +217,10 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_tn_kernel(
 hipError_t gemm_bf16_tn(hipStream_t st, const void* dy, int64_t ldy, const void* x, int64_t ldx,
                         void* dw, int64_t ldo, int R, int N, int K) {
     const int tiles_k = (K + 127) / 128, tiles_n = (N + 127) / 128;
-    hipLaunchKernelGGL((gemm_bf16_tn_kernel<3>), dim3(unsigned(tiles_k * tiles_n)), dim3(256), 0,
+    // two stages (one in flight): measured fastest at the C5 shape (75 us vs
+    // 83-86 us for three to five), the smaller LDS footprint leaving room for
+    // more resident blocks per CU
+    hipLaunchKernelGGL((gemm_bf16_tn_kernel<2>), dim3(unsigned(tiles_k * tiles_n)), dim3(256), 0,
                        st, static_cast<const uint16_t*>(x), ldx, static_cast<const uint16_t*>(dy),
                        ldy, static_cast<uint16_t*>(dw), ldo, R, K, N, tiles_k, tiles_n);
     return hipGetLastError();
