@@ -327,18 +327,19 @@ __global__ __launch_bounds__(WGM * WGN * 64) void gemm_i8_kernel(
 // DMA sources are a per-tile base pointer (wave-uniform) plus a 32-bit offset
 // inside the tile's rows, so no operand size limit beyond K <= 2^23 / BM.
 template <int BM, int BN, int WGM, int WGN, int STAGES, bool KTAIL, class Epi>
-__global__ __launch_bounds__(256, 2) void gemm_i8_big_kernel(
+__global__ __launch_bounds__(WGM * WGN * 64, 8 / (WGM * WGN)) void gemm_i8_big_kernel(
     const int8_t* __restrict__ X, int64_t ldx, const int8_t* __restrict__ W, int64_t ldw, int M,
     int N, int K, int tiles_m, int tiles_n, Epi epi) {
-    static_assert(WGM * WGN == 4, "four waves");
+    constexpr int NW = WGM * WGN;                               // 4 or 8 waves
+    static_assert(NW == 4 || NW == 8, "four or eight waves");
     constexpr int BK = 64;
     constexpr int WM = BM / WGM, WN = BN / WGN, TM = WM / 16, TN = WN / 16;
     constexpr int XB = BM / 16, WB = BN / 16;
-    constexpr int PER_WAVE = (XB + WB + 3) / 4;                 // DMA per wave per step
-    constexpr int STAGE_BYTES = 4 * PER_WAVE * 1024;
+    constexpr int PER_WAVE = (XB + WB + NW - 1) / NW;           // DMA per wave per step
+    constexpr int STAGE_BYTES = NW * PER_WAVE * 1024;
     constexpr int RING = STAGES * STAGE_BYTES;
     constexpr int STG_ROWS = 32;                                // epilogue rows per pass
-    static_assert(!Epi::kStaged || 4 * STG_ROWS * 256 <= RING, "staging fits in the ring");
+    static_assert(!Epi::kStaged || NW * STG_ROWS * 256 <= RING, "staging fits in the ring");
     static_assert(TM % 2 == 0, "epilogue passes of 32 rows");
     constexpr bool PAIRED = Epi::kPaired;
     static_assert(!PAIRED || (Epi::kStaged && TN % 2 == 0), "pairs are whole per wave");
@@ -360,7 +361,7 @@ __global__ __launch_bounds__(256, 2) void gemm_i8_big_kernel(
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = wave / WGN, wn = wave % WGN;
 
-    // DMA: wave w brings blocks w, w+4, ... of every step; blocks 0..XB-1 are
+    // DMA: wave w brings blocks w, w+NW, ... of every step; blocks 0..XB-1 are
     // X rows, XB..XB+WB-1 W rows, the rest padding (a repeat of the last W
     // block into slots nobody reads).  Lane l: row l/4, chunk swz(l/4, l%4).
     // Rows past M or N repeat the last row (their results are never stored).
@@ -373,7 +374,7 @@ __global__ __launch_bounds__(256, 2) void gemm_i8_big_kernel(
     int off[PER_WAVE];
 #pragma unroll
     for (int i = 0; i < PER_WAVE; ++i) {
-        const int j = min(wave + 4 * i, XB + WB - 1);
+        const int j = min(wave + NW * i, XB + WB - 1);
         if (j < XB) {
             base[i] = xbase;
             off[i] = (min(m0 + 16 * j + lr, M - 1) - m0) * int(ldx) + lc;
@@ -391,7 +392,7 @@ __global__ __launch_bounds__(256, 2) void gemm_i8_big_kernel(
         for (int i = 0; i < PER_WAVE; ++i) {
             const int8_t* p = base[i] + (off[i] + k0);
             if (KTAIL && k0 + lc >= K) p = g_zero16;
-            dma16(p, smem + buf * STAGE_BYTES + (wave + 4 * i) * 1024);
+            dma16(p, smem + buf * STAGE_BYTES + (wave + NW * i) * 1024);
         }
     };
 
@@ -508,11 +509,88 @@ hipError_t launch_cfg(hipStream_t st, const int8_t* X, int64_t ldx, const int8_t
     return hipGetLastError();
 }
 
+// ------------------------------------------------------------ skinny M
+// M <= 64: the product streams the weight once, so it is bound by HBM
+// bandwidth, and tiles of 128+ rows would leave most CUs idle.  A block owns 16
+// weight rows (one MFMA row block) and all MB 16-row blocks of X; its 4 waves
+// take every 4th 64-byte K step and keep their operands in registers, loaded
+// straight from global memory in the MFMA layout (lane l: row l%16, bytes
+// 16*(l/16) of the step) D steps ahead.  The four partial accumulators meet in
+// LDS; the epilogue is the per-block form of the same Epi.
+template <int MB, class Epi>
+__global__ __launch_bounds__(256) void gemm_i8_skinny_kernel(
+    const int8_t* __restrict__ X, int64_t ldx, const int8_t* __restrict__ W, int64_t ldw, int M,
+    int N, int K, Epi epi) {
+    constexpr int D = MB <= 2 ? 8 : 4;                       // steps in flight per wave
+    __shared__ v4i part[4][MB][64];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int n0 = blockIdx.x * 16;
+    const int kb = 16 * (lane >> 4);                         // lane's bytes within a step
+    const int8_t* wrow = W + int64_t(min(n0 + (lane & 15), N - 1)) * ldw + kb;
+    const int8_t* xrow[MB];
+#pragma unroll
+    for (int b = 0; b < MB; ++b) xrow[b] = X + int64_t(min(16 * b + (lane & 15), M - 1)) * ldx + kb;
+    const int S = (K + 63) / 64;                             // K steps; this wave: wave, wave+4, ...
+    v4i wbuf[D], xbuf[D][MB];
+    auto load = [&](int slot, int step) {
+        const int k = step * 64;
+        if (step < S && k + kb < K) {
+            wbuf[slot] = *reinterpret_cast<const v4i*>(wrow + k);
+#pragma unroll
+            for (int b = 0; b < MB; ++b) xbuf[slot][b] = *reinterpret_cast<const v4i*>(xrow[b] + k);
+        } else {
+            wbuf[slot] = v4i{0, 0, 0, 0};
+#pragma unroll
+            for (int b = 0; b < MB; ++b) xbuf[slot][b] = v4i{0, 0, 0, 0};
+        }
+    };
+    v4i acc[MB];
+#pragma unroll
+    for (int b = 0; b < MB; ++b) acc[b] = v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < D; ++j) load(j, wave + 4 * j);
+    for (int s0 = 0; wave + 4 * s0 < S; s0 += D) {
+#pragma unroll
+        for (int j = 0; j < D; ++j) {
+#pragma unroll
+            for (int b = 0; b < MB; ++b)
+                acc[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wbuf[j], xbuf[j][b], acc[b], 0, 0, 0);
+            load(j, wave + 4 * (s0 + j + D));
+        }
+    }
+#pragma unroll
+    for (int b = 0; b < MB; ++b) part[wave][b][lane] = acc[b];
+    __syncthreads();
+    // wave w finishes m-blocks w, w+4, ...: lane l holds rows 4*(l/16)+i of
+    // the weight block (n) for x row l%16 (m)
+    for (int b = wave; b < MB; b += 4) {
+        const v4i v = part[0][b][lane] + part[1][b][lane] + part[2][b][lane] + part[3][b][lane];
+        const int m = 16 * b + (lane & 15);
+        const int n = n0 + 4 * (lane >> 4);
+        if (m < M && n < N) epi(m, n, v);
+    }
+}
+
+template <class Epi>
+hipError_t launch_skinny(hipStream_t st, const int8_t* X, int64_t ldx, const int8_t* W,
+                         int64_t ldw, int M, int N, int K, const Epi& epi) {
+    const dim3 grid(unsigned((N + 15) / 16)), block(256);
+    switch ((M + 15) / 16) {
+        case 1: hipLaunchKernelGGL((gemm_i8_skinny_kernel<1, Epi>), grid, block, 0, st, X, ldx, W, ldw, M, N, K, epi); break;
+        case 2: hipLaunchKernelGGL((gemm_i8_skinny_kernel<2, Epi>), grid, block, 0, st, X, ldx, W, ldw, M, N, K, epi); break;
+        case 3: hipLaunchKernelGGL((gemm_i8_skinny_kernel<3, Epi>), grid, block, 0, st, X, ldx, W, ldw, M, N, K, epi); break;
+        default: hipLaunchKernelGGL((gemm_i8_skinny_kernel<4, Epi>), grid, block, 0, st, X, ldx, W, ldw, M, N, K, epi); break;
+    }
+    return hipGetLastError();
+}
+
 // Tile choice: the large tile (256 x 160, 4 waves of 128 x 80, two blocks per
 // CU, two LDS stages: the fastest of the 256x128/128x256/256x192/128x160
 // shapes and stage counts measured at M=4096, K=1280, N=10240) whenever it
 // gives at least 192 tiles; otherwise the small one (128 x 128, 4 waves of
-// 64 x 64, four stages).  Paired epilogues always take the large tile.
+// 64 x 64, four stages); M <= 64 takes the weight-streaming skinny kernel.
+// Paired epilogues always take the large tile.
 template <class Epi>
 hipError_t launch_gemm(hipStream_t st, const int8_t* X, int64_t ldx, const int8_t* W, int64_t ldw,
                        int M, int N, int K, const Epi& epi) {
@@ -530,6 +608,7 @@ hipError_t launch_gemm(hipStream_t st, const int8_t* X, int64_t ldx, const int8_
                                tm, tn, epi);
         return hipGetLastError();
     } else {
+        if (M <= 64) return launch_skinny(st, X, ldx, W, ldw, M, N, K, epi);
         const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
         if (int64_t(tm) * tn >= 192) {
             if (K % 64 == 0)

@@ -238,7 +238,19 @@ def quantize_row(x, col_scale=None):
     x2, shape = _flat2d(x)
     m, n = x2.shape
     if n % 16:
-        raise TypeError(f"quantize_row needs a multiple of 16 columns, got {n}")
+        # the kernel reads rows in 16-element pieces: widths that are not a
+        # multiple of 16 are zero-padded (zeros change neither a row's max nor
+        # any code) and the padding is dropped afterwards
+        n16 = (n + 15) // 16 * 16
+        xp = torch.zeros((m, n16), device=x.device, dtype=torch.bfloat16)
+        xp[:, :n] = x2
+        csp = None
+        if col_scale is not None:
+            csp = torch.zeros(n16, device=x.device, dtype=torch.float32)
+            csp[:n] = expand_scale(col_scale, n, x.device)
+        q, scale = quantize_row(xp, csp)
+        return (q[:, :n].contiguous().reshape(*shape[:-1], n),
+                scale.reshape(shape[:-1]))
     cs = None if col_scale is None else expand_scale(col_scale, n, x.device)
     q = torch.empty((m, n), device=x.device, dtype=torch.int8)
     scale = torch.empty((m,), device=x.device, dtype=torch.float32)

@@ -143,7 +143,7 @@ def test_dequant_weight_exact(dev, n, k):
     assert np.array_equal(got, want), mismatch(got, want)
 
 
-@pytest.mark.parametrize("m,n", [(1, 16), (8, 64), (33, 1040), (4096, 5120)])
+@pytest.mark.parametrize("m,n", [(1, 16), (8, 64), (33, 1040), (4096, 5120), (3, 100), (1, 4)])
 def test_quantize_row_exact(dev, m, n):
     dy = activation(m, n, seed=m, scale=1e-3, n_out=0)
     q, s = int8.quantize_row(dy.to(dev))
@@ -326,6 +326,28 @@ def test_linear_dw(dev, m, n, k):
     err = np.abs(got - ref)
     assert np.all(err <= 2.0 ** -8 * np.abs(ref) + 2.0 ** -14 * mag), float(
         np.max(err / (2.0 ** -8 * np.abs(ref) + 2.0 ** -14 * mag)))
+
+
+@pytest.mark.parametrize("m,n,k", [(16, 4096, 4096), (64, 1024, 1280), (50, 160, 4112), (1, 32, 48),
+                                   (17, 256, 8192)])
+def test_skinny_gemm_exact(dev, m, n, k):
+    """M <= 64 takes the weight-streaming kernel: int32 and fused-dequant forms."""
+    rng = np.random.default_rng(m * 7 + n)
+    a = rng.integers(-127, 128, (m, k), dtype=np.int8)
+    b = rng.integers(-127, 128, (n, k), dtype=np.int8)
+    acc = npy(int8.int_mm(torch.from_numpy(a).to(dev), torch.from_numpy(b).to(dev).t()))
+    want = O.int_mm(a, b)
+    assert np.array_equal(acc, want)
+    xs = rng.uniform(0.01, 0.05, m).astype(np.float32)
+    ws = rng.uniform(1e-5, 1e-4, n).astype(np.float32)
+    bias = rng.standard_normal(n).astype(np.float32) * 0.01
+    t = [torch.from_numpy(v).to(dev) for v in (a, xs, b, ws, bias)]
+    out = torch.empty((m, n), device=dev, dtype=torch.bfloat16)
+    lib = L._lib()
+    rc = lib.xpuint8_linear_gemm_stream(L._stream(dev), L._ptr(t[0]), L._ptr(t[1]), L._ptr(t[2]),
+                                        L._ptr(t[3]), L._ptr(t[4]), 0, L._ptr(out), m, n, k)
+    assert rc == 0, lib.xpuint8_last_error()
+    assert np.array_equal(bits(out), O.dequant(want, xs, ws, bias))
 
 
 def test_linear_dx_int8_exact(dev):
