@@ -182,6 +182,49 @@ __device__ __attribute__((aligned(16))) int8_t g_zero16[16];
 // global_load_lds_dwordx4 writes (lane l -> bytes [16l, 16l+16)).
 __device__ __forceinline__ int swz(int r, int c) { return c ^ ((r >> 1) & 3); }
 
+// LDS reads of MFMA fragments, issued as inline assembly so the kernel can
+// place them all at the start of a K step and wait for each one just before
+// its MFMAs (lgkm_wait<N>: at most N of this wave's LDS reads outstanding).
+// The loop issues no scalar memory reads, which share the counter.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return static_cast<uint32_t>(
+        reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)p));
+}
+__device__ __forceinline__ v4i lds_read16(uint32_t addr) {
+    v4i r;
+    asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(addr));
+    return r;
+}
+// Wait until at most N LDS reads are outstanding; v is tied to the wait so
+// its uses cannot be scheduled above it.
+template <int N>
+__device__ __forceinline__ void lgkm_wait(v4i& v) {
+    asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(v) : "n"(N));
+}
+
+// Column b of the wave's MFMA blocks: wait for X fragment b (and, for b = 0,
+// every W fragment, which were read first), then TN MFMAs, then the step's
+// b-th global->LDS load for a later stage (after_column(b)), so the wave's
+// loads leave spread over the step instead of as a burst ahead of its MFMAs.
+template <int TN, int TM, int B = 0, class F>
+__device__ __forceinline__ void mfma_columns(v4i (&acc)[TN][TM], v4i (&wf)[TN], v4i (&xf)[TM],
+                                             const F& after_column) {
+    if constexpr (B < TM) {
+        if constexpr (B == 0) {
+#pragma unroll
+            for (int a = 0; a < TN; ++a) lgkm_wait<TM>(wf[a]);
+        }
+        lgkm_wait<TM - 1 - B>(xf[B]);
+#pragma unroll
+        for (int a = 0; a < TN; ++a)
+            acc[a][B] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[a], xf[B], acc[a][B], 0, 0, 0);
+        after_column(B);
+        // keep the next column's wait (and load) below these MFMAs
+        __builtin_amdgcn_sched_barrier(0);
+        mfma_columns<TN, TM, B + 1>(acc, wf, xf, after_column);
+    }
+}
+
 // One 16-byte global -> LDS DMA per lane (global_load_lds_dwordx4): lane l's
 // bytes land at ldst + 16*l; ldst must be the same for the whole wave.
 __device__ __forceinline__ void dma16(const int8_t* gsrc, int8_t* ldst) {
@@ -314,9 +357,9 @@ __global__ __launch_bounds__(WGM * WGN * 64) void gemm_i8_kernel(
 // (so one block's prologue and epilogue overlap the other's main loop); a
 // wave owns (BM/WGM) x (BN/WGN) = TM x TN MFMA blocks.  K runs in 64-byte
 // steps through a ring of STAGES LDS stages filled by direct global->LDS
-// loads issued STAGES-1 steps ahead; the stage is padded to a multiple of
-// 4 KB so every wave issues the same number of loads.  A step reads the
-// wave's TM + TN fragments right after its barrier and runs TM * TN MFMAs on
+// loads issued STAGES-1 steps ahead; a stage is exactly (BM + BN) / 16 KB, so
+// three 26 KB stages of two 256x160 blocks fit in a CU's 160 KB.  A step reads
+// the wave's TM + TN fragments right after its barrier and runs TM * TN MFMAs on
 // them; the other block's waves keep the matrix core busy meanwhile.
 //
 // N is the number of output columns.  With a kPaired epilogue the tile's BN
@@ -335,8 +378,10 @@ __global__ __launch_bounds__(WGM * WGN * 64, 8 / (WGM * WGN)) void gemm_i8_big_k
     constexpr int BK = 64;
     constexpr int WM = BM / WGM, WN = BN / WGN, TM = WM / 16, TN = WN / 16;
     constexpr int XB = BM / 16, WB = BN / 16;
-    constexpr int PER_WAVE = (XB + WB + NW - 1) / NW;           // DMA per wave per step
-    constexpr int STAGE_BYTES = NW * PER_WAVE * 1024;
+    constexpr int NB = XB + WB;                                 // 1 KB blocks per stage
+    constexpr int PER_WAVE = (NB + NW - 1) / NW;                // DMA per wave per step (max)
+    constexpr int REM = NB % NW;                                // waves < REM issue PER_WAVE
+    constexpr int STAGE_BYTES = NB * 1024;                      // unpadded: 3 stages x 2 blocks fit
     constexpr int RING = STAGES * STAGE_BYTES;
     constexpr int STG_ROWS = 32;                                // epilogue rows per pass
     static_assert(!Epi::kStaged || NW * STG_ROWS * 256 <= RING, "staging fits in the ring");
@@ -361,10 +406,10 @@ __global__ __launch_bounds__(WGM * WGN * 64, 8 / (WGM * WGN)) void gemm_i8_big_k
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = wave / WGN, wn = wave % WGN;
 
-    // DMA: wave w brings blocks w, w+NW, ... of every step; blocks 0..XB-1 are
-    // X rows, XB..XB+WB-1 W rows, the rest padding (a repeat of the last W
-    // block into slots nobody reads).  Lane l: row l/4, chunk swz(l/4, l%4).
-    // Rows past M or N repeat the last row (their results are never stored).
+    // DMA: wave w brings blocks w, w+NW, ... < NB of every step (PER_WAVE or
+    // PER_WAVE - 1 of them); blocks 0..XB-1 are X rows, XB..NB-1 W rows.
+    // Lane l: row l/4, chunk swz(l/4, l%4).  Rows past M or N repeat the last
+    // row (their results are never stored).
     const int lr = lane >> 2;
     const int lc = swz(lr, lane & 3) * 16;
     const int8_t* const xbase = X + int64_t(m0) * ldx;
@@ -374,7 +419,7 @@ __global__ __launch_bounds__(WGM * WGN * 64, 8 / (WGM * WGN)) void gemm_i8_big_k
     int off[PER_WAVE];
 #pragma unroll
     for (int i = 0; i < PER_WAVE; ++i) {
-        const int j = min(wave + NW * i, XB + WB - 1);
+        const int j = min(wave + NW * i, NB - 1);
         if (j < XB) {
             base[i] = xbase;
             off[i] = (min(m0 + 16 * j + lr, M - 1) - m0) * int(ldx) + lc;
@@ -387,18 +432,35 @@ __global__ __launch_bounds__(WGM * WGN * 64, 8 / (WGM * WGN)) void gemm_i8_big_k
             off[i] = (min(n0 + 16 * (j - XB) + lr, N - 1) - n0) * int(ldw) + lc;
         }
     }
+    const bool full_share = REM == 0 || wave < REM;             // issues PER_WAVE per step
+    auto issue_one = [&](int i, int buf, int k0) {
+        if (i == PER_WAVE - 1 && !full_share) return;
+        const int8_t* p = base[i] + (off[i] + k0);
+        if (KTAIL && k0 + lc >= K) p = g_zero16;
+        dma16(p, smem + buf * STAGE_BYTES + (wave + NW * i) * 1024);
+    };
     auto issue = [&](int buf, int k0) {
 #pragma unroll
-        for (int i = 0; i < PER_WAVE; ++i) {
-            const int8_t* p = base[i] + (off[i] + k0);
-            if (KTAIL && k0 + lc >= K) p = g_zero16;
-            dma16(p, smem + buf * STAGE_BYTES + (wave + NW * i) * 1024);
+        for (int i = 0; i < PER_WAVE; ++i) issue_one(i, buf, k0);
+    };
+    // this wave's loads of a step are complete once at most `later` steps'
+    // worth of its own loads remain outstanding
+    auto wait_loads = [&](int later) {
+        if (full_share) {
+            if (later >= 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * PER_WAVE));
+            else if (later == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(PER_WAVE));
+            else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        } else {
+            if (later >= 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * (PER_WAVE - 1)));
+            else if (later == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(PER_WAVE - 1));
+            else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
         }
     };
 
     const int frag = (lane & 15) * 64 + swz(lane & 15, lane >> 4) * 16;
     const int xoff = (wm * TM) * 1024 + frag;
     const int woff = (XB + wn * TN) * 1024 + frag;
+    const uint32_t sbase = lds_addr(smem);
 
     v4i acc[TN][TM];
 #pragma unroll
@@ -412,25 +474,30 @@ __global__ __launch_bounds__(WGM * WGN * 64, 8 / (WGM * WGN)) void gemm_i8_big_k
         if (s < KT) issue(s, s * BK);
 #pragma clang loop unroll(disable)
     for (int kt = 0; kt < KT; ++kt) {
-        // step kt's loads are done once only the later groups may be pending
-        const int later = min(KT - 1 - kt, STAGES - 2);
-        if (later >= 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * PER_WAVE));
-        else if (later == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(PER_WAVE));
-        else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        // step kt's loads are done once only the later steps' may be pending
+        wait_loads(min(KT - 1 - kt, STAGES - 2));
         __builtin_amdgcn_s_barrier();
-        // the buffer refilled now was read at step kt-1, before this barrier
-        if (kt + STAGES - 1 < KT) issue((kt + STAGES - 1) % STAGES, (kt + STAGES - 1) * BK);
-        const int8_t* sb = smem + (kt % STAGES) * STAGE_BYTES;
+        // the buffer refilled during this step was read at step kt-1, before
+        // this barrier; its loads go out between the MFMA columns
+        const bool refill = kt + STAGES - 1 < KT;
+        const int rbuf = (kt + STAGES - 1) % STAGES, rk0 = (kt + STAGES - 1) * BK;
+        // all TN + TM fragment reads go out at once; column b's MFMAs wait
+        // only for the reads up to X fragment b
+        const uint32_t sb = sbase + (kt % STAGES) * STAGE_BYTES;
         v4i wf[TN], xf[TM];
 #pragma unroll
-        for (int i = 0; i < TN; ++i) wf[i] = *reinterpret_cast<const v4i*>(sb + woff + i * 1024);
+        for (int i = 0; i < TN; ++i) wf[i] = lds_read16(sb + woff + i * 1024);
 #pragma unroll
-        for (int i = 0; i < TM; ++i) xf[i] = *reinterpret_cast<const v4i*>(sb + xoff + i * 1024);
+        for (int i = 0; i < TM; ++i) xf[i] = lds_read16(sb + xoff + i * 1024);
+        static_assert(TM <= 16, "lgkmcnt range");
+        constexpr int LPC = (PER_WAVE + TM - 1) / TM;           // loads per column
+        mfma_columns<TN, TM>(acc, wf, xf, [&](int b) {
+            if (refill) {
 #pragma unroll
-        for (int b = 0; b < TM; ++b)
-#pragma unroll
-            for (int a = 0; a < TN; ++a)
-                acc[a][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[a], xf[b], acc[a][b], 0, 0, 0);
+                for (int i = b * LPC; i < (b + 1) * LPC; ++i)
+                    if (i < PER_WAVE) issue_one(i, rbuf, rk0);
+            }
+        });
     }
 
     if constexpr (Epi::kStaged) {
