@@ -352,6 +352,65 @@ __global__ __launch_bounds__(WGM * WGN * 64) void gemm_i8_kernel(
     }
 }
 
+// The staged epilogue of one wave: its TM x TN blocks of results (output
+// rows m0w.., columns n0w..), 32 rows per pass through `stg` (8 KB of idle
+// LDS): 256-byte rows of 16-byte chunks, chunk c of row r at c ^ (r & 15),
+// each row leaving as contiguous 16-byte stores.  Row and column operands are
+// loaded before any conversion so their latency is paid once.  Paired
+// epilogues take the (first, second) accumulator pairs (2a, 2a+1).
+template <int TM, int TN, int WN_OUT, class Epi>
+__device__ __forceinline__ void staged_epilogue(const Epi& epi, v4i (&acc)[TN][TM], int8_t* stg,
+                                                int m0w, int n0w, int M, int N, int lane) {
+    constexpr bool PAIRED = Epi::kPaired;
+    constexpr int OUT_TN = PAIRED ? TN / 2 : TN;
+    constexpr int STG_ROWS = 32;
+    constexpr int CH = WN_OUT / 8;                                 // live chunks per row
+    static_assert(CH <= 16 && (STG_ROWS * CH) % 64 == 0, "staging shape");
+    static_assert(TM % 2 == 0, "epilogue passes of 32 rows");
+    float xrow[TM];
+    typename Epi::Col ccol[TN];
+#pragma unroll
+    for (int b = 0; b < TM; ++b) xrow[b] = epi.row(min(m0w + 16 * b + (lane & 15), M - 1));
+#pragma unroll
+    for (int a = 0; a < TN; ++a) {
+        if constexpr (PAIRED)
+            ccol[a] = epi.col(min(n0w + 16 * (a >> 1) + 4 * (lane >> 4), N - 4) +
+                              ((a & 1) ? pair_offset(epi) : 0));
+        else
+            ccol[a] = epi.col(min(n0w + 16 * a + 4 * (lane >> 4), N - 4));
+    }
+#pragma unroll
+    for (int pass = 0; pass < TM / 2; ++pass) {
+#pragma unroll
+        for (int bb = 0; bb < 2; ++bb) {
+            const int b = 2 * pass + bb;
+            const int r = 16 * bb + (lane & 15);
+#pragma unroll
+            for (int a = 0; a < OUT_TN; ++a) {
+                const int c = 16 * a + 4 * (lane >> 4);
+                uint2 v;
+                if constexpr (PAIRED)
+                    v = epi.convert2(acc[2 * a][b], acc[2 * a + 1][b], xrow[b], ccol[2 * a],
+                                     ccol[2 * a + 1]);
+                else
+                    v = epi.convert(acc[a][b], xrow[b], ccol[a]);
+                *reinterpret_cast<uint2*>(stg + r * 256 + (((c >> 3) ^ (r & 15)) << 4) +
+                                          (c & 7) * 2) = v;
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);                       // lgkmcnt(0)
+#pragma unroll
+        for (int i = 0; i < (STG_ROWS * CH) / 64; ++i) {
+            const int flat = i * 64 + lane;
+            const int r = flat / CH, c = flat % CH;
+            const uint4 v = *reinterpret_cast<const uint4*>(stg + r * 256 + ((c ^ (r & 15)) << 4));
+            const int m = m0w + 32 * pass + r, n = n0w + 8 * c;
+            if (m < M && n < N) epi.store16(m, n, v);
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);                       // reads done before reuse
+    }
+}
+
 // ------------------------------------------------------------ large tiles
 // A BM x BN tile per block of 4 waves in a WGM x WGN grid, two blocks per CU
 // (so one block's prologue and epilogue overlap the other's main loop); a
@@ -501,56 +560,9 @@ __global__ __launch_bounds__(WGM * WGN * 64, 8 / (WGM * WGN)) void gemm_i8_big_k
     }
 
     if constexpr (Epi::kStaged) {
-        // bf16 results through this wave's part of the (now idle) ring, 32 rows
-        // per pass: 256-byte rows of 16-byte chunks, chunk c of row r at
-        // c ^ (r & 15); each row leaves as contiguous 16-byte stores.
-        constexpr int CH = WN_OUT / 8;                             // live chunks per row
-        static_assert(CH <= 16 && (STG_ROWS * CH) % 64 == 0, "staging shape");
-        float xrow[TM];
-        typename Epi::Col ccol[TN];
-#pragma unroll
-        for (int b = 0; b < TM; ++b)
-            xrow[b] = epi.row(min(m0 + wm * WM + 16 * b + (lane & 15), M - 1));
-#pragma unroll
-        for (int a = 0; a < TN; ++a) {
-            if constexpr (PAIRED)
-                ccol[a] = epi.col(min(n0 + wn * WN_OUT + 16 * (a >> 1) + 4 * (lane >> 4), N - 4) +
-                                  ((a & 1) ? epi.half : 0));
-            else
-                ccol[a] = epi.col(min(n0 + wn * WN + 16 * a + 4 * (lane >> 4), N - 4));
-        }
         __builtin_amdgcn_s_barrier();                              // ring no longer read
-        int8_t* stg = smem + wave * (STG_ROWS * 256);
-#pragma unroll
-        for (int pass = 0; pass < TM / 2; ++pass) {
-#pragma unroll
-            for (int bb = 0; bb < 2; ++bb) {
-                const int b = 2 * pass + bb;
-                const int r = 16 * bb + (lane & 15);
-#pragma unroll
-                for (int a = 0; a < OUT_TN; ++a) {
-                    const int c = 16 * a + 4 * (lane >> 4);
-                    uint2 v;
-                    if constexpr (PAIRED)
-                        v = epi.convert2(acc[2 * a][b], acc[2 * a + 1][b], xrow[b], ccol[2 * a],
-                                         ccol[2 * a + 1]);
-                    else
-                        v = epi.convert(acc[a][b], xrow[b], ccol[a]);
-                    *reinterpret_cast<uint2*>(stg + r * 256 + (((c >> 3) ^ (r & 15)) << 4) +
-                                              (c & 7) * 2) = v;
-                }
-            }
-            __builtin_amdgcn_s_waitcnt(0xC07F);                   // lgkmcnt(0)
-#pragma unroll
-            for (int i = 0; i < (STG_ROWS * CH) / 64; ++i) {
-                const int flat = i * 64 + lane;
-                const int r = flat / CH, c = flat % CH;
-                const uint4 v = *reinterpret_cast<const uint4*>(stg + r * 256 + ((c ^ (r & 15)) << 4));
-                const int m = m0 + wm * WM + 32 * pass + r, n = n0 + wn * WN_OUT + 8 * c;
-                if (m < M && n < N) epi.store16(m, n, v);
-            }
-            __builtin_amdgcn_s_waitcnt(0xC07F);                   // reads done before reuse
-        }
+        staged_epilogue<TM, TN, WN_OUT, Epi>(epi, acc, smem + wave * (32 * 256),
+                                             m0 + wm * WM, n0 + wn * WN_OUT, M, N, lane);
     } else {
         const int mrow = m0 + wm * WM + (lane & 15);
         const int ncol = n0 + wn * WN + 4 * (lane >> 4);
@@ -573,6 +585,139 @@ hipError_t launch_cfg(hipStream_t st, const int8_t* X, int64_t ldx, const int8_t
     const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
     hipLaunchKernelGGL((gemm_i8_kernel<BM, BN, WGM, WGN, STAGES, Epi>), dim3(unsigned(tm * tn)),
                        dim3(WGM * WGN * 64), 0, st, X, ldx, W, ldw, M, N, K, tm, tn, epi);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------ split K
+// Narrow outputs with a long K (the FFN's down-projection, dx: N = 1280,
+// K = 5120) give too few large tiles to fill the chip.  Here a 128 x 160
+// tile belongs to a block of 8 waves in two teams of 4 (2 x 2 waves of
+// 64 x 80 each): team 0 runs the first half of the K steps and team 1 the
+// second, each through its own 2-stage LDS ring, in lock step (one barrier).
+// Team 1 then hands its accumulators to team 0 through LDS in two halves
+// (exact int32 sums), and team 0 runs the epilogue.
+template <bool KTAIL, class Epi>
+__global__ __launch_bounds__(512, 1) void gemm_i8_splitk_kernel(
+    const int8_t* __restrict__ X, int64_t ldx, const int8_t* __restrict__ W, int64_t ldw, int M,
+    int N, int K, int tiles_m, int tiles_n, Epi epi) {
+    constexpr int BM = 128, BN = 160, BK = 64, STAGES = 2;
+    constexpr int TM = 4, TN = 5, WM = 64, WN = 80;
+    constexpr int XB = BM / 16, WB = BN / 16, NB = XB + WB;     // 18 blocks of 1 KB per stage
+    constexpr int PER_WAVE = (NB + 3) / 4, REM = NB % 4;
+    constexpr int STAGE_BYTES = NB * 1024, RING = STAGES * STAGE_BYTES;
+    static_assert(!Epi::kPaired && Epi::kStaged, "dequant epilogues only");
+    static_assert(2 * RING >= 4 * TN * (TM / 2) * 1024, "half of a team's accumulators fit");
+    __shared__ __attribute__((aligned(1024))) int8_t smem[2 * RING];
+
+    const int tiles = tiles_m * tiles_n;
+    int t = blockIdx.x;
+    if (tiles % 8 == 0) t = (t % 8) * (tiles / 8) + t / 8;
+    const int m0 = (t % tiles_m) * BM, n0 = (t / tiles_m) * BN;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int team = wave >> 2, wt = wave & 3;
+    const int wm = wt >> 1, wn = wt & 1;
+    int8_t* ring = smem + team * RING;
+
+    const int KT = (K + BK - 1) / BK, KH = (KT + 1) / 2;      // steps; team 0 takes the first KH
+    const int kt0 = team * KH, kt_end = min(KT, kt0 + KH);
+
+    const int lr = lane >> 2;
+    const int lc = swz(lr, lane & 3) * 16;
+    const int8_t* const xbase = X + int64_t(m0) * ldx;
+    const int8_t* const wbase = W + int64_t(n0) * ldw;
+    const int8_t* base[PER_WAVE];
+    int off[PER_WAVE];
+#pragma unroll
+    for (int i = 0; i < PER_WAVE; ++i) {
+        const int j = min(wt + 4 * i, NB - 1);
+        if (j < XB) {
+            base[i] = xbase;
+            off[i] = (min(m0 + 16 * j + lr, M - 1) - m0) * int(ldx) + lc;
+        } else {
+            base[i] = wbase;
+            off[i] = (min(n0 + 16 * (j - XB) + lr, N - 1) - n0) * int(ldw) + lc;
+        }
+    }
+    const bool full_share = REM == 0 || wt < REM;
+    auto issue = [&](int buf, int k0) {
+#pragma unroll
+        for (int i = 0; i < PER_WAVE; ++i) {
+            if (i == PER_WAVE - 1 && !full_share) break;
+            const int8_t* p = base[i] + (off[i] + k0);
+            if (KTAIL && k0 + lc >= K) p = g_zero16;
+            dma16(p, ring + buf * STAGE_BYTES + (wt + 4 * i) * 1024);
+        }
+    };
+    const int frag = (lane & 15) * 64 + swz(lane & 15, lane >> 4) * 16;
+    const int xoff = (wm * TM) * 1024 + frag;
+    const int woff = (XB + wn * TN) * 1024 + frag;
+    const uint32_t rbase = lds_addr(ring);
+
+    v4i acc[TN][TM];
+#pragma unroll
+    for (int a = 0; a < TN; ++a)
+#pragma unroll
+        for (int b = 0; b < TM; ++b) acc[a][b] = v4i{0, 0, 0, 0};
+
+    if (kt0 < kt_end) issue(0, kt0 * BK);
+#pragma clang loop unroll(disable)
+    for (int s = 0; s < KH; ++s) {
+        const int kt = kt0 + s;
+        const bool live = kt < kt_end;          // team 1 may have one step fewer
+        // this step's loads done (the only ones outstanding), then all waves meet
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        __builtin_amdgcn_s_barrier();
+        if (kt + 1 < kt_end) issue((s + 1) & 1, (kt + 1) * BK);
+        if (live) {
+            const uint32_t sb = rbase + (s & 1) * STAGE_BYTES;
+            v4i wf[TN], xf[TM];
+#pragma unroll
+            for (int i = 0; i < TN; ++i) wf[i] = lds_read16(sb + woff + i * 1024);
+#pragma unroll
+            for (int i = 0; i < TM; ++i) xf[i] = lds_read16(sb + xoff + i * 1024);
+            mfma_columns<TN, TM>(acc, wf, xf, [](int) {});
+        }
+    }
+
+    // team 1 -> team 0 through LDS, TM/2 rows of blocks at a time: lane-linear
+    // 16-byte slots (wt, a, b) so every access is a plain ds_read/write_b128
+    v4i* xchg = reinterpret_cast<v4i*>(smem);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        __syncthreads();                        // rings (or the previous half) no longer read
+        if (team == 1) {
+#pragma unroll
+            for (int a = 0; a < TN; ++a)
+#pragma unroll
+                for (int bb = 0; bb < TM / 2; ++bb)
+                    xchg[((wt * TN + a) * (TM / 2) + bb) * 64 + lane] = acc[a][h * (TM / 2) + bb];
+        }
+        __syncthreads();
+        if (team == 0) {
+#pragma unroll
+            for (int a = 0; a < TN; ++a)
+#pragma unroll
+                for (int bb = 0; bb < TM / 2; ++bb)
+                    acc[a][h * (TM / 2) + bb] += xchg[((wt * TN + a) * (TM / 2) + bb) * 64 + lane];
+        }
+    }
+    __syncthreads();                            // exchange buffer free
+    if (team == 0)
+        staged_epilogue<TM, TN, WN, Epi>(epi, acc, smem + wt * (32 * 256), m0 + wm * WM,
+                                         n0 + wn * WN, M, N, lane);
+}
+
+template <class Epi>
+hipError_t launch_splitk(hipStream_t st, const int8_t* X, int64_t ldx, const int8_t* W,
+                         int64_t ldw, int M, int N, int K, const Epi& epi) {
+    const int tm = (M + 127) / 128, tn = (N + 159) / 160;
+    if (K % 64 == 0)
+        hipLaunchKernelGGL((gemm_i8_splitk_kernel<false, Epi>), dim3(unsigned(tm * tn)), dim3(512),
+                           0, st, X, ldx, W, ldw, M, N, K, tm, tn, epi);
+    else
+        hipLaunchKernelGGL((gemm_i8_splitk_kernel<true, Epi>), dim3(unsigned(tm * tn)), dim3(512),
+                           0, st, X, ldx, W, ldw, M, N, K, tm, tn, epi);
     return hipGetLastError();
 }
 
@@ -656,7 +801,8 @@ hipError_t launch_skinny(hipStream_t st, const int8_t* X, int64_t ldx, const int
 // CU, two LDS stages: the fastest of the 256x128/128x256/256x192/128x160
 // shapes and stage counts measured at M=4096, K=1280, N=10240) whenever it
 // gives at least 192 tiles; otherwise the small one (128 x 128, 4 waves of
-// 64 x 64, four stages); M <= 64 takes the weight-streaming skinny kernel.
+// 64 x 64, four stages); M <= 64 takes the weight-streaming skinny kernel;
+// a narrow output with K >= 2048 (too few large tiles) the split-K kernel.
 // Paired epilogues always take the large tile.
 template <class Epi>
 hipError_t launch_gemm(hipStream_t st, const int8_t* X, int64_t ldx, const int8_t* W, int64_t ldw,
@@ -677,6 +823,12 @@ hipError_t launch_gemm(hipStream_t st, const int8_t* X, int64_t ldx, const int8_
     } else {
         if (M <= 64) return launch_skinny(st, X, ldx, W, ldw, M, N, K, epi);
         const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
+        if constexpr (Epi::kStaged) {
+            // narrow output, long K: split K inside 128 x 160 tiles instead
+            const int64_t tiles_split = int64_t((M + 127) / 128) * ((N + 159) / 160);
+            if (int64_t(tm) * tn < 192 && K >= 2048 && tiles_split >= 128)
+                return launch_splitk(st, X, ldx, W, ldw, M, N, K, epi);
+        }
         if (int64_t(tm) * tn >= 192) {
             if (K % 64 == 0)
                 hipLaunchKernelGGL((gemm_i8_big_kernel<BM, BN, 2, 2, STAGES, false, Epi>),

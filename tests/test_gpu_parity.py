@@ -350,6 +350,33 @@ def test_skinny_gemm_exact(dev, m, n, k):
     assert np.array_equal(bits(out), O.dequant(want, xs, ws, bias))
 
 
+@pytest.mark.parametrize("m,n,k", [(2100, 1296, 2064), (4096, 1280, 5120)])
+def test_split_k_gemm_exact(dev, m, n, k):
+    """Narrow output, long K: the split-K kernel (ragged M and N tiles, K not a
+    multiple of 64), through the fused-dequant entry point."""
+    rng = np.random.default_rng(m + k)
+    a = rng.integers(-127, 128, (m, k), dtype=np.int8)
+    b = rng.integers(-127, 128, (n, k), dtype=np.int8)
+    xs = rng.uniform(0.01, 0.05, m).astype(np.float32)
+    ws = rng.uniform(1e-5, 1e-4, n).astype(np.float32)
+    t = [torch.from_numpy(v).to(dev) for v in (a, xs, b, ws)]
+    out = torch.empty((m, n), device=dev, dtype=torch.bfloat16)
+    lib = L._lib()
+    rc = lib.xpuint8_linear_gemm_stream(L._stream(dev), L._ptr(t[0]), L._ptr(t[1]), L._ptr(t[2]),
+                                        L._ptr(t[3]), None, 0, L._ptr(out), m, n, k)
+    assert rc == 0, lib.xpuint8_last_error()
+    want = O.dequant(O.int_mm(a, b), xs, ws)
+    assert np.array_equal(bits(out), want), mismatch(bits(out), want)
+
+
+def test_linear_dx_int8_full_size_c5(dev):
+    dy = activation(4096, 5120, seed=8, scale=1e-3, n_out=0)
+    w8, ws = int8.prepare_weight(weight(5120, 1280, seed=9).to(dev))
+    dx = int8.linear_dx_int8(dy.to(dev), w8, ws)
+    want = O.linear_dx_int8(bits(dy), npy(w8), npy(ws))
+    assert np.array_equal(bits(dx), want), mismatch(bits(dx), want)
+
+
 def test_linear_dx_int8_exact(dev):
     m, n, k = 512, 1280, 1280
     dy = activation(m, n, seed=8, scale=1e-3, n_out=0)
