@@ -881,22 +881,31 @@ __global__ __launch_bounds__(256) void dequant_kernel(const int32_t* __restrict_
 }
 
 // ------------------------------------------------------------ int8 transpose
-// out[c, r] = in[r, c]; 64 x 64 tiles through LDS.
+// out[c, r] = in[r, c] (R, C multiples of 4).  Each thread moves one 4 x 4
+// byte block: four dword loads of rows r..r+3, a register transpose with
+// byte permutes, four dword stores to rows c..c+3 of the output.  A block of
+// 256 threads covers 64 x 64 bytes; 16 threads share each 64-byte row
+// segment on both sides.
 __global__ __launch_bounds__(256) void transpose_i8_kernel(const int8_t* __restrict__ in,
                                                           int8_t* __restrict__ out, int64_t R,
                                                           int64_t C) {
-    __shared__ int8_t tile[64][65];
-    const int64_t r0 = int64_t(blockIdx.y) * 64, c0 = int64_t(blockIdx.x) * 64;
-    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-    for (int i = ty; i < 64; i += 4) {
-        const int64_t r = r0 + i, c = c0 + tx;
-        tile[i][tx] = (r < R && c < C) ? in[r * C + c] : int8_t(0);
-    }
-    __syncthreads();
-    for (int i = ty; i < 64; i += 4) {
-        const int64_t c = c0 + i, r = r0 + tx;
-        if (c < C && r < R) out[c * R + r] = tile[tx][i];
-    }
+    const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+    const int64_t r = int64_t(blockIdx.y) * 64 + 4 * ty, c = int64_t(blockIdx.x) * 64 + 4 * tx;
+    if (r >= R || c >= C) return;
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = *reinterpret_cast<const uint32_t*>(in + (r + i) * C + c);
+    // w[i] = bytes (row r+i, columns c..c+3); o[j] = bytes (column c+j, rows r..r+3)
+    const uint32_t lo01 = __builtin_amdgcn_perm(w[1], w[0], 0x05010400u);
+    const uint32_t hi01 = __builtin_amdgcn_perm(w[1], w[0], 0x07030602u);
+    const uint32_t lo23 = __builtin_amdgcn_perm(w[3], w[2], 0x05010400u);
+    const uint32_t hi23 = __builtin_amdgcn_perm(w[3], w[2], 0x07030602u);
+    const uint32_t o[4] = {__builtin_amdgcn_perm(lo23, lo01, 0x05040100u),
+                           __builtin_amdgcn_perm(lo23, lo01, 0x07060302u),
+                           __builtin_amdgcn_perm(hi23, hi01, 0x05040100u),
+                           __builtin_amdgcn_perm(hi23, hi01, 0x07060302u)};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) *reinterpret_cast<uint32_t*>(out + (c + j) * R + r) = o[j];
 }
 
 }  // namespace
