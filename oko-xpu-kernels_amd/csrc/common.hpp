@@ -150,6 +150,21 @@ __device__ __forceinline__ float wave_max(float x) {
     return x;
 }
 
+// Max over the 16 lanes of an aligned segment (lanes 16j..16j+15) of the
+// bit patterns of non-negative floats (which order like their values); an
+// integer max folds its DPP operand into one instruction per step.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dppu(uint32_t x) {
+    return uint32_t(__builtin_amdgcn_mov_dpp(int(x), CTRL, 0xF, 0xF, true));
+}
+__device__ __forceinline__ uint32_t segment_max_bits(uint32_t x) {
+    x = max(x, dppu<kDppXor1>(x));
+    x = max(x, dppu<kDppXor2>(x));
+    x = max(x, dppu<kDppXor7>(x));
+    x = max(x, dppu<kDppXor15>(x));
+    return x;
+}
+
 // Max over the 16 lanes of an aligned segment (lanes 16j..16j+15).
 __device__ __forceinline__ float segment_max(float x) {
     x = fmaxf(x, dpp<kDppXor1>(x));

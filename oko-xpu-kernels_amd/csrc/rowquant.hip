@@ -10,6 +10,8 @@
 // keep the whole row in registers across as many 16-lane segments as it needs
 // (rowquant_seg_kernel); rows too long for that use the two-pass variant, one
 // wave per row, which re-reads the row (from L2) to quantize it.
+#include <type_traits>
+
 #include "common.hpp"
 #include "kernels.hpp"
 #include "activations.hpp"
@@ -18,6 +20,18 @@ namespace xpuint8 {
 namespace {
 
 constexpr int kRowsPerBlock = 4;     // 4 waves = 4 rows per 256-thread block
+
+// Element (r, col) of a row-major array whose base is already advanced to a
+// block's first row: the offset is formed in 32 bits (r and col are small,
+// r*ld + col < 2^32), so the address is a wave-uniform base plus one 32-bit
+// lane offset.
+// (r < 64 and ld < 2^24: a 24-bit multiply.)
+template <class T>
+__device__ __forceinline__ T* at32(T* base, int r, int64_t ld, int col) {
+    using B = typename std::conditional<std::is_const<T>::value, const char, char>::type;
+    const uint32_t off = (__umul24(uint32_t(r), uint32_t(ld)) + uint32_t(col)) * uint32_t(sizeof(T));
+    return reinterpret_cast<T*>(reinterpret_cast<B*>(base) + uint64_t(off));
+}
 
 // ------------------------------------------------------------------ loaders
 // A loader produces the pre-rotation values of elements [col, col+16) of a
@@ -32,6 +46,13 @@ struct LoadBF16 {
     struct Raw { u32x4 a, b; };
     __device__ __forceinline__ Raw fetch(int64_t row, int col) const {
         const uint16_t* p = x + row * ld + col;
+        return Raw{load16(p), load16(p + 8)};
+    }
+    // the same loader with row 0 at row0, and fetch() from it with 32-bit
+    // offsets (r < rows per block)
+    __device__ __forceinline__ LoadBF16 rebase(int64_t row0) const { return {x + row0 * ld, ld}; }
+    __device__ __forceinline__ Raw fetch_r(int r, int col) const {
+        const uint16_t* p = at32(x, r, ld, col);
         return Raw{load16(p), load16(p + 8)};
     }
     __device__ __forceinline__ void expand(const Raw& r, float (&v)[16]) const {
@@ -57,6 +78,15 @@ struct LoadAct {
         Raw r;
         r.a = LoadBF16{x, ld}.fetch(row, col);
         if constexpr (act_paired(ACT)) r.b = LoadBF16{x + half, ld}.fetch(row, col);
+        return r;
+    }
+    __device__ __forceinline__ LoadAct rebase(int64_t row0) const {
+        return {x + row0 * ld, ld, half, tab};
+    }
+    __device__ __forceinline__ Raw fetch_r(int rr, int col) const {
+        Raw r;
+        r.a = LoadBF16{x, ld}.fetch_r(rr, col);
+        if constexpr (act_paired(ACT)) r.b = LoadBF16{x + half, ld}.fetch_r(rr, col);
         return r;
     }
     __device__ __forceinline__ void expand(const Raw& r, float (&v)[16]) const {
@@ -121,6 +151,14 @@ struct LoadDequantAct {
         (*this)(row, col, r.v);
         return r;
     }
+    __device__ __forceinline__ LoadDequantAct rebase(int64_t row0) const {
+        return {acc + row0 * ld, ld, half, xs + row0, ws, tab};
+    }
+    __device__ __forceinline__ Raw fetch_r(int r, int col) const {
+        Raw o;
+        (*this)(r, col, o.v);
+        return o;
+    }
     __device__ __forceinline__ void expand(const Raw& r, float (&v)[16]) const {
 #pragma unroll
         for (int t = 0; t < 16; ++t) v[t] = r.v[t];
@@ -135,6 +173,19 @@ struct LoadColScaled {
     int64_t ld;
     const float* colscale;   // may be null: plain bf16 rows
     struct Raw { LoadBF16::Raw x; float4 c[4]; };
+    __device__ __forceinline__ LoadColScaled rebase(int64_t row0) const {
+        return {x + row0 * ld, ld, colscale};
+    }
+    __device__ __forceinline__ Raw fetch_r(int rr, int col) const {
+        Raw r;
+        r.x = LoadBF16{x, ld}.fetch_r(rr, col);
+        if (colscale) {
+            const float4* q = reinterpret_cast<const float4*>(colscale + col);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) r.c[j] = q[j];
+        }
+        return r;
+    }
     __device__ __forceinline__ Raw fetch(int64_t row, int col) const {
         Raw r;
         r.x = LoadBF16{x, ld}.fetch(row, col);
@@ -171,6 +222,12 @@ struct LoadDequantWeight {
     struct Raw { int4 a; float s; };
     __device__ __forceinline__ Raw fetch(int64_t row, int col) const {
         return Raw{*reinterpret_cast<const int4*>(w8 + row * ld + col), scale[row]};
+    }
+    __device__ __forceinline__ LoadDequantWeight rebase(int64_t row0) const {
+        return {w8 + row0 * ld, ld, scale + row0};
+    }
+    __device__ __forceinline__ Raw fetch_r(int r, int col) const {
+        return Raw{*reinterpret_cast<const int4*>(at32(w8, r, ld, col)), scale[r]};
     }
     __device__ __forceinline__ void expand(const Raw& r, float (&v)[16]) const {
         const uint32_t w[4] = {uint32_t(r.a.x), uint32_t(r.a.y), uint32_t(r.a.z), uint32_t(r.a.w)};
@@ -275,21 +332,24 @@ __global__ __launch_bounds__(1024) void rowquant_seg_kernel(Loader load, int8_t*
     __shared__ uint32_t row_max[kMaxSegments];
     const int seg = threadIdx.x >> 4;
     const int sl = threadIdx.x & 15;
-    const int r = (seg * s_mul) >> 12;           // seg / S (exact for seg, S <= 64)
-    const int sg = seg - r * S;                  // segment within the row
-    const int64_t row = int64_t(blockIdx.x) * R + r;
-    const bool live = r < R && row < M;
-    const int64_t row_ld = row < M ? row : M - 1;
+    const int r = int(__umul24(seg, s_mul)) >> 12;   // seg / S (exact for seg, S <= 64)
+    const int sg = seg - int(__umul24(r, S));        // segment within the row
+    // addresses: the block's first row is wave-uniform, a lane's own row
+    // offset r (clamped to the last row) is small
+    const int64_t row0 = int64_t(blockIdx.x) * R;
+    const bool live = r < R && row0 + r < M;
+    const int r_ld = min(r, int(min(M - 1 - row0, int64_t(R - 1))));
+    const Loader lb = load.rebase(row0);
     int col[P];
     typename Loader::Raw raw[P];
 #pragma unroll
     for (int p = 0; p < P; ++p) {
         col[p] = (sg * P + p) * kGroup + lane_w(sl) * 16;
         if constexpr (FULL) {
-            raw[p] = load.fetch(row_ld, col[p]);
+            raw[p] = lb.fetch_r(r_ld, col[p]);
         } else {
             raw[p] = typename Loader::Raw{};
-            if (col[p] < K) raw[p] = load.fetch(row_ld, col[p]);
+            if (col[p] < K) raw[p] = lb.fetch_r(r_ld, col[p]);
         }
     }
     if (threadIdx.x < R) row_max[threadIdx.x] = 0u;
@@ -298,23 +358,24 @@ __global__ __launch_bounds__(1024) void rowquant_seg_kernel(Loader load, int8_t*
     float m = 0.f;
 #pragma unroll
     for (int p = 0; p < P; ++p) {
-        load.expand(raw[p], v[p]);
+        lb.expand(raw[p], v[p]);
         if constexpr (ROT) hadamard16_unscaled(v[p]);
         m = absmax16(v[p], m);
     }
-    m = segment_max(m);
     // m >= 0 (never NaN), so its bit pattern orders like its value
-    if (live && sl == 0) atomicMax(&row_max[r], __float_as_uint(m));
+    const uint32_t mb = segment_max_bits(__float_as_uint(m));
+    if (live && sl == 0) atomicMax(&row_max[r], mb);
     lds_barrier();
     if (!live) return;
     const float rowmax = __uint_as_float(row_max[r]);
     const float sc = row_scale(MODE, finish_max<ROT, MODE>(rowmax));
     const float inv = 1.0f / sc;
-    if (sg == 0 && sl == 0) scale[row] = sc;
+    if (sg == 0 && sl == 0) scale[row0 + r] = sc;
+    int8_t* const qrow = q + row0 * K;
 #pragma unroll
     for (int p = 0; p < P; ++p) {
         const uint4 w = quant16<ROT, MODE>(v[p], sc, inv);
-        if (FULL || col[p] < K) *reinterpret_cast<uint4*>(q + row * K + col[p]) = w;
+        if (FULL || col[p] < K) *reinterpret_cast<uint4*>(at32(qrow, r, K, col[p])) = w;
     }
 }
 
