@@ -591,22 +591,32 @@ hipError_t launch_cfg(hipStream_t st, const int8_t* X, int64_t ldx, const int8_t
 // ------------------------------------------------------------ split K
 // Narrow outputs with a long K (the FFN's down-projection, dx: N = 1280,
 // K = 5120) give too few large tiles to fill the chip.  Here a 128 x 160
-// tile belongs to a block of 8 waves in two teams of 4 (2 x 2 waves of
-// 64 x 80 each): team 0 runs the first half of the K steps and team 1 the
-// second, each through its own 2-stage LDS ring, in lock step (one barrier).
-// Team 1 then hands its accumulators to team 0 through LDS in two halves
-// (exact int32 sums), and team 0 runs the epilogue.
-template <bool KTAIL, class Epi>
+// tile belongs to a block of 8 waves in two teams of 4 (team = wave / 4, 2 x 2
+// waves of 64 x 80 each): team 0 owns the first half of the K steps and team
+// 1 the second, each through its own ring of S LDS stages.  The teams
+// alternate between MFMAs and data movement every half step, so that on each
+// SIMD one wave feeds the matrix core while the other moves data:
+//   A(s): team 0 runs its step s;  team 1 reads its step s's fragments and
+//         issues its loads for step s + S - 1
+//   B(s): team 1 runs its step s;  team 0 reads its step s + 1's fragments
+//         and issues its loads for step s + S - 1
+// with one s_barrier between phases.  A team's step is complete (each wave
+// waits for its own loads, then the barrier) before the phase that reads it;
+// its stage is refilled only after the phase that consumed it.  Team 1 then
+// hands its accumulators to team 0 through LDS in two halves (exact int32
+// sums), and team 0 runs the epilogue.
+template <int S, bool KTAIL, class Epi>
 __global__ __launch_bounds__(512, 1) void gemm_i8_splitk_kernel(
     const int8_t* __restrict__ X, int64_t ldx, const int8_t* __restrict__ W, int64_t ldw, int M,
     int N, int K, int tiles_m, int tiles_n, Epi epi) {
-    constexpr int BM = 128, BN = 160, BK = 64, STAGES = 2;
+    constexpr int BM = 128, BN = 160, BK = 64;
     constexpr int TM = 4, TN = 5, WM = 64, WN = 80;
     constexpr int XB = BM / 16, WB = BN / 16, NB = XB + WB;     // 18 blocks of 1 KB per stage
-    constexpr int PER_WAVE = (NB + 3) / 4, REM = NB % 4;
-    constexpr int STAGE_BYTES = NB * 1024, RING = STAGES * STAGE_BYTES;
+    constexpr int PER = (NB + 3) / 4, REM = NB % 4;
+    constexpr int STAGE_BYTES = NB * 1024, RING = S * STAGE_BYTES;
     static_assert(!Epi::kPaired && Epi::kStaged, "dequant epilogues only");
     static_assert(2 * RING >= 4 * TN * (TM / 2) * 1024, "half of a team's accumulators fit");
+    static_assert(S >= 3 && S <= 4, "three or four stages");
     __shared__ __attribute__((aligned(1024))) int8_t smem[2 * RING];
 
     const int tiles = tiles_m * tiles_n;
@@ -619,17 +629,17 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_splitk_kernel(
     const int wm = wt >> 1, wn = wt & 1;
     int8_t* ring = smem + team * RING;
 
-    const int KT = (K + BK - 1) / BK, KH = (KT + 1) / 2;      // steps; team 0 takes the first KH
-    const int kt0 = team * KH, kt_end = min(KT, kt0 + KH);
+    const int KT = (K + BK - 1) / BK, KH = (KT + 1) / 2;      // team 0 takes the first KH
+    const int kt0 = team * KH, nst = min(KT, kt0 + KH) - kt0; // this team's steps
 
     const int lr = lane >> 2;
     const int lc = swz(lr, lane & 3) * 16;
     const int8_t* const xbase = X + int64_t(m0) * ldx;
     const int8_t* const wbase = W + int64_t(n0) * ldw;
-    const int8_t* base[PER_WAVE];
-    int off[PER_WAVE];
+    const int8_t* base[PER];
+    int off[PER];
 #pragma unroll
-    for (int i = 0; i < PER_WAVE; ++i) {
+    for (int i = 0; i < PER; ++i) {
         const int j = min(wt + 4 * i, NB - 1);
         if (j < XB) {
             base[i] = xbase;
@@ -640,13 +650,27 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_splitk_kernel(
         }
     }
     const bool full_share = REM == 0 || wt < REM;
-    auto issue = [&](int buf, int k0) {
+    // this wave's loads for the team's step s
+    auto issue = [&](int s) {
+        const int k0 = (kt0 + s) * BK;
+        int8_t* const st = ring + (s % S) * STAGE_BYTES;
 #pragma unroll
-        for (int i = 0; i < PER_WAVE; ++i) {
-            if (i == PER_WAVE - 1 && !full_share) break;
-            const int8_t* p = base[i] + (off[i] + k0);
+        for (int i = 0; i < PER; ++i) {
+            if (i == PER - 1 && !full_share) break;
+            const int8_t* p = base[i] + uint64_t(uint32_t(off[i] + k0));
             if (KTAIL && k0 + lc >= K) p = g_zero16;
-            dma16(p, ring + buf * STAGE_BYTES + (wt + 4 * i) * 1024);
+            dma16(p, st + (wt + 4 * i) * 1024);
+        }
+    };
+    auto wait_batches = [&](int later) {
+        if (full_share) {
+            if (later >= 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * PER));
+            else if (later == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(PER));
+            else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        } else {
+            if (later >= 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * (PER - 1)));
+            else if (later == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(PER - 1));
+            else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
         }
     };
     const int frag = (lane & 15) * 64 + swz(lane & 15, lane >> 4) * 16;
@@ -659,33 +683,62 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_splitk_kernel(
     for (int a = 0; a < TN; ++a)
 #pragma unroll
         for (int b = 0; b < TM; ++b) acc[a][b] = v4i{0, 0, 0, 0};
-
-    if (kt0 < kt_end) issue(0, kt0 * BK);
-#pragma clang loop unroll(disable)
-    for (int s = 0; s < KH; ++s) {
-        const int kt = kt0 + s;
-        const bool live = kt < kt_end;          // team 1 may have one step fewer
-        // this step's loads done (the only ones outstanding), then all waves meet
-        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    v4i wf[TN], xf[TM];
+    auto read_frags = [&](int s) {
+        const uint32_t sb = rbase + (s % S) * STAGE_BYTES;
+#pragma unroll
+        for (int i = 0; i < TN; ++i) wf[i] = lds_read16(sb + woff + i * 1024);
+#pragma unroll
+        for (int i = 0; i < TM; ++i) xf[i] = lds_read16(sb + xoff + i * 1024);
+    };
+    auto compute = [&]() {
+        __builtin_amdgcn_s_waitcnt(0xC07F);                     // lgkmcnt(0)
+#pragma unroll
+        for (int b = 0; b < TM; ++b)
+#pragma unroll
+            for (int a = 0; a < TN; ++a)
+                acc[a][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[a], xf[b], acc[a][b], 0, 0, 0);
+    };
+    auto barrier = [&]() {
+        __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_barrier();
-        if (kt + 1 < kt_end) issue((s + 1) & 1, (kt + 1) * BK);
-        if (live) {
-            const uint32_t sb = rbase + (s & 1) * STAGE_BYTES;
-            v4i wf[TN], xf[TM];
-#pragma unroll
-            for (int i = 0; i < TN; ++i) wf[i] = lds_read16(sb + woff + i * 1024);
-#pragma unroll
-            for (int i = 0; i < TM; ++i) xf[i] = lds_read16(sb + xoff + i * 1024);
-            mfma_columns<TN, TM>(acc, wf, xf, [](int) {});
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    for (int s = 0; s < S - 1; ++s)
+        if (s < nst) issue(s);
+    if (nst > 0) wait_batches(min(S - 2, nst - 1));
+    barrier();
+    if (team == 0) {
+        if (nst > 0) read_frags(0);
+        barrier();
+#pragma clang loop unroll(disable)
+        for (int s = 0; s < KH; ++s) {
+            if (s < nst) compute();                             // A(s)
+            if (s + 1 < nst) wait_batches(min(S - 3, nst - 2 - s));
+            barrier();
+            if (s + 1 < nst) read_frags(s + 1);                 // B(s)
+            if (s + S - 1 < nst) issue(s + S - 1);
+            barrier();
+        }
+    } else {
+        barrier();
+#pragma clang loop unroll(disable)
+        for (int s = 0; s < KH; ++s) {
+            if (s < nst) read_frags(s);                         // A(s)
+            if (s + S - 1 < nst) issue(s + S - 1);
+            barrier();
+            if (s < nst) compute();                             // B(s)
+            if (s + 1 < nst) wait_batches(min(S - 2, nst - 2 - s));
+            barrier();
         }
     }
 
-    // team 1 -> team 0 through LDS, TM/2 rows of blocks at a time: lane-linear
-    // 16-byte slots (wt, a, b) so every access is a plain ds_read/write_b128
+    // team 1 -> team 0 through LDS, TM/2 rows of blocks at a time
     v4i* xchg = reinterpret_cast<v4i*>(smem);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-        __syncthreads();                        // rings (or the previous half) no longer read
+        __syncthreads();
         if (team == 1) {
 #pragma unroll
             for (int a = 0; a < TN; ++a)
@@ -702,7 +755,7 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_splitk_kernel(
                     acc[a][h * (TM / 2) + bb] += xchg[((wt * TN + a) * (TM / 2) + bb) * 64 + lane];
         }
     }
-    __syncthreads();                            // exchange buffer free
+    __syncthreads();
     if (team == 0)
         staged_epilogue<TM, TN, WN, Epi>(epi, acc, smem + wt * (32 * 256), m0 + wm * WM,
                                          n0 + wn * WN, M, N, lane);
@@ -711,13 +764,14 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_splitk_kernel(
 template <class Epi>
 hipError_t launch_splitk(hipStream_t st, const int8_t* X, int64_t ldx, const int8_t* W,
                          int64_t ldw, int M, int N, int K, const Epi& epi) {
+    constexpr int S = 4;                        // 2 x 4 x 18 KB of LDS
     const int tm = (M + 127) / 128, tn = (N + 159) / 160;
     if (K % 64 == 0)
-        hipLaunchKernelGGL((gemm_i8_splitk_kernel<false, Epi>), dim3(unsigned(tm * tn)), dim3(512),
-                           0, st, X, ldx, W, ldw, M, N, K, tm, tn, epi);
+        hipLaunchKernelGGL((gemm_i8_splitk_kernel<S, false, Epi>), dim3(unsigned(tm * tn)),
+                           dim3(512), 0, st, X, ldx, W, ldw, M, N, K, tm, tn, epi);
     else
-        hipLaunchKernelGGL((gemm_i8_splitk_kernel<true, Epi>), dim3(unsigned(tm * tn)), dim3(512),
-                           0, st, X, ldx, W, ldw, M, N, K, tm, tn, epi);
+        hipLaunchKernelGGL((gemm_i8_splitk_kernel<S, true, Epi>), dim3(unsigned(tm * tn)),
+                           dim3(512), 0, st, X, ldx, W, ldw, M, N, K, tm, tn, epi);
     return hipGetLastError();
 }
 
