@@ -63,8 +63,10 @@ def selftest(verbose: bool = True) -> bool:
 
     dy = rnd(M, N, s=0.5)
     q_f, s_f = quantize_row(dy)
-    q_c, s_c = quantize_row_torch(dy)
-    rowq_same = q_f.equal(q_c) and s_f.view(torch.int32).equal(s_c.view(torch.int32))
+    # the torch chain on the CPU: its scalar division is correctly rounded
+    # there (ROCm's GPU division is not, so on the device it agrees to +-1)
+    q_c, s_c = quantize_row_torch(dy.cpu())
+    rowq_same = q_f.cpu().equal(q_c) and s_f.cpu().view(torch.int32).equal(s_c.view(torch.int32))
     deq_same = dequant_weight(w8, ws).view(torch.int16).equal(
         dequant_weight_torch(w8, ws).view(torch.int16))
     xr = x.detach().float().requires_grad_(True)
@@ -83,7 +85,7 @@ def selftest(verbose: bool = True) -> bool:
               f"(GELU: the build's exact table vs torch's erf may differ in a few bf16 "
               f"values below -3)")
         print(f"GEGLU FFN == chain through int_mm: {ffn_same}")
-        print(f"quantize_row == torch chain: {rowq_same}")
+        print(f"quantize_row == torch chain (CPU): {rowq_same}")
         print(f"dequant_weight == torch chain: {deq_same}")
         print(f"dx (int8 weight) vs fp32 autograd: rel {dx_rel:.4f} (expect < 0.04)")
         print("PASS" if ok else "FAIL")
