@@ -246,6 +246,27 @@ def main():
         log(f"[bench] config 5: dx {ms_dx:.4f} ms, dW {ms_dw:.4f} ms, quantize_row {ms_rq:.4f} ms, "
             f"skinny {ms_sk:.4f} ms")
 
+        # ------------------------------------ accumulator consumer: rms + rope
+        # q slice [1, 4096, 24, 128] of a qkv accumulator [4096, 3*3072]
+        from xpu_kernels import rope
+        S_r, H_r, D_r = 4096, 24, 128
+        g_r = torch.Generator().manual_seed(12)
+        acc_r = torch.randint(-2 ** 17, 2 ** 17, (1, S_r, 3 * H_r * D_r), generator=g_r,
+                              dtype=torch.int32).to(dev)
+        q_acc = acc_r[..., : H_r * D_r].unflatten(-1, (H_r, D_r))
+        xs_r = (torch.rand(1, S_r, generator=g_r) * 0.05).to(dev)
+        ws_r = (torch.rand(H_r * D_r, generator=g_r) * 1e-4).to(dev)
+        th = torch.rand(1, S_r, 1, D_r // 2, generator=g_r) * 6.28
+        f_r = torch.stack([torch.stack([th.cos(), -th.sin()], -1),
+                           torch.stack([th.sin(), th.cos()], -1)], -2).to(dev)
+        sc_r = torch.ones(D_r, device=dev)
+        ms_rope = timed(torch, lambda: rope.rows_dq(q_acc, f_r, sc_r, 1e-6, xs_r, ws_r), K, W)
+        bytes_rope = S_r * H_r * D_r * (4 + 2) + 4 * S_r + 4 * H_r * D_r
+        extra["rms_rope_dequant_s4096_h24_d128"] = {
+            "ms": round(ms_rope, 5), "GB/s": round(bytes_rope / (ms_rope * 1e-3) / 1e9, 1),
+            "frac_hbm_peak": round(bytes_rope / (ms_rope * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4)}
+        log(f"[bench] rms+rope dequant: {ms_rope:.4f} ms")
+
     line = {
         "metric": "int8_linear TOPS (M=4096,K=1280,N=10240); rotate+quant HBM GB/s",
         "value": round(value, 2),

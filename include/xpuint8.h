@@ -176,6 +176,28 @@ int xpuint8_quantize_row_stream(const void *stream, const void *x, const float *
 int xpuint8_linear_dw_stream(const void *stream, const void *dy, const void *x, void *dw,
                              int64_t M, int64_t N, int64_t K);
 
+/* RMSNorm + rotary embedding of q or k read straight from the int32
+ * accumulator of a quantized qkv projection (one [B,S,H,D] slice of it):
+ *   x = bf16(float(acc) * (w_scale[h*D+d] * x_scale[b,s])),
+ *   y = bf16(x * rsqrt(mean_d(x^2) + epsilon) * scale[d]),
+ *   out = the pairwise rotation of y by freqs_cis (fp32 [FB,FS,1,D/2,2,2],
+ *         FB in {1,B}, FS in {1,S}), pairs (p, p+D/2) when split_half else
+ *         (2p, 2p+1); out bf16 [B,S,H,D] contiguous.
+ * acc's head dim is contiguous (element strides given for b, s, h); x_scale is
+ * [B,S] with the given strides; w_scale fp32 [H*D]; scale fp32 [D]; D even,
+ * 2 <= D <= 256.  Replaces the Triton _rms_rope_rows_dq_kernel behind
+ * rms_rope_split_half_dequant (python/xpu_kernels/triton/rope.py:149-222,
+ * 378-405, 643-652). */
+int xpuint8_rms_rope_dequant_stream(const void *stream, const int32_t *acc, int64_t acc_stride_b,
+                                    int64_t acc_stride_s, int64_t acc_stride_h,
+                                    const float *x_scale, int64_t xs_stride_b,
+                                    int64_t xs_stride_s, const float *w_scale, const float *freqs,
+                                    int64_t f_stride_b, int64_t f_stride_s, int64_t f_stride_dim,
+                                    int64_t f_stride_rot, int64_t f_stride_pair, int64_t f_batch,
+                                    int64_t f_seq, const float *scale, void *out, int64_t B,
+                                    int64_t S, int64_t H, int64_t D, float epsilon,
+                                    int32_t split_half);
+
 /* Host copy of an activation table (65536 bf16 entries indexed by the bf16
  * bit pattern of the input): 0 gelu_erf, 1 gelu_tanh, 2 silu, 3 situ's
  * tanh(bf16(x/4)), 4 sigmoid, 5 situ's tanh(bf16(x/25)).  No device needed.

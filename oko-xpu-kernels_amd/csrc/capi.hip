@@ -367,6 +367,34 @@ int xpuint8_linear_dw_stream(const void* stream, const void* dy, const void* x, 
                     "linear_dw");
 }
 
+// ------------------------------------------------------------- rms + rope
+int xpuint8_rms_rope_dequant_stream(const void* stream, const int32_t* acc, int64_t acc_stride_b,
+                                    int64_t acc_stride_s, int64_t acc_stride_h,
+                                    const float* x_scale, int64_t xs_stride_b,
+                                    int64_t xs_stride_s, const float* w_scale, const float* freqs,
+                                    int64_t f_stride_b, int64_t f_stride_s, int64_t f_stride_dim,
+                                    int64_t f_stride_rot, int64_t f_stride_pair, int64_t f_batch,
+                                    int64_t f_seq, const float* scale, void* out, int64_t B,
+                                    int64_t S, int64_t H, int64_t D, float epsilon,
+                                    int32_t split_half) {
+    if (B <= 0 || S <= 0 || H <= 0) return fail(2, "B, S and H must be positive");
+    if (D < 2 || D > 256 || D % 2 != 0) return fail(2, "D must be even and in [2, 256]");
+    if (B * S > kMaxDim || H * D > kMaxDim || B * S * H > kMaxDim)
+        return fail(4, "B*S*H rows must be < 2^31");
+    if (f_batch != 1 && f_batch != B) return fail(2, "freqs_cis batch must be 1 or B");
+    if (f_seq != 1 && f_seq != S) return fail(2, "freqs_cis sequence length must be 1 or S");
+    if (!(epsilon >= 0.0f)) return fail(2, "epsilon must be >= 0");
+    XPU_NONNULL(acc); XPU_NONNULL(x_scale); XPU_NONNULL(w_scale); XPU_NONNULL(freqs);
+    XPU_NONNULL(scale); XPU_NONNULL(out);
+    XPU_TRY(ensure_device());
+    return launched(rms_rope_dequant(as_stream(stream), acc, acc_stride_b, acc_stride_s,
+                                     acc_stride_h, x_scale, xs_stride_b, xs_stride_s, w_scale,
+                                     freqs, f_stride_b, f_stride_s, f_stride_dim, f_stride_rot,
+                                     f_stride_pair, f_batch, f_seq, scale, out, B, S, int(H),
+                                     int(D), epsilon, split_half != 0),
+                    "rms_rope_dequant");
+}
+
 // ------------------------------------------------------ prepare / row quant
 int xpuint8_prepare_weight_stream(const void* stream, const void* w, int8_t* q, float* scale,
                                   int64_t N, int64_t K) {

@@ -42,6 +42,14 @@ hipError_t transpose_i8(hipStream_t st, const int8_t* in, int8_t* out, int64_t R
 hipError_t gemm_bf16_tn(hipStream_t st, const void* dy, int64_t ldy, const void* x, int64_t ldx,
                         void* dw, int64_t ldo, int R, int N, int K);
 
+// rope.hip: RMSNorm + rotary embedding of an int32 accumulator slice
+hipError_t rms_rope_dequant(hipStream_t st, const int32_t* acc, int64_t a_sb, int64_t a_ss,
+                            int64_t a_sh, const float* xs, int64_t xs_sb, int64_t xs_ss,
+                            const float* ws, const float* freqs, int64_t f_sb, int64_t f_ss,
+                            int64_t f_sdim, int64_t f_srot, int64_t f_spair, int64_t f_batch,
+                            int64_t f_seq, const float* scale, void* out, int64_t B, int64_t S,
+                            int H, int D, float eps, int split_half);
+
 // capi.hip: compute units of the current device (persistent grids)
 int device_cus();
 

@@ -19,8 +19,10 @@ from .convrot import *  # noqa: F401,F403
 from .convrot import __all__ as _convrot_all
 from .activations import *  # noqa: F401,F403
 from .activations import __all__ as _act_all
+from .rope import *  # noqa: F401,F403
+from .rope import __all__ as _rope_all
 
-__all__ = list(_convrot_all) + list(_act_all)
+__all__ = list(_convrot_all) + list(_act_all) + list(_rope_all)
 
 #: function -> the independent checks that pin it (tests/test_oracle_*.py)
 PINNING = {
@@ -53,4 +55,9 @@ PINNING = {
     "dequant_act / dequant_act_quantize": "torch chain bf16(acc*(ws*xs)) then the "
                                           "activation; quantize of it on equal rows",
     "ffn": "float64 down(geglu(up(x)))+b with the unquantized weights",
+    "rms_rope_dequant / rms_rope_bf16": "float64 closed forms: identity rotation gives "
+                                        "x/rms(x)*scale; a constant row gives +-1; a pair "
+                                        "(1, 1) rotated by theta gives (cos-sin, sin+cos); "
+                                        "the rotation keeps each pair's norm; split-half and "
+                                        "interleaved agree under the dim permutation",
 }
