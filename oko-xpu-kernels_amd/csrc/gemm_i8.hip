@@ -353,20 +353,22 @@ __global__ __launch_bounds__(WGM * WGN * 64) void gemm_i8_kernel(
 }
 
 // The staged epilogue of one wave: its TM x TN blocks of results (output
-// rows m0w.., columns n0w..), 32 rows per pass through `stg` (8 KB of idle
-// LDS): 256-byte rows of 16-byte chunks, chunk c of row r at c ^ (r & 15),
-// each row leaving as contiguous 16-byte stores.  Row and column operands are
-// loaded before any conversion so their latency is paid once.  Paired
-// epilogues take the (first, second) accumulator pairs (2a, 2a+1).
-template <int TM, int TN, int WN_OUT, class Epi>
+// rows m0w.., columns n0w..), RB row blocks (16*RB rows) per pass through
+// `stg` (RB * 4 KB of idle LDS): 256-byte rows of 16-byte chunks, chunk c of
+// row r at c ^ (r & 15), each row leaving as contiguous 16-byte stores.  Row
+// and column operands are loaded before any conversion so their latency is
+// paid once.  Paired epilogues take the (first, second) accumulator pairs
+// (2a, 2a+1).
+template <int TM, int TN, int WN_OUT, class Epi, int RB = 2>
 __device__ __forceinline__ void staged_epilogue(const Epi& epi, v4i (&acc)[TN][TM], int8_t* stg,
                                                 int m0w, int n0w, int M, int N, int lane) {
     constexpr bool PAIRED = Epi::kPaired;
     constexpr int OUT_TN = PAIRED ? TN / 2 : TN;
-    constexpr int STG_ROWS = 32;
+    constexpr int STG_ROWS = 16 * RB;
     constexpr int CH = WN_OUT / 8;                                 // live chunks per row
-    static_assert(CH <= 16 && (STG_ROWS * CH) % 64 == 0, "staging shape");
-    static_assert(TM % 2 == 0, "epilogue passes of 32 rows");
+    constexpr int ITEMS = STG_ROWS * CH;
+    static_assert(CH <= 16, "staging shape");
+    static_assert(TM % RB == 0, "whole passes");
     float xrow[TM];
     typename Epi::Col ccol[TN];
 #pragma unroll
@@ -380,10 +382,10 @@ __device__ __forceinline__ void staged_epilogue(const Epi& epi, v4i (&acc)[TN][T
             ccol[a] = epi.col(min(n0w + 16 * a + 4 * (lane >> 4), N - 4));
     }
 #pragma unroll
-    for (int pass = 0; pass < TM / 2; ++pass) {
+    for (int pass = 0; pass < TM / RB; ++pass) {
 #pragma unroll
-        for (int bb = 0; bb < 2; ++bb) {
-            const int b = 2 * pass + bb;
+        for (int bb = 0; bb < RB; ++bb) {
+            const int b = RB * pass + bb;
             const int r = 16 * bb + (lane & 15);
 #pragma unroll
             for (int a = 0; a < OUT_TN; ++a) {
@@ -400,12 +402,14 @@ __device__ __forceinline__ void staged_epilogue(const Epi& epi, v4i (&acc)[TN][T
         }
         __builtin_amdgcn_s_waitcnt(0xC07F);                       // lgkmcnt(0)
 #pragma unroll
-        for (int i = 0; i < (STG_ROWS * CH) / 64; ++i) {
+        for (int i = 0; i < (ITEMS + 63) / 64; ++i) {
             const int flat = i * 64 + lane;
             const int r = flat / CH, c = flat % CH;
-            const uint4 v = *reinterpret_cast<const uint4*>(stg + r * 256 + ((c ^ (r & 15)) << 4));
-            const int m = m0w + 32 * pass + r, n = n0w + 8 * c;
-            if (m < M && n < N) epi.store16(m, n, v);
+            if (ITEMS % 64 == 0 || flat < ITEMS) {
+                const uint4 v = *reinterpret_cast<const uint4*>(stg + r * 256 + ((c ^ (r & 15)) << 4));
+                const int m = m0w + STG_ROWS * pass + r, n = n0w + 8 * c;
+                if (m < M && n < N) epi.store16(m, n, v);
+            }
         }
         __builtin_amdgcn_s_waitcnt(0xC07F);                       // reads done before reuse
     }
@@ -935,31 +939,67 @@ __global__ __launch_bounds__(256) void dequant_kernel(const int32_t* __restrict_
 }
 
 // ------------------------------------------------------------ int8 transpose
-// out[c, r] = in[r, c] (R, C multiples of 4).  Each thread moves one 4 x 4
-// byte block: four dword loads of rows r..r+3, a register transpose with
-// byte permutes, four dword stores to rows c..c+3 of the output.  A block of
-// 256 threads covers 64 x 64 bytes; 16 threads share each 64-byte row
-// segment on both sides.
-__global__ __launch_bounds__(256) void transpose_i8_kernel(const int8_t* __restrict__ in,
-                                                          int8_t* __restrict__ out, int64_t R,
-                                                          int64_t C) {
-    const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
-    const int64_t r = int64_t(blockIdx.y) * 64 + 4 * ty, c = int64_t(blockIdx.x) * 64 + 4 * tx;
-    if (r >= R || c >= C) return;
-    uint32_t w[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) w[i] = *reinterpret_cast<const uint32_t*>(in + (r + i) * C + c);
-    // w[i] = bytes (row r+i, columns c..c+3); o[j] = bytes (column c+j, rows r..r+3)
+// out[c, r] = in[r, c] (R, C multiples of 16), through a 128 x 128 byte LDS
+// tile per block of 256 threads:
+//  * in: each thread loads four 16-byte chunks (rows t/8 + 32i, chunk t%8), so
+//    8 lanes cover a whole 128-byte row segment;
+//  * LDS: row r's 16-byte chunk k sits at slot k ^ ((r / 16) % 8);
+//  * out: thread t owns input rows 16*(t%8) .. +15 of input columns
+//    4*(t/8) .. +3: sixteen dword reads, a 4 x 4 byte register transpose per
+//    four rows, and four 16-byte stores, 8 lanes per 128-byte output segment.
+// Tiles past R or C are masked per 16-byte chunk.
+__device__ __forceinline__ void transpose4x4(const uint32_t (&w)[4], uint32_t (&o)[4]) {
+    // w[i] = bytes (row i, columns 0..3); o[j] = bytes (column j, rows 0..3)
     const uint32_t lo01 = __builtin_amdgcn_perm(w[1], w[0], 0x05010400u);
     const uint32_t hi01 = __builtin_amdgcn_perm(w[1], w[0], 0x07030602u);
     const uint32_t lo23 = __builtin_amdgcn_perm(w[3], w[2], 0x05010400u);
     const uint32_t hi23 = __builtin_amdgcn_perm(w[3], w[2], 0x07030602u);
-    const uint32_t o[4] = {__builtin_amdgcn_perm(lo23, lo01, 0x05040100u),
-                           __builtin_amdgcn_perm(lo23, lo01, 0x07060302u),
-                           __builtin_amdgcn_perm(hi23, hi01, 0x05040100u),
-                           __builtin_amdgcn_perm(hi23, hi01, 0x07060302u)};
+    o[0] = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u);
+    o[1] = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u);
+    o[2] = __builtin_amdgcn_perm(hi23, hi01, 0x05040100u);
+    o[3] = __builtin_amdgcn_perm(hi23, hi01, 0x07060302u);
+}
+
+__global__ __launch_bounds__(256) void transpose_i8_kernel(const int8_t* __restrict__ in,
+                                                          int8_t* __restrict__ out, int64_t R,
+                                                          int64_t C) {
+    __shared__ __attribute__((aligned(16))) uint8_t tile[128 * 128];
+    const int t = threadIdx.x;
+    const int64_t r0 = int64_t(blockIdx.y) * 128, c0 = int64_t(blockIdx.x) * 128;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) *reinterpret_cast<uint32_t*>(out + (c + j) * R + r) = o[j];
+    for (int i = 0; i < 4; ++i) {
+        const int row = 32 * i + (t >> 3), k = t & 7;
+        const int64_t r = r0 + row, c = c0 + 16 * k;
+        uint4 v = make_uint4(0u, 0u, 0u, 0u);
+        if (r < R && c < C) v = *reinterpret_cast<const uint4*>(in + r * C + c);
+        *reinterpret_cast<uint4*>(tile + row * 128 + ((k ^ ((row >> 4) & 7)) << 4)) = v;
+    }
+    __syncthreads();
+    const int rg = t & 7, cg = t >> 3;                 // rows 16rg.., columns 4cg..
+    uint32_t col[4][4];                                // [output column j][row quad q]
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        uint32_t w[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = 16 * rg + 4 * q + i;
+            const int k = cg >> 2;                      // 16-byte chunk of column 4cg
+            w[i] = *reinterpret_cast<const uint32_t*>(tile + row * 128 + ((k ^ rg) << 4) +
+                                                      (cg & 3) * 4);
+        }
+        uint32_t o[4];
+        transpose4x4(w, o);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) col[j][q] = o[j];
+    }
+    const int64_t r = r0 + 16 * rg;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int64_t c = c0 + 4 * cg + j;
+        if (c < C && r < R)
+            *reinterpret_cast<uint4*>(out + c * R + r) =
+                make_uint4(col[j][0], col[j][1], col[j][2], col[j][3]);
+    }
 }
 
 }  // namespace
@@ -1001,7 +1041,7 @@ hipError_t dequant_epilogue(hipStream_t st, const int32_t* acc, int64_t acc_ld, 
 }
 
 hipError_t transpose_i8(hipStream_t st, const int8_t* in, int8_t* out, int64_t R, int64_t C) {
-    const dim3 grid(unsigned((C + 63) / 64), unsigned((R + 63) / 64));
+    const dim3 grid(unsigned((C + 127) / 128), unsigned((R + 127) / 128));
     hipLaunchKernelGGL(transpose_i8_kernel, grid, dim3(256), 0, st, in, out, R, C);
     return hipGetLastError();
 }
