@@ -39,17 +39,21 @@ __device__ __forceinline__ float bf16lo(uint32_t w) { return __uint_as_float(w <
 __device__ __forceinline__ float bf16hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float(uint32_t(b) << 16); }
 
-// fp32 -> bf16 bits, round to nearest even, NaN kept quiet (torch's conversion).
+// fp32 -> bf16, round to nearest even, NaN kept quiet with its sign (torch's
+// conversion: (u >> 16) | 0x40 for a NaN).  gfx950's v_cvt_pk_bf16_f32 gives
+// exactly these bits for every one of the 2^32 fp32 inputs (denormals, infinities
+// and NaNs included; checked exhaustively on the device against the integer
+// formula), so one instruction converts two values.
+typedef float xpu_v2f __attribute__((ext_vector_type(2)));
+typedef __bf16 xpu_v2bf __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(xpu_v2f{lo, hi}, xpu_v2bf));
+}
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (u >> 16) | 0x40u;
-    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+    return pack_bf16x2(f, 0.f) & 0xFFFFu;
 }
 __device__ __forceinline__ float bf16_round(float f) {
-    return __uint_as_float(f32_to_bf16_bits(f) << 16);
-}
-__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-    return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+    return __uint_as_float(pack_bf16x2(f, 0.f) << 16);
 }
 
 // ------------------------------------------------------------ lane exchange
