@@ -175,6 +175,29 @@ def test_quantize_row_column_scaled(dev):
 
 
 # ------------------------------------------------------------- epilogues
+def test_dequant_rounding_edge_cases(dev):
+    """The bf16 conversion at its edges, through the dequant epilogue: exact
+    ties (acc = 2^8 + odd, unit scales: RNE to even), values past the bf16
+    maximum (round to inf), fp32 denormal results, infinities and NaNs of
+    either sign in the column scale (quiet NaN with the sign kept)."""
+    rng = np.random.default_rng(5)
+    n = 64
+    ties = np.array([257, 259, 261, 263, -257, -259, 513, 515], np.int32)
+    acc = np.stack([np.resize(ties, n),
+                    rng.integers(-2 ** 30, 2 ** 30, n),
+                    rng.integers(-2 ** 20, 2 ** 20, n),
+                    rng.integers(1, 2 ** 8, n)]).astype(np.int32)
+    xs = np.array([1.0, 2.0 ** 100, 2.0 ** -120, 1.0], np.float32)
+    ws = np.ones(n, np.float32)
+    ws[8:16] = 2.0 ** 27                     # row 1: |acc| * 2^127 -> past bf16 max
+    ws[16:24] = np.float32(3.0e-8)           # row 2: denormal products
+    ws[24:28] = [np.inf, -np.inf, np.nan, -np.nan]
+    t = lambda a: torch.from_numpy(a).to(dev)
+    got = bits(int8.dequant(t(acc), t(xs), t(ws)))
+    want = O.dequant(acc, xs, ws)
+    assert np.array_equal(got, want), mismatch(got, want)
+
+
 @pytest.mark.parametrize("bias", [False, True])
 def test_dequant_and_slice_exact(dev, bias):
     rng = np.random.default_rng(2)
