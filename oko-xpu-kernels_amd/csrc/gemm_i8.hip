@@ -592,6 +592,193 @@ hipError_t launch_cfg(hipStream_t st, const int8_t* X, int64_t ldx, const int8_t
     return hipGetLastError();
 }
 
+// ------------------------------------------------------------ ping-pong
+// A BM x BN tile (256 x 320) per block of 8 waves in two groups of 4 (group =
+// the tile's row half, 2 x 4 waves of 128 x 80), one block per CU, a ring of S
+// LDS stages of 64-byte K steps filled by direct global->LDS loads.  The
+// groups alternate roles every half step, so that on each SIMD one wave feeds
+// the matrix core while the other moves data:
+//   phase A(k): group 0 runs step k's MFMAs;  group 1 reads step k's
+//               fragments and issues its loads for step k + S - 1
+//   phase B(k): group 1 runs step k's MFMAs;  group 0 reads step k + 1's
+//               fragments and issues its loads for step k + S - 1
+// with one s_barrier between phases.  Step j's loads are complete (each wave
+// waits for its own, then the barrier) before phase B(j - 1), the first
+// reader of stage j % S; stage j % S is refilled (for step j + S) only from
+// phase A(j + 1) on, after its last reader, A(j).  The larger tile halves the
+// operand bytes per MFMA of the two-block 256 x 160 kernel, and the
+// alternation keeps the matrix core fed while the loads go out.
+template <int BM, int BN, int S, bool KTAIL, class Epi>
+__global__ __launch_bounds__(512, 1) void gemm_i8_pp_kernel(
+    const int8_t* __restrict__ X, int64_t ldx, const int8_t* __restrict__ W, int64_t ldw, int M,
+    int N, int K, int tiles_m, int tiles_n, Epi epi) {
+    constexpr int WGM = 2, WGN = 4, NW = 8;
+    constexpr int BK = 64;
+    constexpr int WM = BM / WGM, WN = BN / WGN, TM = WM / 16, TN = WN / 16;
+    constexpr int XB = BM / 16, WB = BN / 16, NB = XB + WB;
+    constexpr int PER = (NB + NW - 1) / NW;                     // loads per wave per step (max)
+    constexpr int REM = NB % NW;                                // waves < REM issue PER
+    static_assert(REM == 0 || REM == 4, "group 0 issues PER, group 1 PER or PER - 1");
+    constexpr int PER0 = PER, PER1 = REM == 0 ? PER : PER - 1;
+    constexpr int STAGE_BYTES = NB * 1024;
+    constexpr int RING = S * STAGE_BYTES;
+    static_assert(S >= 3, "three or more stages");
+    static_assert(!Epi::kStaged || NW * 32 * 256 <= RING, "staging fits in the ring");
+    static_assert(TM % 2 == 0, "epilogue passes of 32 rows");
+    constexpr bool PAIRED = Epi::kPaired;
+    static_assert(!PAIRED || (Epi::kStaged && TN % 2 == 0), "pairs are whole per wave");
+    constexpr int OUT_TN = PAIRED ? TN / 2 : TN;
+    constexpr int WN_OUT = 16 * OUT_TN, BN_OUT = WN_OUT * WGN;
+    __shared__ __attribute__((aligned(1024))) int8_t smem[RING];
+
+    const int tiles = tiles_m * tiles_n;
+    int t = blockIdx.x;
+    if (tiles % 8 == 0) t = (t % 8) * (tiles / 8) + t / 8;
+    constexpr int GROUP = 8;
+    const int band = t / (GROUP * tiles_n);
+    const int first_m = band * GROUP;
+    const int gm = min(tiles_m - first_m, GROUP);
+    const int in_band = t - band * GROUP * tiles_n;
+    const int m0 = (first_m + in_band % gm) * BM, n0 = (in_band / gm) * BN_OUT;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave / WGN, wn = wave % WGN;
+    const int g = wm;                                           // group
+
+    const int lr = lane >> 2;
+    const int lc = swz(lr, lane & 3) * 16;
+    const int8_t* const xbase = X + int64_t(m0) * ldx;
+    const int8_t* const wbase = W + int64_t(n0) * ldw;
+    const int8_t* const gbase = W + (int64_t(pair_offset(epi)) + n0) * ldw;
+    const int8_t* base[PER];
+    int off[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const int j = min(wave + NW * i, NB - 1);
+        if (j < XB) {
+            base[i] = xbase;
+            off[i] = (min(m0 + 16 * j + lr, M - 1) - m0) * int(ldx) + lc;
+        } else if constexpr (PAIRED) {
+            const int jw = j - XB;
+            base[i] = (jw & 1) ? gbase : wbase;
+            off[i] = (min(n0 + 16 * (jw >> 1) + lr, N - 1) - n0) * int(ldw) + lc;
+        } else {
+            base[i] = wbase;
+            off[i] = (min(n0 + 16 * (j - XB) + lr, N - 1) - n0) * int(ldw) + lc;
+        }
+    }
+    const int KT = (K + BK - 1) / BK;
+    // this wave's loads for step kk (its share of the stage's blocks)
+    auto issue = [&](int kk) {
+        const int k0 = kk * BK;
+        int8_t* const st = smem + (kk % S) * STAGE_BYTES;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            if (i == PER - 1 && REM != 0 && g != 0) continue;
+            const int8_t* p = base[i] + uint64_t(uint32_t(off[i] + k0));
+            if (KTAIL && k0 + lc >= K) p = g_zero16;
+            dma16(p, st + (wave + NW * i) * 1024);
+        }
+    };
+    // wait until this wave's loads of every step before `later` more of its
+    // own load batches are complete
+    auto wait_batches = [&](int later) {
+        if (g == 0) {
+            if (later >= 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * PER0));
+            else if (later == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(PER0));
+            else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        } else {
+            if (later >= 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * PER1));
+            else if (later == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(PER1));
+            else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        }
+    };
+    static_assert(S <= 4, "wait_batches covers up to two later batches");
+
+    const int frag = (lane & 15) * 64 + swz(lane & 15, lane >> 4) * 16;
+    const int xoff = (wm * TM) * 1024 + frag;
+    const int woff = (XB + wn * TN) * 1024 + frag;
+    const uint32_t sbase = lds_addr(smem);
+
+    v4i acc[TN][TM];
+#pragma unroll
+    for (int a = 0; a < TN; ++a)
+#pragma unroll
+        for (int b = 0; b < TM; ++b) acc[a][b] = v4i{0, 0, 0, 0};
+    v4i wf[TN], xf[TM];
+    auto read_frags = [&](int kk) {
+        const uint32_t sb = sbase + (kk % S) * STAGE_BYTES;
+#pragma unroll
+        for (int i = 0; i < TN; ++i) wf[i] = lds_read16(sb + woff + i * 1024);
+#pragma unroll
+        for (int i = 0; i < TM; ++i) xf[i] = lds_read16(sb + xoff + i * 1024);
+    };
+    auto compute = [&]() {
+        __builtin_amdgcn_s_waitcnt(0xC07F);                     // lgkmcnt(0): fragments in
+#pragma unroll
+        for (int b = 0; b < TM; ++b)
+#pragma unroll
+            for (int a = 0; a < TN; ++a)
+                acc[a][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[a], xf[b], acc[a][b], 0, 0, 0);
+    };
+    auto barrier = [&]() {
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    // prologue: steps 0 .. S-2 requested by every wave; step 0 complete;
+    // group 0 reads step 0's fragments.  Each group then runs its own loop of
+    // (first half, barrier, second half, barrier), group 0 a half step ahead.
+    for (int kk = 0; kk < S - 1; ++kk)
+        if (kk < KT) issue(kk);
+    wait_batches(min(S - 2, KT - 1));
+    barrier();
+    if (g == 0) {
+        read_frags(0);
+        barrier();
+#pragma clang loop unroll(disable)
+        for (int k = 0; k < KT; ++k) {
+            compute();                                          // A(k)
+            if (k + 1 < KT) wait_batches(min(S - 3, KT - 2 - k));
+            barrier();
+            if (k + 1 < KT) read_frags(k + 1);                  // B(k)
+            if (k + S - 1 < KT) issue(k + S - 1);
+            barrier();
+        }
+    } else {
+        barrier();
+#pragma clang loop unroll(disable)
+        for (int k = 0; k < KT; ++k) {
+            read_frags(k);                                      // A(k)
+            if (k + S - 1 < KT) issue(k + S - 1);
+            if (k + 1 < KT) wait_batches(min(S - 2, KT - 2 - k));
+            barrier();
+            compute();                                          // B(k)
+            barrier();
+        }
+    }
+
+    if constexpr (Epi::kStaged) {
+        staged_epilogue<TM, TN, WN_OUT, Epi>(epi, acc, smem + wave * (32 * 256),
+                                             m0 + wm * WM, n0 + wn * WN_OUT, M, N, lane);
+    } else {
+        const int mrow = m0 + wm * WM + (lane & 15);
+        const int ncol = n0 + wn * WN + 4 * (lane >> 4);
+#pragma unroll
+        for (int b = 0; b < TM; ++b) {
+            const int m = mrow + 16 * b;
+            if (m >= M) continue;
+#pragma unroll
+            for (int a = 0; a < TN; ++a) {
+                const int n = ncol + 16 * a;
+                if (n < N) epi(m, n, acc[a][b]);
+            }
+        }
+    }
+}
+
 // ------------------------------------------------------------ split K
 // Narrow outputs with a long K (the FFN's down-projection, dx: N = 1280,
 // K = 5120) give too few large tiles to fill the chip.  Here a 128 x 160
@@ -855,9 +1042,10 @@ hipError_t launch_skinny(hipStream_t st, const int8_t* X, int64_t ldx, const int
     return hipGetLastError();
 }
 
-// Tile choice: the large tile (256 x 160, 4 waves of 128 x 80, two blocks per
-// CU, two LDS stages: the fastest of the 256x128/128x256/256x192/128x160
-// shapes and stage counts measured at M=4096, K=1280, N=10240) whenever it
+// Tile choice: the 256 x 320 ping-pong tile when it gives at least one tile
+// per CU (8-12% faster than the two-block 256 x 160 kernel at M=4096, K=1280
+// and 2560, N=5120 and 10240, interleaved A/B timing); else the large tile
+// (256 x 160, 4 waves of 128 x 80, two blocks per CU, two LDS stages) when it
 // gives at least 192 tiles; otherwise the small one (128 x 128, 4 waves of
 // 64 x 64, four stages); M <= 64 takes the weight-streaming skinny kernel;
 // a narrow output with K >= 2048 (too few large tiles) the split-K kernel.
@@ -886,6 +1074,19 @@ hipError_t launch_gemm(hipStream_t st, const int8_t* X, int64_t ldx, const int8_
             const int64_t tiles_split = int64_t((M + 127) / 128) * ((N + 159) / 160);
             if (int64_t(tm) * tn < 192 && K >= 2048 && tiles_split >= 128)
                 return launch_splitk(st, X, ldx, W, ldw, M, N, K, epi);
+        }
+        // one 256 x 320 ping-pong tile per CU when they fill every CU
+        const int tn_pp = (N + 319) / 320;
+        if (int64_t(tm) * tn_pp >= device_cus()) {
+            if (K % 64 == 0)
+                hipLaunchKernelGGL((gemm_i8_pp_kernel<256, 320, 4, false, Epi>),
+                                   dim3(unsigned(tm * tn_pp)), dim3(512), 0, st, X, ldx, W, ldw, M,
+                                   N, K, tm, tn_pp, epi);
+            else
+                hipLaunchKernelGGL((gemm_i8_pp_kernel<256, 320, 4, true, Epi>),
+                                   dim3(unsigned(tm * tn_pp)), dim3(512), 0, st, X, ldx, W, ldw, M,
+                                   N, K, tm, tn_pp, epi);
+            return hipGetLastError();
         }
         if (int64_t(tm) * tn >= 192) {
             if (K % 64 == 0)
