@@ -202,6 +202,20 @@ __device__ __forceinline__ void lgkm_wait(v4i& v) {
     asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(v) : "n"(N));
 }
 
+// Wait for every outstanding LDS read, tied to all of a step's fragments: the
+// one s_waitcnt comes first, then an empty volatile asm per fragment that
+// "redefines" it, so no use of any fragment (an MFMA) can be scheduled above
+// the wait.  (The inline-asm reads complete asynchronously, which the compiler
+// does not know: a plain s_waitcnt builtin lets it hoist MFMAs above the wait.)
+template <int TN, int TM>
+__device__ __forceinline__ void lgkm_wait_all(v4i (&wf)[TN], v4i (&xf)[TM]) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(wf[0]));
+#pragma unroll
+    for (int a = 1; a < TN; ++a) asm volatile("" : "+v"(wf[a]));
+#pragma unroll
+    for (int b = 0; b < TM; ++b) asm volatile("" : "+v"(xf[b]));
+}
+
 // Column b of the wave's MFMA blocks: wait for X fragment b (and, for b = 0,
 // every W fragment, which were read first), then TN MFMAs, then the step's
 // b-th global->LDS load for a later stage (after_column(b)), so the wave's
@@ -716,7 +730,7 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_pp_kernel(
         for (int i = 0; i < TM; ++i) xf[i] = lds_read16(sb + xoff + i * 1024);
     };
     auto compute = [&]() {
-        __builtin_amdgcn_s_waitcnt(0xC07F);                     // lgkmcnt(0): fragments in
+        lgkm_wait_all(wf, xf);                                  // fragments in
 #pragma unroll
         for (int b = 0; b < TM; ++b)
 #pragma unroll
@@ -884,7 +898,7 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_splitk_kernel(
         for (int i = 0; i < TM; ++i) xf[i] = lds_read16(sb + xoff + i * 1024);
     };
     auto compute = [&]() {
-        __builtin_amdgcn_s_waitcnt(0xC07F);                     // lgkmcnt(0)
+        lgkm_wait_all(wf, xf);                                  // fragments in
 #pragma unroll
         for (int b = 0; b < TM; ++b)
 #pragma unroll
