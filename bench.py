@@ -1,14 +1,15 @@
 #!/usr/bin/env python3
 """Benchmark of the ConvRot INT8 linear path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--settle S] [--no-cpu]
 
 A *step* is one ``xpu_kernels.int8.linear`` at config 3 of BASELINE.json
 (x bf16 [4096,1280] with 1% outlier channels x30, W prepared from bf16
 [10240,1280], bias bf16 [10240]): rotate+quantize of x, then the int8 MFMA
 GEMM with the dequant+bias epilogue fused into its store.  Inputs are resident
-in HBM before the timed region; W is prepared once, untimed.  W warm-up steps,
-then exactly K steps between two ``torch.cuda.synchronize()`` calls, timed with
+in HBM before the timed region; W is prepared once, untimed.  An untimed run-in
+of S seconds (default 0.25, so the GPU clock reaches its sustained level), W
+warm-up steps, then exactly K steps between two ``torch.cuda.synchronize()`` calls, timed with
 HIP events on the stream the kernels run on (torch's current stream).
 
 ``value`` is end-to-end TOP/s at config 3 (2*M*N*K = 107.37 GOP per step).
@@ -70,9 +71,29 @@ def weight(torch, n, k, seed=1, std=0.02):
     return (torch.randn(n, k, generator=g) * std).to(torch.bfloat16)
 
 
-def timed(torch, fn, steps, warmup):
+SETTLE_S = 0.25                  # untimed run-in per measurement, seconds (see settle())
+
+
+def settle(torch, fn, seconds):
+    """Run ``fn`` untimed for about ``seconds``.  The MI355X's shader clock
+    ramps up over the first tens of milliseconds of sustained load (measured
+    with s_memtime against s_memrealtime inside the GEMM: ~1.6 GHz after an
+    idle period, ~2.0 GHz after 30 ms of back-to-back launches on full-range
+    int8 data), so without a run-in a short timed region measures the ramp,
+    not the steady state a serving loop runs at."""
+    if seconds <= 0:
+        return
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end:
+        for _ in range(20):
+            fn()
+        torch.cuda.synchronize()
+
+
+def timed(torch, fn, steps, warmup, settle_s=0.0):
     """Average ms per call of ``fn`` over ``steps`` calls (HIP events on the
-    current stream, after ``warmup`` untimed calls)."""
+    current stream, after a ``settle_s`` run-in and ``warmup`` untimed calls)."""
+    settle(torch, fn, settle_s)
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -125,6 +146,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--settle", type=float, default=SETTLE_S,
+                    help="untimed run-in (seconds) before each measurement's warm-up, so the "
+                         "GPU clock has reached its sustained level (0 = none)")
     ap.add_argument("--only-main", action="store_true", help="config 3 only (for profiling)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run an elementwise int8 kernel over 256 MiB (reads and writes "
@@ -141,7 +165,7 @@ def main():
     if not int8.available():
         raise SystemExit(f"libxpuint8 unavailable: {L._ERR}")
     dev = torch.device("cuda", 0)
-    K, W = args.steps, args.warmup
+    K, W, SET = args.steps, args.warmup, args.settle
     if args.calibrate_copy:
         src = torch.ones(CALIB_BYTES, dtype=torch.int8, device=dev)
         dst = torch.empty_like(src)
@@ -157,7 +181,7 @@ def main():
     bias = weight(torch, 1, N, seed=2, std=0.01)[0].to(dev)
     ops3 = 2.0 * M * N * Kd
     log(f"[bench] config 3 linear {M}x{Kd}x{N}: {W} warm-up + {K} timed steps")
-    ms = timed(torch, lambda: int8.linear(x, w8, ws, bias), K, W)
+    ms = timed(torch, lambda: int8.linear(x, w8, ws, bias), K, W, SET)
     value = ops3 / (ms * 1e-3) / 1e12
 
     # the dominant kernel alone: the GEMM with the fused epilogue
@@ -168,9 +192,9 @@ def main():
     def gemm():
         lib.xpuint8_linear_gemm_stream(L._stream(dev), L._ptr(xq), L._ptr(xs), L._ptr(w8),
                                        L._ptr(ws), L._ptr(bias), 1, L._ptr(out), M, N, Kd)
-    ms_gemm = timed(torch, gemm, K, W)
+    ms_gemm = timed(torch, gemm, K, W, SET)
     gemm_tops = ops3 / (ms_gemm * 1e-3) / 1e12
-    ms_q3 = timed(torch, lambda: int8.quantize(x), K, W)
+    ms_q3 = timed(torch, lambda: int8.quantize(x), K, W, SET)
     log(f"[bench] step {ms:.4f} ms = {value:.1f} TOP/s; GEMM {ms_gemm:.4f} ms = "
         f"{gemm_tops:.1f} TOP/s; quantize {ms_q3:.4f} ms")
 
@@ -185,14 +209,14 @@ def main():
         q2 = torch.empty((4096, 5120), device=dev, dtype=torch.int8)
         s2 = torch.empty(4096, device=dev, dtype=torch.float32)
         ms_q = timed(torch, lambda: lib.xpuint8_convrot_quantize_stream(
-            st, L._ptr(x2), L._ptr(q2), L._ptr(s2), 4096, 5120), K, W)
-        ms_q_api = timed(torch, lambda: int8.quantize(x2), K, W)
+            st, L._ptr(x2), L._ptr(q2), L._ptr(s2), 4096, 5120), K, W, SET)
+        ms_q_api = timed(torch, lambda: int8.quantize(x2), K, W, SET)
         bytes_q = 2 * 4096 * 5120 + 4096 * 5120 + 4 * 4096
         w2 = weight(torch, 10240, 1280).to(dev)
         q2w = torch.empty((10240, 1280), device=dev, dtype=torch.int8)
         s2w = torch.empty(10240, device=dev, dtype=torch.float32)
         ms_p = timed(torch, lambda: lib.xpuint8_prepare_weight_stream(
-            st, L._ptr(w2), L._ptr(q2w), L._ptr(s2w), 10240, 1280), K, W)
+            st, L._ptr(w2), L._ptr(q2w), L._ptr(s2w), 10240, 1280), K, W, SET)
         bytes_p = 3 * 10240 * 1280 + 4 * 10240
         extra["config2_rotate_quant"] = {
             "ms": round(ms_q, 5), "GB/s": round(bytes_q / (ms_q * 1e-3) / 1e9, 1),
@@ -208,7 +232,7 @@ def main():
         up8, ups = int8.prepare_weight(weight(torch, 10240, 1280, seed=4).to(dev))
         dn8, dns = int8.prepare_weight(weight(torch, 1280, 5120, seed=5).to(dev))
         db = weight(torch, 1, 1280, seed=6, std=0.01)[0].to(dev)
-        ms_f = timed(torch, lambda: int8.ffn(xf, up8, ups, dn8, dns, db, act="geglu_erf"), K, W)
+        ms_f = timed(torch, lambda: int8.ffn(xf, up8, ups, dn8, dns, db, act="geglu_erf"), K, W, SET)
         ops4 = 2.0 * 4096 * 1280 * 10240 + 2.0 * 4096 * 5120 * 1280
         extra["config4_ffn"] = {"ms": round(ms_f, 5), "TOP/s": round(ops4 / (ms_f * 1e-3) / 1e12, 1)}
         log(f"[bench] config 4: ffn {ms_f:.4f} ms")
@@ -217,12 +241,12 @@ def main():
         dy = (torch.randn(4096, 5120, generator=torch.Generator().manual_seed(8)) * 1e-3
               ).to(torch.bfloat16).to(dev)
         x5 = activation(torch, 4096, 1280, seed=9).to(dev)
-        ms_dx = timed(torch, lambda: int8.linear_dx_int8(dy, w5_8, w5_s), K, W)
-        ms_dw = timed(torch, lambda: int8.linear_dw(dy, x5), K, W)
+        ms_dx = timed(torch, lambda: int8.linear_dx_int8(dy, w5_8, w5_s), K, W, SET)
+        ms_dw = timed(torch, lambda: int8.linear_dw(dy, x5), K, W, SET)
         q5 = torch.empty((4096, 5120), device=dev, dtype=torch.int8)
         s5 = torch.empty(4096, device=dev, dtype=torch.float32)
         ms_rq = timed(torch, lambda: lib.xpuint8_quantize_row_stream(
-            st, L._ptr(dy), L._ptr(w5_s), L._ptr(q5), L._ptr(s5), 4096, 5120), K, W)
+            st, L._ptr(dy), L._ptr(w5_s), L._ptr(q5), L._ptr(s5), 4096, 5120), K, W, SET)
         ops5 = 2.0 * 4096 * 5120 * 1280
         bytes_rq = 3 * 4096 * 5120 + 4 * 4096
         extra["config5_dx_int8"] = {"ms": round(ms_dx, 5), "TOP/s": round(ops5 / (ms_dx * 1e-3) / 1e12, 1)}
@@ -231,13 +255,13 @@ def main():
                                          "GB/s": round(bytes_rq / (ms_rq * 1e-3) / 1e9, 1)}
         xs16 = activation(torch, 16, 4096, seed=10).to(dev)
         sk8, sks = int8.prepare_weight(weight(torch, 4096, 4096, seed=11).to(dev))
-        ms_sk_api = timed(torch, lambda: int8.linear(xs16, sk8, sks), K, W)
+        ms_sk_api = timed(torch, lambda: int8.linear(xs16, sk8, sks), K, W, SET)
         # the weight-streaming GEMM itself (quantized x resident, preallocated out)
         q16, s16 = int8.quantize(xs16)
         o16 = torch.empty((16, 4096), device=dev, dtype=torch.bfloat16)
         ms_sk = timed(torch, lambda: lib.xpuint8_linear_gemm_stream(
             st, L._ptr(q16), L._ptr(s16), L._ptr(sk8), L._ptr(sks), None, 0, L._ptr(o16),
-            16, 4096, 4096), K, W)
+            16, 4096, 4096), K, W, SET)
         bytes_sk = 4096 * 4096 + 16 * 4096 + 2 * 16 * 4096 + 4 * 4096 + 4 * 16
         extra["config5_skinny_m16"] = {
             "ms": round(ms_sk, 5), "GB/s": round(bytes_sk / (ms_sk * 1e-3) / 1e9, 1),
@@ -260,7 +284,7 @@ def main():
         f_r = torch.stack([torch.stack([th.cos(), -th.sin()], -1),
                            torch.stack([th.sin(), th.cos()], -1)], -2).to(dev)
         sc_r = torch.ones(D_r, device=dev)
-        ms_rope = timed(torch, lambda: rope.rows_dq(q_acc, f_r, sc_r, 1e-6, xs_r, ws_r), K, W)
+        ms_rope = timed(torch, lambda: rope.rows_dq(q_acc, f_r, sc_r, 1e-6, xs_r, ws_r), K, W, SET)
         bytes_rope = S_r * H_r * D_r * (4 + 2) + 4 * S_r + 4 * H_r * D_r
         extra["rms_rope_dequant_s4096_h24_d128"] = {
             "ms": round(ms_rope, 5), "GB/s": round(bytes_rope / (ms_rope * 1e-3) / 1e9, 1),
@@ -274,6 +298,7 @@ def main():
         "n_gpus": 1,
         "steps": K,
         "warmup": W,
+        "settle_s": SET,
         "ms_per_step": round(ms, 5),
         "higher_is_better": True,
         "scaling": "weak",
