@@ -24,6 +24,8 @@
 // (an explicit vmcnt) and one s_barrier.  Tiles are ordered so that each of
 // the 8 XCDs (blockIdx % 8) works on a compact rectangle of the output,
 // keeping its X rows and W rows in its own L2.
+#include <algorithm>
+
 #include "activations.hpp"
 #include "common.hpp"
 #include "kernels.hpp"
@@ -92,6 +94,20 @@ struct EpiDequant {
         }
         return c;
     }
+    // The persistent kernel keeps a tile's operands in LDS: the row scales,
+    // then kColVals fp32 values per output column (column scale, bias), each
+    // `stride` apart.
+    static constexpr int kColVals = 2;
+    __device__ __forceinline__ float col_value(int which, int n) const {
+        if (which == 0) return ws ? ws[n] : 1.f;
+        if (bias) return bias[n];
+        if (bias16) return __uint_as_float(uint32_t(bias16[n]) << 16);
+        return 0.f;
+    }
+    __device__ __forceinline__ Col col_lds(const float* c, int stride, int nl, int) const {
+        return Col{*reinterpret_cast<const float4*>(c + nl),
+                   *reinterpret_cast<const float4*>(c + stride + nl)};
+    }
     // the four bf16 results of one row, columns n..n+3, packed
     __device__ __forceinline__ uint2 convert(const v4i& v, float x, const Col& c) const {
         float r0 = float(v[0]) * (c.w.x * x), r1 = float(v[1]) * (c.w.y * x);
@@ -135,6 +151,15 @@ struct EpiAct {
     __device__ __forceinline__ float row(int m) const { return xs[m]; }
     __device__ __forceinline__ Col col(int n) const {
         return Col{*reinterpret_cast<const float4*>(ws + n)};
+    }
+    // LDS-held operands (as EpiDequant): the first half's column scales, then
+    // (paired) the second half's
+    static constexpr int kColVals = kPaired ? 2 : 1;
+    __device__ __forceinline__ float col_value(int which, int n) const {
+        return ws[which ? half + n : n];
+    }
+    __device__ __forceinline__ Col col_lds(const float* c, int stride, int nl, int second) const {
+        return Col{*reinterpret_cast<const float4*>(c + (second ? stride : 0) + nl)};
     }
     __device__ __forceinline__ static float deq(int a, float w, float x) {
         return bf16_round(float(a) * (w * x));
@@ -194,6 +219,23 @@ __device__ __forceinline__ v4i lds_read16(uint32_t addr) {
     v4i r;
     asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(addr));
     return r;
+}
+// the same with a constant byte offset in the instruction's offset field (one
+// address register serves a row of fragments)
+template <int OFF>
+__device__ __forceinline__ v4i lds_read16_at(uint32_t addr) {
+    static_assert(OFF >= 0 && OFF < 65536, "ds offset field");
+    v4i r;
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "n"(OFF));
+    return r;
+}
+// fragments i = 0 .. COUNT-1 at addr + i * 1024
+template <int COUNT, int I = 0, int NF>
+__device__ __forceinline__ void lds_read_frags(v4i (&f)[NF], uint32_t addr) {
+    if constexpr (I < COUNT) {
+        f[I] = lds_read16_at<I * 1024>(addr);
+        lds_read_frags<COUNT, I + 1>(f, addr);
+    }
 }
 // Wait until at most N LDS reads are outstanding; v is tied to the wait so
 // its uses cannot be scheduled above it.
@@ -369,13 +411,14 @@ __global__ __launch_bounds__(WGM * WGN * 64) void gemm_i8_kernel(
 // The staged epilogue of one wave: its TM x TN blocks of results (output
 // rows m0w.., columns n0w..), RB row blocks (16*RB rows) per pass through
 // `stg` (RB * 4 KB of idle LDS): 256-byte rows of 16-byte chunks, chunk c of
-// row r at c ^ (r & 15), each row leaving as contiguous 16-byte stores.  Row
-// and column operands are loaded before any conversion so their latency is
-// paid once.  Paired epilogues take the (first, second) accumulator pairs
+// row r at c ^ (r & 15), each row leaving as contiguous 16-byte stores.  The
+// column operands arrive in registers, the row operand of row block b as
+// rowv(b).  Paired epilogues take the (first, second) accumulator pairs
 // (2a, 2a+1).
-template <int TM, int TN, int WN_OUT, class Epi, int RB = 2>
-__device__ __forceinline__ void staged_epilogue(const Epi& epi, v4i (&acc)[TN][TM], int8_t* stg,
-                                                int m0w, int n0w, int M, int N, int lane) {
+template <int TM, int TN, int WN_OUT, class Epi, int RB, class RowF>
+__device__ __forceinline__ void staged_store(const Epi& epi, v4i (&acc)[TN][TM], const RowF& rowv,
+                                             const typename Epi::Col (&ccol)[TN], int8_t* stg,
+                                             int m0w, int n0w, int M, int N, int lane) {
     constexpr bool PAIRED = Epi::kPaired;
     constexpr int OUT_TN = PAIRED ? TN / 2 : TN;
     constexpr int STG_ROWS = 16 * RB;
@@ -383,33 +426,22 @@ __device__ __forceinline__ void staged_epilogue(const Epi& epi, v4i (&acc)[TN][T
     constexpr int ITEMS = STG_ROWS * CH;
     static_assert(CH <= 16, "staging shape");
     static_assert(TM % RB == 0, "whole passes");
-    float xrow[TM];
-    typename Epi::Col ccol[TN];
-#pragma unroll
-    for (int b = 0; b < TM; ++b) xrow[b] = epi.row(min(m0w + 16 * b + (lane & 15), M - 1));
-#pragma unroll
-    for (int a = 0; a < TN; ++a) {
-        if constexpr (PAIRED)
-            ccol[a] = epi.col(min(n0w + 16 * (a >> 1) + 4 * (lane >> 4), N - 4) +
-                              ((a & 1) ? pair_offset(epi) : 0));
-        else
-            ccol[a] = epi.col(min(n0w + 16 * a + 4 * (lane >> 4), N - 4));
-    }
 #pragma unroll
     for (int pass = 0; pass < TM / RB; ++pass) {
 #pragma unroll
         for (int bb = 0; bb < RB; ++bb) {
             const int b = RB * pass + bb;
             const int r = 16 * bb + (lane & 15);
+            const float x = rowv(b);
 #pragma unroll
             for (int a = 0; a < OUT_TN; ++a) {
                 const int c = 16 * a + 4 * (lane >> 4);
                 uint2 v;
                 if constexpr (PAIRED)
-                    v = epi.convert2(acc[2 * a][b], acc[2 * a + 1][b], xrow[b], ccol[2 * a],
+                    v = epi.convert2(acc[2 * a][b], acc[2 * a + 1][b], x, ccol[2 * a],
                                      ccol[2 * a + 1]);
                 else
-                    v = epi.convert(acc[a][b], xrow[b], ccol[a]);
+                    v = epi.convert(acc[a][b], x, ccol[a]);
                 *reinterpret_cast<uint2*>(stg + r * 256 + (((c >> 3) ^ (r & 15)) << 4) +
                                           (c & 7) * 2) = v;
             }
@@ -427,6 +459,27 @@ __device__ __forceinline__ void staged_epilogue(const Epi& epi, v4i (&acc)[TN][T
         }
         __builtin_amdgcn_s_waitcnt(0xC07F);                       // reads done before reuse
     }
+}
+
+// staged_store with the row and column operands read from global memory, all
+// before any conversion so that their latency is paid once
+template <int TM, int TN, int WN_OUT, class Epi, int RB = 2>
+__device__ __forceinline__ void staged_epilogue(const Epi& epi, v4i (&acc)[TN][TM], int8_t* stg,
+                                                int m0w, int n0w, int M, int N, int lane) {
+    float xrow[TM];
+    typename Epi::Col ccol[TN];
+#pragma unroll
+    for (int b = 0; b < TM; ++b) xrow[b] = epi.row(min(m0w + 16 * b + (lane & 15), M - 1));
+#pragma unroll
+    for (int a = 0; a < TN; ++a) {
+        if constexpr (Epi::kPaired)
+            ccol[a] = epi.col(min(n0w + 16 * (a >> 1) + 4 * (lane >> 4), N - 4) +
+                              ((a & 1) ? pair_offset(epi) : 0));
+        else
+            ccol[a] = epi.col(min(n0w + 16 * a + 4 * (lane >> 4), N - 4));
+    }
+    staged_store<TM, TN, WN_OUT, Epi, RB>(epi, acc, [&](int b) { return xrow[b]; }, ccol, stg,
+                                          m0w, n0w, M, N, lane);
 }
 
 // ------------------------------------------------------------ large tiles
@@ -607,21 +660,30 @@ hipError_t launch_cfg(hipStream_t st, const int8_t* X, int64_t ldx, const int8_t
 }
 
 // ------------------------------------------------------------ ping-pong
-// A BM x BN tile (256 x 320) per block of 8 waves in two groups of 4 (group =
-// the tile's row half, 2 x 4 waves of 128 x 80), one block per CU, a ring of S
-// LDS stages of 64-byte K steps filled by direct global->LDS loads.  The
-// groups alternate roles every half step, so that on each SIMD one wave feeds
-// the matrix core while the other moves data:
+// BM x BN tiles (256 x 320) for one persistent block of 8 waves per CU, in two
+// groups of 4 (group = the tile's row half, 2 x 4 waves of 128 x 80, or 4 x 2
+// of 64 x 160 for paired epilogues), a ring of S = 4 LDS slots of 64-byte K
+// steps filled by direct global->LDS loads.  Block b takes tiles b, b + G,
+// b + 2G, ... (G = gridDim.x, one block per CU).  Within a tile the groups
+// alternate roles every half step, so that on each SIMD one wave feeds the
+// matrix core while the other moves data:
 //   phase A(k): group 0 runs step k's MFMAs;  group 1 reads step k's
 //               fragments and issues its loads for step k + S - 1
 //   phase B(k): group 1 runs step k's MFMAs;  group 0 reads step k + 1's
 //               fragments and issues its loads for step k + S - 1
 // with one s_barrier between phases.  Step j's loads are complete (each wave
 // waits for its own, then the barrier) before phase B(j - 1), the first
-// reader of stage j % S; stage j % S is refilled (for step j + S) only from
-// phase A(j + 1) on, after its last reader, A(j).  The larger tile halves the
-// operand bytes per MFMA of the two-block 256 x 160 kernel, and the
-// alternation keeps the matrix core fed while the loads go out.
+// reader of step j; its slot is refilled (for step j + S) only from phase
+// A(j + 1) on, after its last reader, A(j).  Step k lives in slot (k + 1) % S.
+//
+// Between tiles: once a tile's last MFMAs are issued (every fragment read is
+// complete), each wave issues the next tile's steps 0-2 into slots 1-3 and
+// the global loads of its row/column operands, and only then runs this tile's
+// epilogue, staged through slot 0.  Those loads are older than the epilogue's
+// stores, so they land while it runs; one vmcnt(0) afterwards (the stores
+// included) and a barrier start the next tile.  The epilogue's per-row and
+// per-column operands come from LDS (two buffers after the ring, filled one
+// tile ahead), not from global memory at the end of the tile.
 template <int BM, int BN, int WGM, int WGN, int S, bool KTAIL, class Epi>
 __global__ __launch_bounds__(512, 1) void gemm_i8_pp_kernel(
     const int8_t* __restrict__ X, int64_t ldx, const int8_t* __restrict__ W, int64_t ldw, int M,
@@ -637,57 +699,76 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_pp_kernel(
     constexpr int PER0 = PER, PER1 = REM == 0 ? PER : PER - 1;
     constexpr int STAGE_BYTES = NB * 1024;
     constexpr int RING = S * STAGE_BYTES;
-    static_assert(S >= 3, "three or more stages");
-    static_assert(!Epi::kStaged || NW * 32 * 256 <= RING, "staging fits in the ring");
-    static_assert(TM % 2 == 0, "epilogue passes of 32 rows");
+    static_assert(S == 4, "slot 0 stages the epilogue while the next tile's steps 0-2 fill 1-3");
+    constexpr bool STAGED = Epi::kStaged;
+    static_assert(!STAGED || NW * 16 * 256 <= STAGE_BYTES, "epilogue staging fits in one slot");
     constexpr bool PAIRED = Epi::kPaired;
-    static_assert(!PAIRED || (Epi::kStaged && TN % 2 == 0), "pairs are whole per wave");
+    static_assert(!PAIRED || (STAGED && TN % 2 == 0), "pairs are whole per wave");
     constexpr int OUT_TN = PAIRED ? TN / 2 : TN;
     constexpr int WN_OUT = 16 * OUT_TN, BN_OUT = WN_OUT * WGN;
-    __shared__ __attribute__((aligned(1024))) int8_t smem[RING];
+    // a tile's epilogue operands in LDS: BM row scales, then NCV x BN_OUT
+    // column values; two buffers (the next tile's are written after this
+    // tile's epilogue has read its own)
+    constexpr int NCV = [] { if constexpr (STAGED) return Epi::kColVals; else return 0; }();
+    constexpr int NSCALE = STAGED ? BM + NCV * BN_OUT : 0;
+    constexpr int SCALE_BYTES = NSCALE * 4;
+    constexpr int SPT = (NSCALE + 511) / 512;                   // operand values per thread
+    __shared__ __attribute__((aligned(1024))) int8_t smem[RING + 2 * SCALE_BYTES + 16];
 
     const int tiles = tiles_m * tiles_n;
-    int t = blockIdx.x;
-    if (tiles % 8 == 0) t = (t % 8) * (tiles / 8) + t / 8;
-    constexpr int GROUP = 8;
-    const int band = t / (GROUP * tiles_n);
-    const int first_m = band * GROUP;
-    const int gm = min(tiles_m - first_m, GROUP);
-    const int in_band = t - band * GROUP * tiles_n;
-    const int m0 = (first_m + in_band % gm) * BM, n0 = (in_band / gm) * BN_OUT;
-
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = wave / WGN, wn = wave % WGN;
     const int g = wm / (WGM / 2);                               // group: the row half
 
+    // tile origin of sequence number i: each XCD (i % 8, as blockIdx % 8)
+    // takes a contiguous eighth of the tiles, walked in column bands of 8 row
+    // tiles
+    auto tile_origin = [&](int i, int& m0, int& n0) {
+        int t = i;
+        if (tiles % 8 == 0) t = (t % 8) * (tiles / 8) + t / 8;
+        constexpr int GROUP = 8;
+        const int band = t / (GROUP * tiles_n);
+        const int first_m = band * GROUP;
+        const int gm = min(tiles_m - first_m, GROUP);
+        const int in_band = t - band * GROUP * tiles_n;
+        m0 = (first_m + in_band % gm) * BM;
+        n0 = (in_band / gm) * BN_OUT;
+    };
+
+    // DMA: wave w brings blocks w, w + NW, ... of every step; lane l row l/4,
+    // chunk swz(l/4, l%4).  Rows past M or N repeat the last row (their
+    // results are never stored).  The 32-bit offsets keep the saddr form.
     const int lr = lane >> 2;
     const int lc = swz(lr, lane & 3) * 16;
-    const int8_t* const xbase = X + int64_t(m0) * ldx;
-    const int8_t* const wbase = W + int64_t(n0) * ldw;
-    const int8_t* const gbase = W + (int64_t(pair_offset(epi)) + n0) * ldw;
     const int8_t* base[PER];
     int off[PER];
+    auto setup = [&](int m0, int n0) {
+        const int8_t* const xbase = X + int64_t(m0) * ldx;
+        const int8_t* const wbase = W + int64_t(n0) * ldw;
+        const int8_t* const gbase = W + (int64_t(pair_offset(epi)) + n0) * ldw;
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-        const int j = min(wave + NW * i, NB - 1);
-        if (j < XB) {
-            base[i] = xbase;
-            off[i] = (min(m0 + 16 * j + lr, M - 1) - m0) * int(ldx) + lc;
-        } else if constexpr (PAIRED) {
-            const int jw = j - XB;
-            base[i] = (jw & 1) ? gbase : wbase;
-            off[i] = (min(n0 + 16 * (jw >> 1) + lr, N - 1) - n0) * int(ldw) + lc;
-        } else {
-            base[i] = wbase;
-            off[i] = (min(n0 + 16 * (j - XB) + lr, N - 1) - n0) * int(ldw) + lc;
+        for (int i = 0; i < PER; ++i) {
+            const int j = min(wave + NW * i, NB - 1);
+            if (j < XB) {
+                base[i] = xbase;
+                off[i] = (min(m0 + 16 * j + lr, M - 1) - m0) * int(ldx) + lc;
+            } else if constexpr (PAIRED) {
+                const int jw = j - XB;
+                base[i] = (jw & 1) ? gbase : wbase;
+                off[i] = (min(n0 + 16 * (jw >> 1) + lr, N - 1) - n0) * int(ldw) + lc;
+            } else {
+                base[i] = wbase;
+                off[i] = (min(n0 + 16 * (j - XB) + lr, N - 1) - n0) * int(ldw) + lc;
+            }
         }
-    }
+    };
     const int KT = (K + BK - 1) / BK;
+    auto slot = [&](int kk) { return ((kk + 1) % S) * STAGE_BYTES; };
     // this wave's loads for step kk (its share of the stage's blocks)
     auto issue = [&](int kk) {
         const int k0 = kk * BK;
-        int8_t* const st = smem + (kk % S) * STAGE_BYTES;
+        int8_t* const st = smem + slot(kk);
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
             if (i == PER - 1 && REM != 0 && g != 0) continue;
@@ -709,7 +790,36 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_pp_kernel(
             else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
         }
     };
-    static_assert(S <= 4, "wait_batches covers up to two later batches");
+
+    // the epilogue operands of a tile: global loads into registers (issued
+    // early), written to LDS buffer `buf` once they have landed
+    float sv[SPT > 0 ? SPT : 1];
+    auto fetch_scales = [&](int m0, int n0) {
+        if constexpr (STAGED) {
+#pragma unroll
+            for (int i = 0; i < SPT; ++i) {
+                const int idx = threadIdx.x + 512 * i;
+                float v = 0.f;
+                if (idx < BM) {
+                    v = epi.row(min(m0 + idx, M - 1));
+                } else if (idx < NSCALE) {
+                    const int c = idx - BM, which = c / BN_OUT, nl = c - which * BN_OUT;
+                    v = epi.col_value(which, min(n0 + nl, N - 1));
+                }
+                sv[i] = v;
+            }
+        }
+    };
+    auto put_scales = [&](int buf) {
+        if constexpr (STAGED) {
+            float* d = reinterpret_cast<float*>(smem + RING + buf * SCALE_BYTES);
+#pragma unroll
+            for (int i = 0; i < SPT; ++i) {
+                const int idx = threadIdx.x + 512 * i;
+                if (idx < NSCALE) d[idx] = sv[i];
+            }
+        }
+    };
 
     const int frag = (lane & 15) * 64 + swz(lane & 15, lane >> 4) * 16;
     const int xoff = (wm * TM) * 1024 + frag;
@@ -717,17 +827,11 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_pp_kernel(
     const uint32_t sbase = lds_addr(smem);
 
     v4i acc[TN][TM];
-#pragma unroll
-    for (int a = 0; a < TN; ++a)
-#pragma unroll
-        for (int b = 0; b < TM; ++b) acc[a][b] = v4i{0, 0, 0, 0};
     v4i wf[TN], xf[TM];
     auto read_frags = [&](int kk) {
-        const uint32_t sb = sbase + (kk % S) * STAGE_BYTES;
-#pragma unroll
-        for (int i = 0; i < TN; ++i) wf[i] = lds_read16(sb + woff + i * 1024);
-#pragma unroll
-        for (int i = 0; i < TM; ++i) xf[i] = lds_read16(sb + xoff + i * 1024);
+        const uint32_t sb = sbase + slot(kk);
+        lds_read_frags<TN>(wf, sb + woff);
+        lds_read_frags<TM>(xf, sb + xoff);
     };
     auto compute = [&]() {
         lgkm_wait_all(wf, xf);                                  // fragments in
@@ -742,55 +846,102 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_pp_kernel(
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
     };
+    auto epilogue = [&](int m0, int n0, int buf) {
+        if constexpr (STAGED) {
+            const float* sc = reinterpret_cast<const float*>(smem + RING + buf * SCALE_BYTES);
+            const float* xr = sc + wm * WM + (lane & 15);
+            typename Epi::Col ccol[TN];
+#pragma unroll
+            for (int a = 0; a < TN; ++a) {
+                if constexpr (PAIRED)
+                    ccol[a] = epi.col_lds(sc + BM, BN_OUT,
+                                          wn * WN_OUT + 16 * (a >> 1) + 4 * (lane >> 4), a & 1);
+                else
+                    ccol[a] = epi.col_lds(sc + BM, BN_OUT, wn * WN_OUT + 16 * a + 4 * (lane >> 4), 0);
+            }
+            staged_store<TM, TN, WN_OUT, Epi, 1>(epi, acc, [&](int b) { return xr[16 * b]; }, ccol,
+                                                 smem + wave * (16 * 256), m0 + wm * WM,
+                                                 n0 + wn * WN_OUT, M, N, lane);
+        } else {
+            const int mrow = m0 + wm * WM + (lane & 15);
+            const int ncol = n0 + wn * WN + 4 * (lane >> 4);
+#pragma unroll
+            for (int b = 0; b < TM; ++b) {
+                const int m = mrow + 16 * b;
+                if (m >= M) continue;
+#pragma unroll
+                for (int a = 0; a < TN; ++a) {
+                    const int n = ncol + 16 * a;
+                    if (n < N) epi(m, n, acc[a][b]);
+                }
+            }
+        }
+    };
 
-    // prologue: steps 0 .. S-2 requested by every wave; step 0 complete;
-    // group 0 reads step 0's fragments.  Each group then runs its own loop of
-    // (first half, barrier, second half, barrier), group 0 a half step ahead.
+    int ti = blockIdx.x;
+    if (ti >= tiles) return;
+    int m0, n0;
+    tile_origin(ti, m0, n0);
+    setup(m0, n0);
+    // first tile: its operands, steps 0 .. S-2 requested, step 0 complete
+    fetch_scales(m0, n0);
     for (int kk = 0; kk < S - 1; ++kk)
         if (kk < KT) issue(kk);
     wait_batches(min(S - 2, KT - 1));
+    put_scales(0);
     barrier();
-    if (g == 0) {
-        read_frags(0);
-        barrier();
-#pragma clang loop unroll(disable)
-        for (int k = 0; k < KT; ++k) {
-            compute();                                          // A(k)
-            if (k + 1 < KT) wait_batches(min(S - 3, KT - 2 - k));
-            barrier();
-            if (k + 1 < KT) read_frags(k + 1);                  // B(k)
-            if (k + S - 1 < KT) issue(k + S - 1);
-            barrier();
-        }
-    } else {
-        barrier();
-#pragma clang loop unroll(disable)
-        for (int k = 0; k < KT; ++k) {
-            read_frags(k);                                      // A(k)
-            if (k + S - 1 < KT) issue(k + S - 1);
-            if (k + 1 < KT) wait_batches(min(S - 2, KT - 2 - k));
-            barrier();
-            compute();                                          // B(k)
-            barrier();
-        }
-    }
-
-    if constexpr (Epi::kStaged) {
-        staged_epilogue<TM, TN, WN_OUT, Epi>(epi, acc, smem + wave * (32 * 256),
-                                             m0 + wm * WM, n0 + wn * WN_OUT, M, N, lane);
-    } else {
-        const int mrow = m0 + wm * WM + (lane & 15);
-        const int ncol = n0 + wn * WN + 4 * (lane >> 4);
+    for (int it = 0;; ++it) {
 #pragma unroll
-        for (int b = 0; b < TM; ++b) {
-            const int m = mrow + 16 * b;
-            if (m >= M) continue;
+        for (int a = 0; a < TN; ++a)
 #pragma unroll
-            for (int a = 0; a < TN; ++a) {
-                const int n = ncol + 16 * a;
-                if (n < N) epi(m, n, acc[a][b]);
+            for (int b = 0; b < TM; ++b) acc[a][b] = v4i{0, 0, 0, 0};
+        // group 0 reads step 0's fragments; each group then runs its own loop
+        // of (first half, barrier, second half, barrier), group 0 a half step
+        // ahead
+        if (g == 0) {
+            read_frags(0);
+            barrier();
+#pragma clang loop unroll(disable)
+            for (int k = 0; k < KT; ++k) {
+                compute();                                      // A(k)
+                if (k + 1 < KT) wait_batches(min(S - 3, KT - 2 - k));
+                barrier();
+                if (k + 1 < KT) read_frags(k + 1);              // B(k)
+                if (k + S - 1 < KT) issue(k + S - 1);
+                barrier();
+            }
+        } else {
+            barrier();
+#pragma clang loop unroll(disable)
+            for (int k = 0; k < KT; ++k) {
+                read_frags(k);                                  // A(k)
+                if (k + S - 1 < KT) issue(k + S - 1);
+                if (k + 1 < KT) wait_batches(min(S - 2, KT - 2 - k));
+                barrier();
+                compute();                                      // B(k)
+                barrier();
             }
         }
+        // every fragment read has completed: the next tile's first steps and
+        // operands go out ahead of this tile's stores
+        const int tnext = ti + int(gridDim.x);
+        const bool more = tnext < tiles;
+        int m0n = 0, n0n = 0;
+        if (more) {
+            tile_origin(tnext, m0n, n0n);
+            setup(m0n, n0n);
+            fetch_scales(m0n, n0n);
+            for (int kk = 0; kk < S - 1; ++kk)
+                if (kk < KT) issue(kk);
+        }
+        epilogue(m0, n0, it & 1);
+        if (!more) break;
+        __builtin_amdgcn_s_waitcnt(0);                          // stores, loads, LDS all done
+        put_scales((it + 1) & 1);
+        barrier();
+        ti = tnext;
+        m0 = m0n;
+        n0 = n0n;
     }
 }
 
@@ -1074,14 +1225,13 @@ hipError_t launch_gemm(hipStream_t st, const int8_t* X, int64_t ldx, const int8_
         // when it gives one tile per CU (5% faster at the FFN up-projection)
         const int tm = (M + BM - 1) / BM, tn_pp = (N + 159) / 160;
         if (int64_t(tm) * tn_pp >= device_cus()) {
+            const dim3 grid(unsigned(std::min<int64_t>(int64_t(tm) * tn_pp, device_cus())));
             if (K % 64 == 0)
-                hipLaunchKernelGGL((gemm_i8_pp_kernel<256, 320, 4, 2, 4, false, Epi>),
-                                   dim3(unsigned(tm * tn_pp)), dim3(512), 0, st, X, ldx, W, ldw,
-                                   M, N, K, tm, tn_pp, epi);
+                hipLaunchKernelGGL((gemm_i8_pp_kernel<256, 320, 4, 2, 4, false, Epi>), grid,
+                                   dim3(512), 0, st, X, ldx, W, ldw, M, N, K, tm, tn_pp, epi);
             else
-                hipLaunchKernelGGL((gemm_i8_pp_kernel<256, 320, 4, 2, 4, true, Epi>),
-                                   dim3(unsigned(tm * tn_pp)), dim3(512), 0, st, X, ldx, W, ldw,
-                                   M, N, K, tm, tn_pp, epi);
+                hipLaunchKernelGGL((gemm_i8_pp_kernel<256, 320, 4, 2, 4, true, Epi>), grid,
+                                   dim3(512), 0, st, X, ldx, W, ldw, M, N, K, tm, tn_pp, epi);
             return hipGetLastError();
         }
         // 4 x 1 waves of 64 x 160: each wave holds five (first, second) pairs
@@ -1107,14 +1257,13 @@ hipError_t launch_gemm(hipStream_t st, const int8_t* X, int64_t ldx, const int8_
         // one 256 x 320 ping-pong tile per CU when they fill every CU
         const int tn_pp = (N + 319) / 320;
         if (int64_t(tm) * tn_pp >= device_cus()) {
+            const dim3 grid(unsigned(std::min<int64_t>(int64_t(tm) * tn_pp, device_cus())));
             if (K % 64 == 0)
-                hipLaunchKernelGGL((gemm_i8_pp_kernel<256, 320, 2, 4, 4, false, Epi>),
-                                   dim3(unsigned(tm * tn_pp)), dim3(512), 0, st, X, ldx, W, ldw, M,
-                                   N, K, tm, tn_pp, epi);
+                hipLaunchKernelGGL((gemm_i8_pp_kernel<256, 320, 2, 4, 4, false, Epi>), grid,
+                                   dim3(512), 0, st, X, ldx, W, ldw, M, N, K, tm, tn_pp, epi);
             else
-                hipLaunchKernelGGL((gemm_i8_pp_kernel<256, 320, 2, 4, 4, true, Epi>),
-                                   dim3(unsigned(tm * tn_pp)), dim3(512), 0, st, X, ldx, W, ldw, M,
-                                   N, K, tm, tn_pp, epi);
+                hipLaunchKernelGGL((gemm_i8_pp_kernel<256, 320, 2, 4, 4, true, Epi>), grid,
+                                   dim3(512), 0, st, X, ldx, W, ldw, M, N, K, tm, tn_pp, epi);
             return hipGetLastError();
         }
         if (int64_t(tm) * tn >= 192) {

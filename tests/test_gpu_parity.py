@@ -58,6 +58,36 @@ def test_int8_gemm_full_size_c3(dev):
     assert np.array_equal(got, O.int_mm(a, b))
 
 
+@pytest.mark.parametrize("m,n,k", [(2100, 10000, 1040), (4300, 6000, 272)])
+def test_persistent_tiles_exact(dev, m, n, k):
+    """Shapes that take the persistent 256x320 kernel (one block per CU
+    looping over tiles): ragged last row and column tiles, K not a multiple of
+    64, and 288 / 323 tiles, so some blocks run two tiles and others one.  The
+    int32 product, then the dequant epilogue (fp32 bias, then bf16 bias) on
+    the same operands."""
+    rng = np.random.default_rng(m + n + k)
+    a = rng.integers(-127, 128, (m, k), dtype=np.int8)
+    b = rng.integers(-127, 128, (n, k), dtype=np.int8)
+    want32 = O.int_mm(a, b)
+    ta, tb = torch.from_numpy(a).to(dev), torch.from_numpy(b).to(dev)
+    got = npy(int8.int_mm(ta, tb.t()))
+    assert np.array_equal(got, want32), mismatch(got, want32)
+    xs = rng.uniform(1e-3, 5e-2, m).astype(np.float32)
+    ws = rng.uniform(1e-5, 1e-3, n).astype(np.float32)
+    bias = (rng.standard_normal(n) * 0.1).astype(np.float32)
+    bias16 = O.f32_to_bf16(bias)
+    lib = L._lib()
+    t = lambda v: torch.from_numpy(v).to(dev)
+    txs, tws = t(xs), t(ws)
+    for bvec, kind, bref in ((t(bias), 0, bias), (t(bias16.view(np.int16)), 1, O.bf16_to_f32(bias16))):
+        out = torch.empty((m, n), device=dev, dtype=torch.bfloat16)
+        rc = lib.xpuint8_linear_gemm_stream(L._stream(dev), L._ptr(ta), L._ptr(txs), L._ptr(tb),
+                                            L._ptr(tws), L._ptr(bvec), kind, L._ptr(out), m, n, k)
+        assert rc == 0, lib.xpuint8_last_error()
+        want = O.dequant(want32, xs, ws, bref)
+        assert np.array_equal(bits(out), want), mismatch(bits(out), want)
+
+
 # ------------------------------------------------------- rotate / quantize
 QSHAPES = [(1, 256), (7, 1280), (64, 5120), (33, 8192), (5, 3072), (3, 10240), (2, 16384),
            (5, 4352), (3, 16896), (2, 32768), (2, 33792), (2, 66560), (3, 16640)]
@@ -291,6 +321,17 @@ def test_ffn_up_epilogue_exact(dev, act, m, inner, k):
     """The up-projection GEMM's activation epilogue against the oracle's
     dequant_act of the int32 product (ragged M, a partial last column tile,
     K not a multiple of 64)."""
+    check_ffn_up(dev, act, m, inner, k)
+
+
+@pytest.mark.parametrize("act", [4, 5])
+def test_ffn_up_persistent_tiles_exact(dev, act):
+    """The same through the persistent 256x320 kernel: 578 paired tiles
+    (GEGLU) or 289 plain ones (GELU), ragged in both dimensions, K % 64 != 0."""
+    check_ffn_up(dev, act, 4100, 5200, 1040)
+
+
+def check_ffn_up(dev, act, m, inner, k):
     rng = np.random.default_rng(act * 100 + m)
     rows = 2 * inner if act in O.PAIRED else inner
     xq = rng.integers(-127, 128, (m, k), dtype=np.int8)
