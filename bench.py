@@ -311,7 +311,7 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(gemm_tops, 2), "peak": PEAK_INT8_TOPS,
                      "unit": "TOP/s", "frac": round(gemm_tops / PEAK_INT8_TOPS, 4),
                      "traffic": measured_traffic(),
-                     "kernel": "gemm_i8_pp_kernel (256x320 ping-pong) with dequant epilogue "
+                     "kernel": "gemm_i8_pp_kernel (persistent 256x320 ping-pong) with dequant epilogue "
                                "(2*M*N*K int ops per launch)"},
         "extra": extra,
     }
