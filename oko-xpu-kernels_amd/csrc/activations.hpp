@@ -60,4 +60,24 @@ __device__ __forceinline__ float activate(const uint16_t* tab, float a, float b)
     }
 }
 
+// The activation before its last bf16 rounding: bf16(activate_pre(..)) is
+// activate(..) bit for bit (rounding to nearest even is idempotent, and the
+// tables hold quiet NaNs), so a caller that packs two results with one
+// v_cvt_pk_bf16_f32 can skip the separate rounding of each.
+template <int ACT>
+__device__ __forceinline__ float activate_pre(const uint16_t* tab, float a, float b) {
+    if constexpr (ACT == 2) {
+        return tab_lookup(tab, kTabSilu, a) * b;
+    } else if constexpr (ACT == 3) {
+        const float tg = tab_lookup(tab, kTabSituTanhG, b);
+        const float sg = tab_lookup(tab, kTabSigmoid, b);
+        const float th = tab_lookup(tab, kTabSituTanhH, a);
+        return bf16_round(tg * sg) * th;
+    } else if constexpr (ACT == 4) {
+        return a * tab_lookup(tab, kTabGeluErf, b);
+    } else {
+        return activate<ACT>(tab, a, b);
+    }
+}
+
 }  // namespace xpuint8

@@ -164,19 +164,20 @@ struct EpiAct {
     __device__ __forceinline__ static float deq(int a, float w, float x) {
         return bf16_round(float(a) * (w * x));
     }
+    // the activations' last bf16 rounding is the packing conversion itself
     __device__ __forceinline__ uint2 convert(const v4i& v, float x, const Col& c) const {
-        const float r0 = activate<ACT>(tab, deq(v[0], c.w.x, x), 0.f);
-        const float r1 = activate<ACT>(tab, deq(v[1], c.w.y, x), 0.f);
-        const float r2 = activate<ACT>(tab, deq(v[2], c.w.z, x), 0.f);
-        const float r3 = activate<ACT>(tab, deq(v[3], c.w.w, x), 0.f);
+        const float r0 = activate_pre<ACT>(tab, deq(v[0], c.w.x, x), 0.f);
+        const float r1 = activate_pre<ACT>(tab, deq(v[1], c.w.y, x), 0.f);
+        const float r2 = activate_pre<ACT>(tab, deq(v[2], c.w.z, x), 0.f);
+        const float r3 = activate_pre<ACT>(tab, deq(v[3], c.w.w, x), 0.f);
         return make_uint2(cvt_pk_bf16(r0, r1), cvt_pk_bf16(r2, r3));
     }
     __device__ __forceinline__ uint2 convert2(const v4i& a, const v4i& b, float x, const Col& ca,
                                               const Col& cb) const {
-        const float r0 = activate<ACT>(tab, deq(a[0], ca.w.x, x), deq(b[0], cb.w.x, x));
-        const float r1 = activate<ACT>(tab, deq(a[1], ca.w.y, x), deq(b[1], cb.w.y, x));
-        const float r2 = activate<ACT>(tab, deq(a[2], ca.w.z, x), deq(b[2], cb.w.z, x));
-        const float r3 = activate<ACT>(tab, deq(a[3], ca.w.w, x), deq(b[3], cb.w.w, x));
+        const float r0 = activate_pre<ACT>(tab, deq(a[0], ca.w.x, x), deq(b[0], cb.w.x, x));
+        const float r1 = activate_pre<ACT>(tab, deq(a[1], ca.w.y, x), deq(b[1], cb.w.y, x));
+        const float r2 = activate_pre<ACT>(tab, deq(a[2], ca.w.z, x), deq(b[2], cb.w.z, x));
+        const float r3 = activate_pre<ACT>(tab, deq(a[3], ca.w.w, x), deq(b[3], cb.w.w, x));
         return make_uint2(cvt_pk_bf16(r0, r1), cvt_pk_bf16(r2, r3));
     }
     __device__ __forceinline__ void store16(int m, int n, const uint4& v) const {
