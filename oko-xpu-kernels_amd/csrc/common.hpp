@@ -113,34 +113,89 @@ __device__ __forceinline__ int lane_w(int sl) {
     return i2 + 4 * i3;
 }
 
-// Axes 2 and 3.  The 4-point butterfly over lanes {L, L^m1, L^m2, L^m1^m2}
-// as the reference's bfly_xor (src/xpuint8.cpp:441-448): A = v + v[L^m1];
-// B = v - v[L^m1]; out = A + B[L^m2].  With the lane holding index
-// j = c1 + 2*c2 of the 4-point set (c1, c2 its m1, m2 components) this is
-// bit-identical to bfly4 (src/xpuint8.cpp:279-285) for any masks m1, m2:
-// each output is the same two IEEE additions of the same operands, up to
-// commutation and the exact negation x + (b - a) == x - (a - b).
-__device__ __forceinline__ void hadamard_xlane(float (&v)[16]) {
-#pragma unroll
-    for (int t = 0; t < 16; ++t) {           // axis 2: lane xor 1, xor 2
-        const float p = dpp<kDppXor1>(v[t]);
-        const float A = v[t] + p;
-        const float B = v[t] - p;
-        v[t] = A + dpp<kDppXor2>(B);
-    }
-#pragma unroll
-    for (int t = 0; t < 16; ++t) {           // axis 3: lane xor 7, xor 15
-        const float p = dpp<kDppXor7>(v[t]);
-        const float A = v[t] + p;
-        const float B = v[t] - p;
-        v[t] = A + dpp<kDppXor15>(B);
-    }
+// Axes 2 and 3.  The reference's 4-point butterfly over lanes {L, L^m1, L^m2,
+// L^m1^m2} (bfly_xor, src/xpuint8.cpp:441-448) forms, for the lane holding
+// index j of the 4-point set,
+//   out_j = A_j + B_(j^2),   A_j = x_j + x_(j^1),   B_j = x_j - x_(j^1)
+// (bit-identical to bfly4, src/xpuint8.cpp:279-285).  A_j = A_(j^1) and
+// B_(j^1) = -B_j exactly, so four lanes need only four distinct sums, and each
+// lane forms one of them and then one output, two instructions instead of
+// three:
+//   step 1 (partner j^1): even j keeps A_j = x_j + x_(j^1), odd j keeps
+//          B_j = x_j - x_(j^1);
+//   step 2 (partner j^3): even j outputs out_j = A_j - B_(j^3) (= A_j + B_(j^2));
+//          odd j outputs out_(j^2) = B_j + A_(j^3) (= A_(j^2) + B_j).
+// Each step is x + s * dpp(x) with a per-lane sign s = +-1 (step 2 takes -s
+// through the source negation modifier): one v_fmac_f32_dpp, whose product is
+// exact, so it rounds exactly as the add or
+// subtract it replaces (signed zeros included).  The lane with an odd j then
+// holds output j^2: after both axes lane sl holds register lane_w_rot(sl).
+// Index j^1 / j^3 is lane xor 1 / xor 3 for axis 2 (digit i2) and lane xor 7 /
+// xor 8 for axis 3 (digit i3), all single DPP controls (quad_perm, row_half_mirror,
+// row_ror:8).
+struct XlaneSigns {
+    float a2, a3;     // step-1 signs of axes 2 and 3; step 2 uses their negation
+};
+// The step-1 sign is -1 where the lane's digit is odd (bit 0 of i2 is bit 0 of
+// w = lane_w(sl), bit 0 of i3 is bit 2 of w).
+__device__ __forceinline__ XlaneSigns xlane_signs(int sl) {
+    const uint32_t w = uint32_t(lane_w(sl));
+    return XlaneSigns{__uint_as_float((w << 31) | 0x3F800000u),
+                      __uint_as_float(((w >> 2) << 31) | 0x3F800000u)};
+}
+// The register (group elements [16w, 16w+16)) that lane sl holds once the
+// transform is done: each digit of lane_w(sl) that is odd has its bit 1
+// flipped (d -> d ^ 2).
+__device__ __forceinline__ int lane_w_rot(int sl) {
+    const int w = lane_w(sl);
+    return w ^ ((w & 5) << 1);
 }
 
+// One step over the 16 registers: v[t] += s * v[t] of the DPP partner.  One
+// asm block, so the compiler places nothing between its instructions; it
+// starts and ends with two wait states (s_nop 1), which a DPP read of a VGPR
+// needs after the VALU write of it (the compiler cannot see the writes inside
+// an asm block, nor can it see that the block's DPP reads need them).
+#define XPU_FMAC_DPP(I, S, CTRL) \
+    "v_fmac_f32_dpp %" #I ", %" #I ", " S " " CTRL " row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+#define XPU_FMAC_DPP16(S, CTRL)                                                                    \
+    XPU_FMAC_DPP(0, S, CTRL) XPU_FMAC_DPP(1, S, CTRL) XPU_FMAC_DPP(2, S, CTRL)                     \
+    XPU_FMAC_DPP(3, S, CTRL) XPU_FMAC_DPP(4, S, CTRL) XPU_FMAC_DPP(5, S, CTRL)                     \
+    XPU_FMAC_DPP(6, S, CTRL) XPU_FMAC_DPP(7, S, CTRL) XPU_FMAC_DPP(8, S, CTRL)                     \
+    XPU_FMAC_DPP(9, S, CTRL) XPU_FMAC_DPP(10, S, CTRL) XPU_FMAC_DPP(11, S, CTRL)                   \
+    XPU_FMAC_DPP(12, S, CTRL) XPU_FMAC_DPP(13, S, CTRL) XPU_FMAC_DPP(14, S, CTRL)                  \
+    XPU_FMAC_DPP(15, S, CTRL)
+#define XPU_V16_OPERANDS(v)                                                                        \
+    "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]),           \
+        "+v"(v[7]), "+v"(v[8]), "+v"(v[9]), "+v"(v[10]), "+v"(v[11]), "+v"(v[12]), "+v"(v[13]),   \
+        "+v"(v[14]), "+v"(v[15])
+
+__device__ __forceinline__ void hadamard_xlane(float (&v)[16], const XlaneSigns& s) {
+    // axis 2: partners lane xor 1 (quad_perm [1,0,3,2]) and xor 3 ([3,2,1,0])
+    asm volatile("s_nop 1\n\t"
+                 XPU_FMAC_DPP16("%16", "quad_perm:[1,0,3,2]")
+                 XPU_FMAC_DPP16("-%16", "quad_perm:[3,2,1,0]")
+                 "s_nop 1"
+                 : XPU_V16_OPERANDS(v)
+                 : "v"(s.a2));
+    // axis 3: partners lane xor 7 (row_half_mirror) and xor 8 (row_ror:8)
+    asm volatile("s_nop 1\n\t"
+                 XPU_FMAC_DPP16("%16", "row_half_mirror")
+                 XPU_FMAC_DPP16("-%16", "row_ror:8")
+                 "s_nop 1"
+                 : XPU_V16_OPERANDS(v)
+                 : "v"(s.a3));
+}
+#undef XPU_FMAC_DPP
+#undef XPU_FMAC_DPP16
+#undef XPU_V16_OPERANDS
+
 // The full unscaled group transform: the true rotation is this times 1/16.
-__device__ __forceinline__ void hadamard16_unscaled(float (&v)[16]) {
+// Lane sl of a 16-lane segment enters with register lane_w(sl) and leaves
+// with register lane_w_rot(sl); s = xlane_signs(sl).
+__device__ __forceinline__ void hadamard16_unscaled(float (&v)[16], const XlaneSigns& s) {
     hadamard_inreg(v);
-    hadamard_xlane(v);
+    hadamard_xlane(v, s);
 }
 
 // --------------------------------------------------------------- reductions
@@ -183,6 +238,37 @@ __device__ __forceinline__ float segment_max(float x) {
 // low byte of (t + 1.5*2^23)'s bits is the two's-complement int8 of rint(t).
 __device__ __forceinline__ uint32_t rint_bits(float t) {
     return __float_as_uint(t + 12582912.0f);
+}
+// rint_bits of eight values, their low bytes packed into two dwords (element 0
+// lowest): each add writes its result's low byte straight into byte 0 or 1 of
+// a 16-bit half (SDWA dst_sel BYTE_0 zero-padded, then BYTE_1 with the rest
+// preserved) and a shift-or joins two halves: ten instructions for eight
+// values instead of eight adds and six byte permutes.  On gfx940 and later a
+// VALU result written with dst_sel other than DWORD must not be read by the
+// next instruction (the forwarded value is the unformatted result), so the
+// four halves are interleaved and every reader is at least two instructions
+// behind its writer; the compiler cannot see inside the block to do that.
+__device__ __forceinline__ uint2 rint_pack8(const float (&t)[8]) {
+    const float magic = 12582912.0f;
+    uint32_t h0, h1, h2, h3;
+    uint2 r;
+#define XPU_SDWA_ADD(D, S, SEL, UNUSED) \
+    "v_add_f32_sdwa %" #D ", %" #S ", %14 dst_sel:" SEL " dst_unused:" UNUSED " src0_sel:DWORD src1_sel:DWORD\n\t"
+    asm(XPU_SDWA_ADD(2, 6, "BYTE_0", "UNUSED_PAD")
+        XPU_SDWA_ADD(3, 8, "BYTE_0", "UNUSED_PAD")
+        XPU_SDWA_ADD(4, 10, "BYTE_0", "UNUSED_PAD")
+        XPU_SDWA_ADD(5, 12, "BYTE_0", "UNUSED_PAD")
+        XPU_SDWA_ADD(2, 7, "BYTE_1", "UNUSED_PRESERVE")
+        XPU_SDWA_ADD(3, 9, "BYTE_1", "UNUSED_PRESERVE")
+        XPU_SDWA_ADD(4, 11, "BYTE_1", "UNUSED_PRESERVE")
+        XPU_SDWA_ADD(5, 13, "BYTE_1", "UNUSED_PRESERVE")
+        "v_lshl_or_b32 %0, %3, 16, %2\n\t"
+        "v_lshl_or_b32 %1, %5, 16, %4"
+        : "=&v"(r.x), "=&v"(r.y), "=&v"(h0), "=&v"(h1), "=&v"(h2), "=&v"(h3)
+        : "v"(t[0]), "v"(t[1]), "v"(t[2]), "v"(t[3]), "v"(t[4]), "v"(t[5]), "v"(t[6]),
+          "v"(t[7]), "v"(magic));
+#undef XPU_SDWA_ADD
+    return r;
 }
 // Pack the low bytes of four such words into one dword (element 0 lowest).
 __device__ __forceinline__ uint32_t pack4(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {

@@ -6,7 +6,8 @@
 // lanes, each holding one 16-element register of it (elements [16w, 16w+16)
 // in lane L for w = lane_w(L), a permutation of the reference sub-group
 // kernel's w = L, src/xpuint8.cpp:406-438, that keeps every cross-lane
-// butterfly on DPP).  Row kernels
+// butterfly on DPP; after the transform the lane holds register
+// lane_w_rot(L), which is where its results are stored).  Row kernels
 // keep the whole row in registers across as many 16-lane segments as it needs
 // (rowquant_seg_kernel); rows too long for that use the two-pass variant, one
 // wave per row, which re-reads the row (from L2) to quantize it.
@@ -263,27 +264,33 @@ __device__ __forceinline__ float row_scale(int mode, float rowmax) {
 // case they are the unscaled Hadamard sums: the rotation is u/16).
 template <bool ROT, int MODE>
 __device__ __forceinline__ uint4 quant16(const float (&u)[16], float s, float inv) {
-    uint32_t b[16];
     if constexpr (MODE == kRecip) {
         // rint(fl(u/16) * inv) == rint(u * fl(inv/16)): both products are exact
         // power-of-two rescalings of the same rounded product.
         const float k = ROT ? inv * 0.0625f : inv;
+        float a[8], b[8];
 #pragma unroll
-        for (int t = 0; t < 16; ++t) b[t] = rint_bits(u[t] * k);
+        for (int t = 0; t < 8; ++t) {
+            a[t] = u[t] * k;
+            b[t] = u[t + 8] * k;
+        }
+        const uint2 lo = rint_pack8(a), hi = rint_pack8(b);
+        return make_uint4(lo.x, lo.y, hi.x, hi.y);
     } else {
+        uint32_t b[16];
 #pragma unroll
         for (int t = 0; t < 16; ++t) {
             float x = ROT ? u[t] * 0.0625f : u[t];
             if (MODE == kPrepare) x = bf16_round(x);
             b[t] = rint_bits(rint_div(x, s, inv));
         }
+        uint4 r;
+        r.x = pack4(b[0], b[1], b[2], b[3]);
+        r.y = pack4(b[4], b[5], b[6], b[7]);
+        r.z = pack4(b[8], b[9], b[10], b[11]);
+        r.w = pack4(b[12], b[13], b[14], b[15]);
+        return r;
     }
-    uint4 r;
-    r.x = pack4(b[0], b[1], b[2], b[3]);
-    r.y = pack4(b[4], b[5], b[6], b[7]);
-    r.z = pack4(b[8], b[9], b[10], b[11]);
-    r.w = pack4(b[12], b[13], b[14], b[15]);
-    return r;
 }
 
 // Running max of |u| over 16 raw values (unscaled Hadamard sums when ROT).
@@ -304,8 +311,8 @@ __device__ __forceinline__ float finish_max(float raw) {
 }
 
 // Segmented row kernel.  A segment is 16 lanes holding P (1 or 2) whole
-// 256-groups of one row (lane L of the segment holds register lane_w(L) of
-// each of its groups); a row is S = G/P consecutive segments and a block is
+// 256-groups of one row (lane L of the segment loads register lane_w(L) of
+// each of its groups and stores register lane_w_rot(L)); a row is S = G/P consecutive segments and a block is
 // R whole rows, so R*S*16 threads (rounded up to whole waves with idle
 // padding segments).  The row is register-resident (16P floats per lane):
 // the group maxima are reduced inside the segment with DPP, combined across
@@ -342,6 +349,7 @@ __global__ __launch_bounds__(1024) void rowquant_seg_kernel(Loader load, int8_t*
     const Loader lb = load.rebase(row0);
     int col[P];
     typename Loader::Raw raw[P];
+    const XlaneSigns sgn = xlane_signs(sl);
 #pragma unroll
     for (int p = 0; p < P; ++p) {
         col[p] = (sg * P + p) * kGroup + lane_w(sl) * 16;
@@ -359,7 +367,7 @@ __global__ __launch_bounds__(1024) void rowquant_seg_kernel(Loader load, int8_t*
 #pragma unroll
     for (int p = 0; p < P; ++p) {
         lb.expand(raw[p], v[p]);
-        if constexpr (ROT) hadamard16_unscaled(v[p]);
+        if constexpr (ROT) hadamard16_unscaled(v[p], sgn);
         m = absmax16(v[p], m);
     }
     // m >= 0 (never NaN), so its bit pattern orders like its value
@@ -372,10 +380,12 @@ __global__ __launch_bounds__(1024) void rowquant_seg_kernel(Loader load, int8_t*
     const float inv = 1.0f / sc;
     if (sg == 0 && sl == 0) scale[row0 + r] = sc;
     int8_t* const qrow = q + row0 * K;
+    // the transform leaves register lane_w_rot(sl) of the group in the lane
+    const int dcol = ROT ? (lane_w_rot(sl) - lane_w(sl)) * 16 : 0;
 #pragma unroll
     for (int p = 0; p < P; ++p) {
         const uint4 w = quant16<ROT, MODE>(v[p], sc, inv);
-        if (FULL || col[p] < K) *reinterpret_cast<uint4*>(at32(qrow, r, K, col[p])) = w;
+        if (FULL || col[p] < K) *reinterpret_cast<uint4*>(at32(qrow, r, K, col[p] + dcol)) = w;
     }
 }
 
@@ -389,16 +399,18 @@ __global__ __launch_bounds__(256) void rowquant_2pass_kernel(Loader load, int8_t
     const int64_t row = int64_t(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6);
     if (row >= M) return;
     const int slots = (K + 1023) / 1024;
+    const XlaneSigns sgn = xlane_signs(lane & 15);
+    const int w_in = lane_w(lane & 15), w_st = ROT ? lane_w_rot(lane & 15) : w_in;
     float m = 0.f;
     for (int s = 0; s < slots; ++s) {
         float v[16];
-        const int col = s * 1024 + (lane >> 4) * kGroup + lane_w(lane & 15) * 16;
+        const int col = s * 1024 + (lane >> 4) * kGroup + w_in * 16;
         if (col < K) load(row, col, v);
         else {
 #pragma unroll
             for (int t = 0; t < 16; ++t) v[t] = 0.f;
         }
-        if constexpr (ROT) hadamard16_unscaled(v);
+        if constexpr (ROT) hadamard16_unscaled(v, sgn);
         m = absmax16(v, m);
     }
     const float rowmax = finish_max<ROT, MODE>(wave_max(m));
@@ -407,15 +419,16 @@ __global__ __launch_bounds__(256) void rowquant_2pass_kernel(Loader load, int8_t
     if (lane == 0) scale[row] = sc;
     for (int s = 0; s < slots; ++s) {
         float v[16];
-        const int col = s * 1024 + (lane >> 4) * kGroup + lane_w(lane & 15) * 16;
+        const int col = s * 1024 + (lane >> 4) * kGroup + w_in * 16;
         if (col < K) load(row, col, v);
         else {
 #pragma unroll
             for (int t = 0; t < 16; ++t) v[t] = 0.f;
         }
-        if constexpr (ROT) hadamard16_unscaled(v);
+        if constexpr (ROT) hadamard16_unscaled(v, sgn);
         const uint4 r = quant16<ROT, MODE>(v, sc, inv);
-        if (col < K) *reinterpret_cast<uint4*>(q + row * K + col) = r;
+        const int cst = col + (w_st - w_in) * 16;   // same 256-group as col
+        if (cst < K) *reinterpret_cast<uint4*>(q + row * K + cst) = r;
     }
 }
 
@@ -487,15 +500,18 @@ template <class Loader>
 __global__ __launch_bounds__(256) void rotate_kernel(Loader load, uint16_t* __restrict__ out,
                                                      int64_t M, int K) {
     const int sl = threadIdx.x & 15;
+    const XlaneSigns sgn = xlane_signs(sl);
+    const int w_out = lane_w_rot(sl);
     const int64_t G = K / kGroup;
     const int64_t total = M * G;
     for (int64_t g = int64_t(blockIdx.x) * 16 + (threadIdx.x >> 4); g < total;
          g += int64_t(gridDim.x) * 16) {
         const int64_t row = g / G;
-        const int col = int(g - row * G) * kGroup + lane_w(sl) * 16;
+        const int gcol = int(g - row * G) * kGroup;
         float v[16];
-        load(row, col, v);
-        hadamard16_unscaled(v);
+        load(row, gcol + lane_w(sl) * 16, v);
+        hadamard16_unscaled(v, sgn);
+        const int col = gcol + w_out * 16;
         uint4 a, b;
         a.x = pack_bf16x2(v[0] * 0.0625f, v[1] * 0.0625f);
         a.y = pack_bf16x2(v[2] * 0.0625f, v[3] * 0.0625f);
@@ -513,7 +529,7 @@ __global__ __launch_bounds__(256) void rotate_kernel(Loader load, uint16_t* __re
 
 // The loop exit can differ between the segments of a wave on the last step;
 // that is safe because the butterfly only exchanges lanes inside a segment
-// (DPP quad_perm and ds_swizzle xor 4/8), whose 16 lanes always share g.
+// (DPP lane xors 1, 3, 7 and 8), whose 16 lanes always share g.
 template <class Loader>
 hipError_t launch_rotate(hipStream_t st, const Loader& ld, uint16_t* out, int64_t M, int K) {
     const int64_t groups = M * (K / kGroup);
