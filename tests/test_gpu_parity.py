@@ -373,7 +373,7 @@ def test_ffn_full_size_c4(dev):
 
 
 @pytest.mark.parametrize("m,n,k", [(4096, 5120, 1280), (1000, 272, 208), (1, 16, 16),
-                                   (77, 1280, 4096)])
+                                   (77, 1280, 4096), (300, 2000, 2000), (33, 2400, 1600)])
 def test_linear_dw(dev, m, n, k):
     """dL/dW = dy^T x through the bf16 MFMA kernel, against float64: each
     element within one bf16 rounding of the exact value plus the fp32
