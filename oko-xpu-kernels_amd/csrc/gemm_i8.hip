@@ -700,7 +700,8 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_pp_kernel(
     constexpr int PER0 = PER, PER1 = REM == 0 ? PER : PER - 1;
     constexpr int STAGE_BYTES = NB * 1024;
     constexpr int RING = S * STAGE_BYTES;
-    static_assert(S == 4, "slot 0 stages the epilogue while the next tile's steps 0-2 fill 1-3");
+    static_assert(S == 4, "a tile's last slot stages the epilogue while the next tile's steps 0-2 "
+                          "fill the other three");
     constexpr bool STAGED = Epi::kStaged;
     static_assert(!STAGED || NW * 16 * 256 <= STAGE_BYTES, "epilogue staging fits in one slot");
     constexpr bool PAIRED = Epi::kPaired;
@@ -740,11 +741,18 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_pp_kernel(
     // DMA: wave w brings blocks w, w + NW, ... of every step; lane l row l/4,
     // chunk swz(l/4, l%4).  Rows past M or N repeat the last row (their
     // results are never stored).  The 32-bit offsets keep the saddr form.
-    const int lr = lane >> 2;
-    const int lc = swz(lr, lane & 3) * 16;
     const int8_t* base[PER];
     int off[PER];
+    // K offset of this lane's 16-byte chunk, for the zero fill past K
+    const int lc_tail = KTAIL ? swz(lane >> 2, lane & 3) * 16 : 0;
     auto setup = [&](int m0, int n0) {
+        // the lane index is formed afresh here (an asm the compiler cannot
+        // merge with the kernel's other lane values), so nothing per-lane has
+        // to stay live across the K loops for the next tile's setup
+        int ln;
+        asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(ln));
+        const int lr = ln >> 2;
+        const int lc = swz(lr, ln & 3) * 16;
         const int8_t* const xbase = X + int64_t(m0) * ldx;
         const int8_t* const wbase = W + int64_t(n0) * ldw;
         const int8_t* const gbase = W + (int64_t(pair_offset(epi)) + n0) * ldw;
@@ -765,19 +773,25 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_pp_kernel(
         }
     };
     const int KT = (K + BK - 1) / BK;
-    auto slot = [&](int kk) { return ((kk + 1) % S) * STAGE_BYTES; };
-    // this wave's loads for step kk (its share of the stage's blocks)
-    auto issue = [&](int kk) {
-        const int k0 = kk * BK;
+    // The ring runs on across tiles: a block's steps are numbered on from
+    // tile to tile, and step kk of the current tile (whose first step has
+    // number kb) lives in slot (kb + kk + 1) % S; ring0 = kb % S.
+    int ring0 = 0;
+    auto slot = [&](int kk) { return ((ring0 + kk + 1) & (S - 1)) * STAGE_BYTES; };
+    // this wave's loads for ring position kk (its share of the stage's
+    // blocks), from K offset kstep * BK of the tile set up last
+    auto issue_at = [&](int kk, int kstep) {
+        const int k0 = kstep * BK;
         int8_t* const st = smem + slot(kk);
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
             if (i == PER - 1 && REM != 0 && g != 0) continue;
             const int8_t* p = base[i] + uint64_t(uint32_t(off[i] + k0));
-            if (KTAIL && k0 + lc >= K) p = g_zero16;
+            if (KTAIL && k0 + lc_tail >= K) p = g_zero16;
             dma16(p, st + (wave + NW * i) * 1024);
         }
     };
+    auto issue = [&](int kk) { issue_at(kk, kk); };
     // wait until this wave's loads of every step before `later` more of its
     // own load batches are complete
     auto wait_batches = [&](int later) {
@@ -860,9 +874,11 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_pp_kernel(
                 else
                     ccol[a] = epi.col_lds(sc + BM, BN_OUT, wn * WN_OUT + 16 * a + 4 * (lane >> 4), 0);
             }
+            // staged through the slot of the tile's last step (the other
+            // three hold the next tile's first steps)
             staged_store<TM, TN, WN_OUT, Epi, 1>(epi, acc, [&](int b) { return xr[16 * b]; }, ccol,
-                                                 smem + wave * (16 * 256), m0 + wm * WM,
-                                                 n0 + wn * WN_OUT, M, N, lane);
+                                                 smem + slot(KT - 1) + wave * (16 * 256),
+                                                 m0 + wm * WM, n0 + wn * WN_OUT, M, N, lane);
         } else {
             const int mrow = m0 + wm * WM + (lane & 15);
             const int ncol = n0 + wn * WN + 4 * (lane >> 4);
@@ -896,6 +912,20 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_pp_kernel(
         for (int a = 0; a < TN; ++a)
 #pragma unroll
             for (int b = 0; b < TM; ++b) acc[a][b] = v4i{0, 0, 0, 0};
+        const int tnext = ti + int(gridDim.x);
+        const bool more = tnext < tiles;
+        int m0n = 0, n0n = 0;
+        if (more) tile_origin(tnext, m0n, n0n);
+        // With a next tile (and K steps enough), the loads of its steps 0-2
+        // go out in this tile's last three steps, in the ring positions where
+        // steps KT..KT+2 would go: the loop's loads never stop at the tile
+        // boundary.  Every wait then has the usual number of later batches.
+        const bool cont = more && KT >= S - 1;
+        // the loop runs in two parts: steps 0 .. KT-S (this tile's loads, as
+        // long as there are any) and, with cont, steps KT-S+1 .. KT-1 (the next
+        // tile's loads, after setup() has switched the load addresses), so no
+        // branch on the tile boundary sits inside either loop
+        const int kmain = cont ? KT - (S - 1) : KT;
         // group 0 reads step 0's fragments; each group then runs its own loop
         // of (first half, barrier, second half, barrier), group 0 a half step
         // ahead
@@ -903,7 +933,7 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_pp_kernel(
             read_frags(0);
             barrier();
 #pragma clang loop unroll(disable)
-            for (int k = 0; k < KT; ++k) {
+            for (int k = 0; k < kmain; ++k) {
                 compute();                                      // A(k)
                 if (k + 1 < KT) wait_batches(min(S - 3, KT - 2 - k));
                 barrier();
@@ -911,10 +941,22 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_pp_kernel(
                 if (k + S - 1 < KT) issue(k + S - 1);
                 barrier();
             }
+            if (cont) {
+                setup(m0n, n0n);
+#pragma clang loop unroll(disable)
+                for (int k = kmain; k < KT; ++k) {
+                    compute();                                  // A(k)
+                    if (k + 1 < KT) wait_batches(S - 3);
+                    barrier();
+                    if (k + 1 < KT) read_frags(k + 1);          // B(k)
+                    issue_at(k + S - 1, k + S - 1 - KT);
+                    barrier();
+                }
+            }
         } else {
             barrier();
 #pragma clang loop unroll(disable)
-            for (int k = 0; k < KT; ++k) {
+            for (int k = 0; k < kmain; ++k) {
                 read_frags(k);                                  // A(k)
                 if (k + S - 1 < KT) issue(k + S - 1);
                 if (k + 1 < KT) wait_batches(min(S - 2, KT - 2 - k));
@@ -922,24 +964,36 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_pp_kernel(
                 compute();                                      // B(k)
                 barrier();
             }
+            if (cont) {
+                setup(m0n, n0n);
+#pragma clang loop unroll(disable)
+                for (int k = kmain; k < KT; ++k) {
+                    read_frags(k);                              // A(k)
+                    issue_at(k + S - 1, k + S - 1 - KT);
+                    if (k + 1 < KT) wait_batches(S - 2);
+                    barrier();
+                    compute();                                  // B(k)
+                    barrier();
+                }
+            }
         }
-        // every fragment read has completed: the next tile's first steps and
-        // operands go out ahead of this tile's stores
-        const int tnext = ti + int(gridDim.x);
-        const bool more = tnext < tiles;
-        int m0n = 0, n0n = 0;
+        // every fragment read has completed: the next tile's operands (and,
+        // with too few K steps for the loop to have issued them, its first
+        // steps) go out ahead of this tile's stores
         if (more) {
-            tile_origin(tnext, m0n, n0n);
-            setup(m0n, n0n);
+            if (!cont) {
+                setup(m0n, n0n);
+                for (int kk = 0; kk < S - 1; ++kk)
+                    if (kk < KT) issue_at(KT + kk, kk);
+            }
             fetch_scales(m0n, n0n);
-            for (int kk = 0; kk < S - 1; ++kk)
-                if (kk < KT) issue(kk);
         }
         epilogue(m0, n0, it & 1);
         if (!more) break;
         __builtin_amdgcn_s_waitcnt(0);                          // stores, loads, LDS all done
         put_scales((it + 1) & 1);
         barrier();
+        ring0 = (ring0 + KT) & (S - 1);
         ti = tnext;
         m0 = m0n;
         n0 = n0n;

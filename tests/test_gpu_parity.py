@@ -58,13 +58,17 @@ def test_int8_gemm_full_size_c3(dev):
     assert np.array_equal(got, O.int_mm(a, b))
 
 
-@pytest.mark.parametrize("m,n,k", [(2100, 10000, 1040), (4300, 6000, 272)])
+@pytest.mark.parametrize("m,n,k", [(2100, 10000, 1040), (4300, 6000, 272), (4352, 5120, 128),
+                                   (4352, 5120, 192), (4096, 15360, 320)])
 def test_persistent_tiles_exact(dev, m, n, k):
     """Shapes that take the persistent 256x320 kernel (one block per CU
     looping over tiles): ragged last row and column tiles, K not a multiple of
-    64, and 288 / 323 tiles, so some blocks run two tiles and others one.  The
-    int32 product, then the dequant epilogue (fp32 bias, then bf16 bias) on
-    the same operands."""
+    64, and 288 / 323 / 272 tiles, so some blocks run two tiles and others
+    one; two K steps (the next tile's loads issued between the tiles) and
+    three (all of them issued from the previous tile's loop); 768 tiles of
+    five K steps, three per block, so the LDS ring starts each tile at a
+    different slot.  The int32 product, then the dequant epilogue (fp32
+    bias, then bf16 bias) on the same operands."""
     rng = np.random.default_rng(m + n + k)
     a = rng.integers(-127, 128, (m, k), dtype=np.int8)
     b = rng.integers(-127, 128, (n, k), dtype=np.int8)
