@@ -40,6 +40,12 @@ CASES = [
     (2, 64, 3, 256, False, 2, 64, 3 * 256),
     (3, 5, 1, 2, True, 1, 1, 2),
     (2, 33, 7, 96, True, 2, 1, 7 * 96 + 16),
+    # the 16-byte vector kernel (D = 64 or 128): interleaved pairs, a partial
+    # last wave of heads, broadcast rotations, a padded accumulator row
+    (2, 64, 5, 128, False, 1, 64, 5 * 128),
+    (1, 128, 24, 64, True, 1, 1, 3 * 24 * 64),
+    (2, 40, 9, 64, False, 2, 40, 9 * 64 + 64),
+    (1, 16, 64, 128, True, 1, 16, 64 * 128),
 ]
 
 
