@@ -1031,10 +1031,29 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_splitk_kernel(
     static_assert(S >= 3 && S <= 4, "three or four stages");
     __shared__ __attribute__((aligned(1024))) int8_t smem[2 * RING];
 
-    const int tiles = tiles_m * tiles_n;
-    int t = blockIdx.x;
-    if (tiles % 8 == 0) t = (t % 8) * (tiles / 8) + t / 8;
-    const int m0 = (t % tiles_m) * BM, n0 = (t / tiles_m) * BN;
+    // Blocks are dispatched to the 8 XCDs round robin (block b on b % 8),
+    // each with its own L2: give every XCD a gx x (8 / gx) block of the tile
+    // grid, with gx chosen so that it reads the fewest operand rows (at the
+    // FFN's down-projection, 32 x 8 tiles: 8 x 4 tiles per XCD, X and W read
+    // 4 and 2 times over instead of X 8 times).
+    int tmi = blockIdx.x % tiles_m, tni = blockIdx.x / tiles_m;
+    {
+        int best = 0, cost = 0;
+        for (int gx = 1; gx <= 8; gx *= 2) {
+            const int gy = 8 / gx;
+            if (tiles_m % gx || tiles_n % gy) continue;
+            const int c = (tiles_m / gx) * BM + (tiles_n / gy) * BN;
+            if (!best || c < cost) best = gx, cost = c;
+        }
+        if (best) {
+            const int x = blockIdx.x % 8, j = blockIdx.x / 8;
+            const int lm = tiles_m / best;                      // row tiles per XCD
+            const int ln = tiles_n / (8 / best);
+            tmi = (x % best) * lm + j % lm;
+            tni = (x / best) * ln + j / lm;
+        }
+    }
+    const int m0 = tmi * BM, n0 = tni * BN;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int team = wave >> 2, wt = wave & 3;
