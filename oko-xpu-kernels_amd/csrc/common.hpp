@@ -5,13 +5,18 @@
 // src/xpuint8.cpp (cited per routine).  Files that include this header are
 // compiled with -ffp-contract=off, so no multiply-add is ever fused.
 //
-// The Hadamard is evaluated *unscaled*: each of the four radix-4 axes adds and
-// subtracts without the reference's factor 0.5, and the product 1/16 of the
-// four factors is applied once at the end (or folded into the quantizer's
-// reciprocal).  Scaling by a power of two commutes with IEEE rounding whenever
-// no intermediate is subnormal or overflows, so for every input whose nonzero
-// magnitudes lie in [2^-110, 2^120] the result equals the reference's
-// ((0.5*a + 0.5*b) + ...) chains exactly.
+// The Hadamard is evaluated *unscaled* on the fast path: each of the four
+// radix-4 axes adds and subtracts without the reference's factor 0.5, and the
+// product 1/16 of the four factors is applied once at the end (or folded into
+// the quantizer's reciprocal).  Scaling by a power of two commutes with IEEE
+// rounding unless a result overflows or rounds in the subnormal range.  The
+// second cannot happen: the inputs are bf16 values (multiples of 2^-133), every
+// intermediate of either order is a multiple of 2^-137, and a sum of such
+// multiples that falls below 2^-126 is exact.  The first is excluded by the
+// input range: with every |x| < 2^120 an unscaled intermediate is at most
+// 256*max|x| < 2^128.  Groups with an input at or above 2^120 (or an inf) take
+// hadamard16_scaled, which is the reference's own operation order, factors of
+// 0.5 included, and so overflows exactly where the reference does.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -170,21 +175,27 @@ __device__ __forceinline__ int lane_w_rot(int sl) {
         "+v"(v[7]), "+v"(v[8]), "+v"(v[9]), "+v"(v[10]), "+v"(v[11]), "+v"(v[12]), "+v"(v[13]),   \
         "+v"(v[14]), "+v"(v[15])
 
-__device__ __forceinline__ void hadamard_xlane(float (&v)[16], const XlaneSigns& s) {
-    // axis 2: partners lane xor 1 (quad_perm [1,0,3,2]) and xor 3 ([3,2,1,0])
+// axis 2: partners lane xor 1 (quad_perm [1,0,3,2]) and xor 3 ([3,2,1,0])
+__device__ __forceinline__ void hadamard_axis2(float (&v)[16], const XlaneSigns& s) {
     asm volatile("s_nop 1\n\t"
                  XPU_FMAC_DPP16("%16", "quad_perm:[1,0,3,2]")
                  XPU_FMAC_DPP16("-%16", "quad_perm:[3,2,1,0]")
                  "s_nop 1"
                  : XPU_V16_OPERANDS(v)
                  : "v"(s.a2));
-    // axis 3: partners lane xor 7 (row_half_mirror) and xor 8 (row_ror:8)
+}
+// axis 3: partners lane xor 7 (row_half_mirror) and xor 8 (row_ror:8)
+__device__ __forceinline__ void hadamard_axis3(float (&v)[16], const XlaneSigns& s) {
     asm volatile("s_nop 1\n\t"
                  XPU_FMAC_DPP16("%16", "row_half_mirror")
                  XPU_FMAC_DPP16("-%16", "row_ror:8")
                  "s_nop 1"
                  : XPU_V16_OPERANDS(v)
                  : "v"(s.a3));
+}
+__device__ __forceinline__ void hadamard_xlane(float (&v)[16], const XlaneSigns& s) {
+    hadamard_axis2(v, s);
+    hadamard_axis3(v, s);
 }
 #undef XPU_FMAC_DPP
 #undef XPU_FMAC_DPP16
@@ -196,6 +207,50 @@ __device__ __forceinline__ void hadamard_xlane(float (&v)[16], const XlaneSigns&
 __device__ __forceinline__ void hadamard16_unscaled(float (&v)[16], const XlaneSigns& s) {
     hadamard_inreg(v);
     hadamard_xlane(v, s);
+}
+
+__device__ __forceinline__ void halve16(float (&v)[16]) {
+#pragma unroll
+    for (int t = 0; t < 16; ++t) v[t] *= 0.5f;
+}
+
+// The same transform in the reference's scaled operation order, giving the
+// true rotation (no final 1/16).  Axes 0 and 1 multiply their inputs by the
+// coefficients +-0.5 and then chain (src/xpuint8.cpp:290-301): the product by
+// 0.5 is exact and the sign is the chain's add or subtract, so it is halve16
+// then h4_chain.  Axes 2 and 3 form (p + n) * 0.5 with p, n unscaled sums
+// (bfly4, src/xpuint8.cpp:279-285): the butterfly, then halve16.  This is the
+// path for groups the fast form could overflow on; see the header comment.
+__device__ __forceinline__ void hadamard16_scaled(float (&v)[16], const XlaneSigns& s) {
+    halve16(v);
+#pragma unroll
+    for (int b = 0; b < 16; b += 4) h4_chain(v[b], v[b + 1], v[b + 2], v[b + 3]);
+    halve16(v);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) h4_chain(v[c], v[c + 4], v[c + 8], v[c + 12]);
+    hadamard_axis2(v, s);
+    halve16(v);
+    hadamard_axis3(v, s);
+    halve16(v);
+}
+
+// Inputs at or above this magnitude (or an inf) send a group to the scaled
+// transform: below it, 256 * max|x| < 2^128 bounds every unscaled intermediate.
+constexpr float kUnscaledLimit = 0x1p120f;
+
+// Max |x| over a lane's 16 inputs; NaN inputs are ignored (fmaxf), and a NaN
+// propagates through either transform the same way.
+__device__ __forceinline__ float inmax16(const float (&v)[16], float m) {
+#pragma unroll
+    for (int t = 0; t < 16; ++t) m = fmaxf(m, fabsf(v[t]));
+    return m;
+}
+
+// Whether any lane of the wave holds a group that needs the scaled transform.
+// The result is wave-uniform, so the branch on it keeps every lane of a
+// segment (and the DPP partners of each lane) on the same path.
+__device__ __forceinline__ bool wave_needs_scaled(float inmax) {
+    return __builtin_amdgcn_ballot_w64(!(inmax < kUnscaledLimit)) != 0;
 }
 
 // --------------------------------------------------------------- reductions

@@ -260,14 +260,15 @@ __device__ __forceinline__ float row_scale(int mode, float rowmax) {
     return fmaxf(rowmax / 127.0f, 1e-30f);
 }
 
-// Quantize 16 values (already in their final scaled form unless ROT, in which
-// case they are the unscaled Hadamard sums: the rotation is u/16).
+// Quantize 16 values: the values themselves unless ROT, in which case the
+// rotation is u * dom (dom = 1/16 for the unscaled transform's sums, 1 for the
+// scaled one's).
 template <bool ROT, int MODE>
-__device__ __forceinline__ uint4 quant16(const float (&u)[16], float s, float inv) {
+__device__ __forceinline__ uint4 quant16(const float (&u)[16], float s, float inv, float dom) {
     if constexpr (MODE == kRecip) {
         // rint(fl(u/16) * inv) == rint(u * fl(inv/16)): both products are exact
         // power-of-two rescalings of the same rounded product.
-        const float k = ROT ? inv * 0.0625f : inv;
+        const float k = ROT ? inv * dom : inv;
         float a[8], b[8];
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
@@ -280,7 +281,7 @@ __device__ __forceinline__ uint4 quant16(const float (&u)[16], float s, float in
         uint32_t b[16];
 #pragma unroll
         for (int t = 0; t < 16; ++t) {
-            float x = ROT ? u[t] * 0.0625f : u[t];
+            float x = ROT ? u[t] * dom : u[t];
             if (MODE == kPrepare) x = bf16_round(x);
             b[t] = rint_bits(rint_div(x, s, inv));
         }
@@ -293,19 +294,40 @@ __device__ __forceinline__ uint4 quant16(const float (&u)[16], float s, float in
     }
 }
 
-// Running max of |u| over 16 raw values (unscaled Hadamard sums when ROT).
+// Running max of |u| over 16 raw values.
 __device__ __forceinline__ float absmax16(const float (&u)[16], float m) {
 #pragma unroll
     for (int t = 0; t < 16; ++t) m = fmaxf(m, fabsf(u[t]));
     return m;
 }
 
-// The row max of the values the quantizer sees, from the max of the raw
-// ones: f(max|u|) == max f(|u|) for the monotone non-decreasing
-// f(u) = u/16 (ROT) and bf16 rounding (kPrepare), so one application suffices.
-template <bool ROT, int MODE>
-__device__ __forceinline__ float finish_max(float raw) {
-    float x = ROT ? raw * 0.0625f : raw;
+// Rotate one lane's register of each of its P groups in place, choosing the
+// transform for the whole wave: the unscaled one unless some input of the
+// wave is at or above kUnscaledLimit (common.hpp), then the reference's scaled
+// one.  Returns dom, the factor from the values left in v to the rotation
+// (1/16 or 1), which the callers apply to the row max and in the quantizer;
+// both products are exact (a power of two on a value that neither overflows
+// nor rounds in the subnormal range).
+template <int P>
+__device__ __forceinline__ float rotate_groups(float (&v)[P][16], const XlaneSigns& sgn) {
+    float mi = 0.f;
+#pragma unroll
+    for (int p = 0; p < P; ++p) mi = inmax16(v[p], mi);
+    if (__builtin_expect(wave_needs_scaled(mi), 0)) {
+#pragma unroll
+        for (int p = 0; p < P; ++p) hadamard16_scaled(v[p], sgn);
+        return 1.0f;
+    }
+#pragma unroll
+    for (int p = 0; p < P; ++p) hadamard16_unscaled(v[p], sgn);
+    return 0.0625f;
+}
+
+// The row max of the values the quantizer sees, from the max of the rotated
+// (or, without ROT, raw) ones: bf16 rounding (kPrepare) is monotone
+// non-decreasing, so f(max|u|) == max f(|u|) and one application suffices.
+template <int MODE>
+__device__ __forceinline__ float finish_max(float x) {
     if (MODE == kPrepare) x = bf16_round(x);
     return x;
 }
@@ -363,20 +385,21 @@ __global__ __launch_bounds__(1024) void rowquant_seg_kernel(Loader load, int8_t*
     if (threadIdx.x < R) row_max[threadIdx.x] = 0u;
     lds_barrier();                               // the zeros land before any max
     float v[P][16];
+#pragma unroll
+    for (int p = 0; p < P; ++p) lb.expand(raw[p], v[p]);
+    float dom = 1.0f;
+    if constexpr (ROT) dom = rotate_groups<P>(v, sgn);
     float m = 0.f;
 #pragma unroll
-    for (int p = 0; p < P; ++p) {
-        lb.expand(raw[p], v[p]);
-        if constexpr (ROT) hadamard16_unscaled(v[p], sgn);
-        m = absmax16(v[p], m);
-    }
+    for (int p = 0; p < P; ++p) m = absmax16(v[p], m);
+    if constexpr (ROT) m *= dom;
     // m >= 0 (never NaN), so its bit pattern orders like its value
     const uint32_t mb = segment_max_bits(__float_as_uint(m));
     if (live && sl == 0) atomicMax(&row_max[r], mb);
     lds_barrier();
     if (!live) return;
     const float rowmax = __uint_as_float(row_max[r]);
-    const float sc = row_scale(MODE, finish_max<ROT, MODE>(rowmax));
+    const float sc = row_scale(MODE, finish_max<MODE>(rowmax));
     const float inv = 1.0f / sc;
     if (sg == 0 && sl == 0) scale[row0 + r] = sc;
     int8_t* const qrow = q + row0 * K;
@@ -384,7 +407,7 @@ __global__ __launch_bounds__(1024) void rowquant_seg_kernel(Loader load, int8_t*
     const int dcol = ROT ? (lane_w_rot(sl) - lane_w(sl)) * 16 : 0;
 #pragma unroll
     for (int p = 0; p < P; ++p) {
-        const uint4 w = quant16<ROT, MODE>(v[p], sc, inv);
+        const uint4 w = quant16<ROT, MODE>(v[p], sc, inv, dom);
         if (FULL || col[p] < K) *reinterpret_cast<uint4*>(at32(qrow, r, K, col[p] + dcol)) = w;
     }
 }
@@ -403,30 +426,35 @@ __global__ __launch_bounds__(256) void rowquant_2pass_kernel(Loader load, int8_t
     const int w_in = lane_w(lane & 15), w_st = ROT ? lane_w_rot(lane & 15) : w_in;
     float m = 0.f;
     for (int s = 0; s < slots; ++s) {
-        float v[16];
+        float v[1][16];
         const int col = s * 1024 + (lane >> 4) * kGroup + w_in * 16;
-        if (col < K) load(row, col, v);
+        if (col < K) load(row, col, v[0]);
         else {
 #pragma unroll
-            for (int t = 0; t < 16; ++t) v[t] = 0.f;
+            for (int t = 0; t < 16; ++t) v[0][t] = 0.f;
         }
-        if constexpr (ROT) hadamard16_unscaled(v, sgn);
-        m = absmax16(v, m);
+        if constexpr (ROT) {
+            const float dom = rotate_groups<1>(v, sgn);
+            m = fmaxf(m, absmax16(v[0], 0.f) * dom);
+        } else {
+            m = absmax16(v[0], m);
+        }
     }
-    const float rowmax = finish_max<ROT, MODE>(wave_max(m));
+    const float rowmax = finish_max<MODE>(wave_max(m));
     const float sc = row_scale(MODE, rowmax);
     const float inv = 1.0f / sc;
     if (lane == 0) scale[row] = sc;
     for (int s = 0; s < slots; ++s) {
-        float v[16];
+        float v[1][16];
         const int col = s * 1024 + (lane >> 4) * kGroup + w_in * 16;
-        if (col < K) load(row, col, v);
+        if (col < K) load(row, col, v[0]);
         else {
 #pragma unroll
-            for (int t = 0; t < 16; ++t) v[t] = 0.f;
+            for (int t = 0; t < 16; ++t) v[0][t] = 0.f;
         }
-        if constexpr (ROT) hadamard16_unscaled(v, sgn);
-        const uint4 r = quant16<ROT, MODE>(v, sc, inv);
+        float dom = 1.0f;
+        if constexpr (ROT) dom = rotate_groups<1>(v, sgn);
+        const uint4 r = quant16<ROT, MODE>(v[0], sc, inv, dom);
         const int cst = col + (w_st - w_in) * 16;   // same 256-group as col
         if (cst < K) *reinterpret_cast<uint4*>(q + row * K + cst) = r;
     }
@@ -508,19 +536,20 @@ __global__ __launch_bounds__(256) void rotate_kernel(Loader load, uint16_t* __re
          g += int64_t(gridDim.x) * 16) {
         const int64_t row = g / G;
         const int gcol = int(g - row * G) * kGroup;
-        float v[16];
-        load(row, gcol + lane_w(sl) * 16, v);
-        hadamard16_unscaled(v, sgn);
+        float v[1][16];
+        load(row, gcol + lane_w(sl) * 16, v[0]);
+        const float dom = rotate_groups<1>(v, sgn);
+        const float* u = v[0];
         const int col = gcol + w_out * 16;
         uint4 a, b;
-        a.x = pack_bf16x2(v[0] * 0.0625f, v[1] * 0.0625f);
-        a.y = pack_bf16x2(v[2] * 0.0625f, v[3] * 0.0625f);
-        a.z = pack_bf16x2(v[4] * 0.0625f, v[5] * 0.0625f);
-        a.w = pack_bf16x2(v[6] * 0.0625f, v[7] * 0.0625f);
-        b.x = pack_bf16x2(v[8] * 0.0625f, v[9] * 0.0625f);
-        b.y = pack_bf16x2(v[10] * 0.0625f, v[11] * 0.0625f);
-        b.z = pack_bf16x2(v[12] * 0.0625f, v[13] * 0.0625f);
-        b.w = pack_bf16x2(v[14] * 0.0625f, v[15] * 0.0625f);
+        a.x = pack_bf16x2(u[0] * dom, u[1] * dom);
+        a.y = pack_bf16x2(u[2] * dom, u[3] * dom);
+        a.z = pack_bf16x2(u[4] * dom, u[5] * dom);
+        a.w = pack_bf16x2(u[6] * dom, u[7] * dom);
+        b.x = pack_bf16x2(u[8] * dom, u[9] * dom);
+        b.y = pack_bf16x2(u[10] * dom, u[11] * dom);
+        b.z = pack_bf16x2(u[12] * dom, u[13] * dom);
+        b.w = pack_bf16x2(u[14] * dom, u[15] * dom);
         uint4* p = reinterpret_cast<uint4*>(out + row * K + col);
         p[0] = a;
         p[1] = b;
@@ -529,7 +558,8 @@ __global__ __launch_bounds__(256) void rotate_kernel(Loader load, uint16_t* __re
 
 // The loop exit can differ between the segments of a wave on the last step;
 // that is safe because the butterfly only exchanges lanes inside a segment
-// (DPP lane xors 1, 3, 7 and 8), whose 16 lanes always share g.
+// (DPP lane xors 1, 3, 7 and 8), whose 16 lanes always share g, and the
+// choice of transform is a ballot over the lanes still in the loop.
 template <class Loader>
 hipError_t launch_rotate(hipStream_t st, const Loader& ld, uint16_t* out, int64_t M, int K) {
     const int64_t groups = M * (K / kGroup);

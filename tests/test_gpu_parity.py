@@ -130,6 +130,106 @@ def test_quantize_special_rows(dev):
     assert np.array_equal(npy(q), wq) and np.array_equal(npy(s), ws)
 
 
+def _huge_rows(k, seed=7):
+    """bf16 rows at the top of the range, where the Hadamard's unscaled sums
+    would overflow (max |x| in [2^120, 2^128)), mixed with ordinary rows and
+    groups: a constant 2^124 row (a fixed point of the reference's chain),
+    random signs and exponents in [120, 127), one huge group in an ordinary
+    row (so the waves of one row take different transforms), a single spike
+    of 2^127, values next to the bf16 maximum (the reference itself overflows
+    on some outputs), an inf, and an ordinary row."""
+    rng = np.random.default_rng(seed)
+    sg = lambda: rng.choice([-1.0, 1.0], k)
+    rows = [np.full(k, 2.0 ** 124), np.full(k, -2.0 ** 121),
+            sg() * rng.uniform(1, 2, k) * 2.0 ** rng.integers(120, 127, k),
+            sg() * rng.uniform(1, 2, k) * 2.0 ** rng.integers(110, 121, k)]
+    r = rng.standard_normal(k)
+    r[256:512] = sg()[:256] * 2.0 ** 125
+    rows.append(r)
+    r = np.zeros(k)
+    r[5] = 2.0 ** 127
+    rows.append(r)
+    rows.append(sg() * 3.38e38)
+    r = rng.standard_normal(k)
+    r[3] = np.inf
+    rows.append(r)
+    rows.append(rng.standard_normal(k))
+    return O.f32_to_bf16(np.array(rows, dtype=np.float32))
+
+
+def _bf16_equal(a, b):
+    """Bit equality of bf16 arrays, any NaN equal to any NaN (IEEE leaves the
+    sign of an inf - inf NaN open, and x86 and the GPU differ on it)."""
+    a, b = np.asarray(a, np.uint16), np.asarray(b, np.uint16)
+    nan = lambda x: (x & 0x7FFF) > 0x7F80
+    return bool(np.all((a == b) | (nan(a) & nan(b))))
+
+
+def _finite_rows(xb):
+    """The rows whose rotation the reference computes without overflow."""
+    with np.errstate(over="ignore", invalid="ignore"):
+        r = O.hadamard256(O.bf16_to_f32(xb))
+    return np.isfinite(r).all(axis=1)
+
+
+@pytest.mark.parametrize("k", [1280, 5120])
+def test_rotate_huge_rows(dev, k):
+    xb = _huge_rows(k)
+    got = bits(int8.rotate(from_bits(xb, dev)))
+    with np.errstate(over="ignore", invalid="ignore"):
+        want = O.rotate_bf16(xb)
+    assert _bf16_equal(got, want), mismatch(got, want)
+    assert np.isinf(O.bf16_to_f32(want)).any()          # the reference's own overflow is covered
+
+
+@pytest.mark.parametrize("k", [1280, 5120, 16896, 33024])
+def test_quantize_huge_rows(dev, k):
+    """The ConvRot quantizer on rows the reference rotates without overflow,
+    through the one-group (k <= 64 groups), two-group (16896) and two-pass
+    (33024 = 129 groups) row kernels."""
+    xb = _huge_rows(k)[_finite_rows(_huge_rows(k))]
+    assert len(xb) >= 4
+    q, s = int8.quantize(from_bits(xb, dev))
+    wq, ws = O.convrot_quantize(xb)
+    assert np.array_equal(npy(s).view(np.uint32), ws.view(np.uint32)), mismatch(npy(s), ws)
+    assert np.array_equal(npy(q), wq), mismatch(npy(q), wq)
+
+
+@pytest.mark.parametrize("k", [1280, 5120])
+def test_prepare_weight_huge_rows(dev, k):
+    wb = _huge_rows(k, seed=8)
+    wb = wb[_finite_rows(wb)]
+    q, s = int8.prepare_weight(from_bits(wb, dev))
+    wq, ws = O.prepare_weight(wb)
+    assert np.array_equal(npy(s).view(np.uint32), ws.view(np.uint32)), mismatch(npy(s), ws)
+    assert np.array_equal(npy(q), wq), mismatch(npy(q), wq)
+
+
+@pytest.mark.parametrize("act", [4, 5])
+def test_quantize_act_huge_rows(dev, act):
+    """gelu_erf keeps a huge positive input (x * Phi(x) = x) and GEGLU multiplies
+    a huge hidden value by gelu(gate): the activation's output reaches the
+    scaled transform's range."""
+    k = 1280
+    h = _huge_rows(k, seed=9)
+    h = h[_finite_rows(h)]
+    rows = len(h)
+    if act == 4:
+        gate = np.abs(O.bf16_to_f32(bits(activation(rows, k, seed=10, n_out=0)))) + np.float32(0.5)
+        x = np.concatenate([h, O.f32_to_bf16(gate)], axis=1)
+    else:
+        x = O.f32_to_bf16(np.abs(O.bf16_to_f32(h)))
+    name = {v: kk for kk, v in int8.ACTIVATIONS.items()}[act]
+    xb = np.ascontiguousarray(x)
+    with np.errstate(over="ignore", invalid="ignore"):
+        wq, ws = O.quantize_act(xb, act)
+    keep = np.isfinite(ws) & (ws > 0)
+    q, s = int8.quantize_act(from_bits(xb, dev), name)
+    assert np.array_equal(npy(s)[keep].view(np.uint32), ws[keep].view(np.uint32)), mismatch(npy(s), ws)
+    assert np.array_equal(npy(q)[keep], wq[keep]), mismatch(npy(q)[keep], wq[keep])
+    assert keep.sum() >= 3
+
+
 @pytest.mark.parametrize("act", [1, 2, 3, 4, 5])
 @pytest.mark.parametrize("m,k", [(9, 1280), (16, 5120)])
 def test_quantize_act_exact(dev, act, m, k):

@@ -127,3 +127,69 @@ def test_operation_order_is_observable():
     h = O.hadamard256_matrix().astype(np.float32)
     other = (x @ h.T).astype(np.float32)       # a BLAS order
     assert not np.array_equal(other.view(np.uint32), O.hadamard256(x).view(np.uint32))
+
+
+# ------------------------------------------------ the kernels' two operation orders
+def _unscaled(v):
+    """The reference's operation order with every factor 0.5 dropped (the
+    kernels' fast path): chains with coefficients +-1 on axes 0 and 1, the
+    butterflies without their final halving on axes 2 and 3.  Its result is
+    16 times the rotation wherever nothing overflows."""
+    v = np.asarray(v, dtype=np.float32)
+    k = v.shape[-1]
+    r = v.reshape(-1, k // 256, 16, 4, 4)
+    t = np.empty_like(r)
+    for o in range(4):
+        acc = O.H4[o, 0] * r[..., 0]
+        for c in range(1, 4):
+            acc = acc + O.H4[o, c] * r[..., c]
+        t[..., o] = acc
+    u = np.empty_like(t)
+    for o in range(4):
+        acc = O.H4[o, 0] * t[..., 0, :]
+        for c in range(1, 4):
+            acc = acc + O.H4[o, c] * t[..., c, :]
+        u[..., o, :] = acc
+
+    def bfly(a0, a1, a2, a3):
+        p, m, q, n = a0 + a1, a0 - a1, a2 + a3, a2 - a3
+        return p + n, p - n, m + q, q - m
+
+    w = u.reshape(-1, k // 256, 4, 4, 16)
+    w = np.stack(bfly(w[:, :, :, 0], w[:, :, :, 1], w[:, :, :, 2], w[:, :, :, 3]), axis=3)
+    w = np.stack(bfly(w[:, :, 0], w[:, :, 1], w[:, :, 2], w[:, :, 3]), axis=2)
+    return w.reshape(v.shape)
+
+
+def _bf16_rows(rng, rows, lo_exp, hi_exp):
+    """bf16 rows of random sign and mantissa whose exponents span [lo_exp, hi_exp)."""
+    e = rng.integers(lo_exp, hi_exp, (rows, 256)).astype(np.float64)
+    x = rng.choice([-1.0, 1.0], (rows, 256)) * rng.uniform(1, 2, (rows, 256)) * 2.0 ** e
+    return O.bf16_round(x.astype(np.float32))
+
+
+def test_unscaled_order_is_exact_below_two_to_120():
+    """The fast path's claim: for every group with max|x| < 2^120 the unscaled
+    order gives exactly 16 x the reference's result, across the whole bf16
+    range below that bound, subnormal inputs included."""
+    rng = np.random.default_rng(5)
+    with np.errstate(over="ignore", invalid="ignore"):
+        for lo, hi in ((-133, -126), (-140, -100), (-60, 60), (100, 119), (118, 120)):
+            x = _bf16_rows(rng, 64, lo, hi)
+            x[np.abs(x) >= 2.0 ** 120] = np.float32(2.0 ** 119)
+            x[0] = np.float32(-(2.0 - 2.0 ** -7) * 2.0 ** 119)      # largest magnitude below the bound
+            x[1] = O.bf16_round(np.full(256, 2.0 ** -133, np.float32))   # smallest bf16 subnormal
+            ref = O.hadamard256(x)
+            fast = _unscaled(x) * np.float32(0.0625)
+            assert np.isfinite(fast).all()
+            assert np.array_equal(fast.view(np.uint32), ref.view(np.uint32)), (lo, hi)
+
+
+def test_unscaled_order_overflows_above_two_to_120():
+    """Why the kernels keep the reference's scaled order for larger inputs: a
+    constant row of 2^124 is a fixed point of the reference's chain, but its
+    unscaled sums reach 2^128 = inf."""
+    c = np.full((1, 256), 2.0 ** 124, np.float32)
+    assert np.array_equal(O.hadamard256(c), c)
+    with np.errstate(over="ignore"):
+        assert np.isinf(_unscaled(c)).all()
