@@ -154,6 +154,27 @@ int xpuint8_dx_gemm_stream(const void *stream, const int8_t *q, const float *a,
                            const int8_t *w8, void *dx, int64_t M, int64_t N, int64_t K,
                            int8_t *work);
 
+/* linear_dx_int8 in one call: dL/dx of the INT8 linear against the weight
+ * still in int8,
+ *   d = bf16(dy * bf16(w_scale[n])),  (q, a) = quantize_row(d),
+ *   dx = rotate_bf16(bf16(float(sum_n q[m,n] w8[n,k]) * a[m]))
+ * with dy bf16 [M,N], w8 int8 [N,K] (prepared: rotated rows), w_scale fp32
+ * [N], dx bf16 [M,K].  K % 256 == 0, N % 16 == 0.  `work` is a device buffer
+ * of at least xpuint8_linear_dx_int8_workspace_size(M, N, K) bytes (the
+ * quantized gradient, its scales, the transposed weight and the product before
+ * the inverse rotation), 16-byte aligned; it is fully written before it is
+ * read, so it needs no clearing.  Replaces linear_dx_int8
+ * (python/xpu_kernels/int8/ops.py:353-377): its torch multiply, the Triton
+ * quantize_row, torch._int_mm, dequant and rotate. */
+int xpuint8_linear_dx_int8_stream(const void *stream, const void *dy, const float *w_scale,
+                                  const int8_t *w8, void *dx, int64_t M, int64_t N, int64_t K,
+                                  void *work, int64_t work_bytes);
+
+/* The workspace xpuint8_linear_dx_int8_stream needs, in bytes, or -1 when the
+ * shape is not supported.  No device needed.  A helper of the entry point
+ * above, with no counterpart in the reference. */
+int64_t xpuint8_linear_dx_int8_workspace_size(int64_t M, int64_t N, int64_t K);
+
 /* prepare_weight in one kernel, bit-identical to the torch chain of
  * python/xpu_kernels/int8/ops.py:93-99: bf16 w[N,K] -> int8 q[N,K] + fp32
  * scale[N].  (xpuint8_convrot_quantize is prepare_weight_fused.) */

@@ -123,6 +123,47 @@ int check_gemm(int64_t M, int64_t N, int64_t K) {
         if (rc_ != 0) return rc_;  \
     } while (0)
 
+// The workspace of linear_dx_int8: the row-quantized column-scaled gradient
+// q [M,N] int8 and its row scales a [M] fp32, the transposed weight w8^T
+// [K,N] int8 (the GEMM's K-contiguous operand), and the product before the
+// inverse rotation, bf16 [M,K].  Each piece starts on a 256-byte boundary.
+struct DxWork {
+    size_t q, a, wt, pre, total;
+};
+DxWork dx_work_layout(int64_t M, int64_t N, int64_t K) {
+    auto up = [](int64_t b) { return (size_t(b) + 255) & ~size_t(255); };
+    DxWork w;
+    w.q = 0;
+    w.a = w.q + up(M * N);
+    w.wt = w.a + up(4 * M);
+    w.pre = w.wt + up(N * K);
+    w.total = w.pre + up(2 * M * K);
+    return w;
+}
+
+int check_dx(int64_t M, int64_t N, int64_t K) {
+    XPU_TRY(check_rows(M, K));               // the inverse rotation: K % 256
+    XPU_TRY(check_epilogue(M, N));           // the row quantizer: N % 16
+    return check_gemm(M, K, N);              // q [M,N] @ w8 [N,K], contraction over N
+}
+
+// quantize_row (column-scaled) -> w8^T -> GEMM with the row-scale epilogue ->
+// inverse rotation, all on one stream, through the workspace at `work`.
+int dx_chain(hipStream_t st, const void* dy, const float* w_scale, const int8_t* w8, void* dx,
+             int64_t M, int64_t N, int64_t K, char* work) {
+    const DxWork L = dx_work_layout(M, N, K);
+    int8_t* q = reinterpret_cast<int8_t*>(work + L.q);
+    float* a = reinterpret_cast<float*>(work + L.a);
+    int8_t* wt = reinterpret_cast<int8_t*>(work + L.wt);
+    void* pre = work + L.pre;
+    XPU_TRY(launched(quantize_row(st, dy, w_scale, q, a, M, int(N)), "linear_dx_int8 (quantize_row)"));
+    XPU_TRY(launched(transpose_i8(st, w8, wt, N, K), "linear_dx_int8 (transpose)"));
+    XPU_TRY(launched(gemm_dequant(st, q, N, wt, N, pre, K, a, nullptr, nullptr, nullptr, int(M),
+                                  int(K), int(N)),
+                     "linear_dx_int8 (gemm)"));
+    return launched(rotate_bf16(st, pre, dx, M, int(K)), "linear_dx_int8 (rotate)");
+}
+
 int act_ok(int32_t act) {
     if (act < 1 || act > 5)
         return fail(6, "activation must be 1 (GELU-tanh), 2 (SwiGLU), 3 (situ), 4 (GEGLU) "
@@ -354,6 +395,22 @@ int xpuint8_dx_gemm_stream(const void* stream, const int8_t* q, const float* a, 
     return launched(gemm_dequant(st, q, N, work, N, dx, K, a, nullptr, nullptr, nullptr, int(M), int(K),
                                  int(N)),
                     "dx_gemm");
+}
+
+int64_t xpuint8_linear_dx_int8_workspace_size(int64_t M, int64_t N, int64_t K) {
+    if (check_dx(M, N, K) != 0) return -1;
+    return int64_t(dx_work_layout(M, N, K).total);
+}
+
+int xpuint8_linear_dx_int8_stream(const void* stream, const void* dy, const float* w_scale,
+                                  const int8_t* w8, void* dx, int64_t M, int64_t N, int64_t K,
+                                  void* work, int64_t work_bytes) {
+    XPU_TRY(check_dx(M, N, K));
+    XPU_NONNULL(dy); XPU_NONNULL(w_scale); XPU_NONNULL(w8); XPU_NONNULL(dx); XPU_NONNULL(work);
+    if (work_bytes < int64_t(dx_work_layout(M, N, K).total))
+        return fail(2, "work must hold xpuint8_linear_dx_int8_workspace_size(M, N, K) bytes");
+    XPU_TRY(ensure_device());
+    return dx_chain(as_stream(stream), dy, w_scale, w8, dx, M, N, K, static_cast<char*>(work));
 }
 
 int xpuint8_linear_dw_stream(const void* stream, const void* dy, const void* x, void* dw,

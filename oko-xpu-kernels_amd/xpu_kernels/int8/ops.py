@@ -269,15 +269,18 @@ def linear_dx_int8(dy, w8, w_scale):
     n, k = int(w8.shape[0]), int(w8.shape[1])
     d2 = _c(dy.to(torch.bfloat16).reshape(-1, n))
     m = d2.shape[0]
-    q, a = quantize_row(d2, w_scale)
-    work = torch.empty((k * n,), device=dy.device, dtype=torch.int8)
-    dx = torch.empty((m, k), device=dy.device, dtype=torch.bfloat16)
+    ws = expand_scale(w_scale, n, dy.device)
     w8c = _c(w8)
-    rc = lib.xpuint8_dx_gemm_stream(_stream(dy.device), _ptr(q), _ptr(a), _ptr(w8c), _ptr(dx),
-                                    m, n, k, _ptr(work))
+    nbytes = lib.xpuint8_linear_dx_int8_workspace_size(m, n, k)
+    if nbytes < 0:
+        _err(lib, "linear_dx_int8")
+    work = torch.empty((nbytes,), device=dy.device, dtype=torch.int8)
+    dx = torch.empty((m, k), device=dy.device, dtype=torch.bfloat16)
+    rc = lib.xpuint8_linear_dx_int8_stream(_stream(dy.device), _ptr(d2), _ptr(ws), _ptr(w8c),
+                                           _ptr(dx), m, n, k, _ptr(work), nbytes)
     if rc != 0:
         _err(lib, "linear_dx_int8")
-    return rotate(dx).reshape(*dy.shape[:-1], k)
+    return dx.reshape(*dy.shape[:-1], k)
 
 
 def expand_scale(scale, n, device=None):

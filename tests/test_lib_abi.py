@@ -70,6 +70,10 @@ def _rc(lib, fn, *args):
     ("xpuint8_ffn_up_stream", (Z, P, P, P, P, P, 4, 24, 512, 4), 2, "16"),
     ("xpuint8_ffn_up_stream", (Z, P, P, Z, P, P, 4, 512, 512, 4), 6, "null"),
     ("xpuint8_dx_gemm_stream", (Z, P, P, P, P, 4, 24, 512, P), 2, "16"),
+    ("xpuint8_linear_dx_int8_stream", (Z, P, P, P, P, 4, 32, 300, P, 1 << 20), 3, "256"),
+    ("xpuint8_linear_dx_int8_stream", (Z, P, P, P, P, 4, 24, 512, P, 1 << 20), 2, "16"),
+    ("xpuint8_linear_dx_int8_stream", (Z, P, P, P, P, 4, 32, 512, Z, 1 << 20), 6, "null"),
+    ("xpuint8_linear_dx_int8_stream", (Z, P, P, P, P, 4, 32, 512, P, 1024), 2, "workspace_size"),
     ("xpuint8_prepare_weight_stream", (Z, P, P, P, 16, 300), 3, "256"),
     ("xpuint8_quantize_row_stream", (Z, P, Z, P, P, 4, 20), 2, "16"),
     ("xpuint8_activation_table", (7, P), 6, "0..5"),
@@ -101,3 +105,16 @@ def test_errors_are_per_thread(lib):
 def test_init_without_a_device_fails_cleanly(lib):
     rc = lib.xpuint8_init()
     assert rc == 1 and "device" in lib.xpuint8_last_error().decode().lower()
+
+
+def test_dx_workspace_size(lib):
+    """The linear_dx_int8 workspace: q [M,N] int8, a [M] fp32, w8^T [K,N] int8
+    and the bf16 [M,K] product, each rounded up to 256 bytes; -1 for a shape
+    the entry point rejects."""
+    up = lambda b: (b + 255) // 256 * 256
+    m, n, k = 4096, 5120, 1280
+    want = up(m * n) + up(4 * m) + up(n * k) + up(2 * m * k)
+    assert lib.xpuint8_linear_dx_int8_workspace_size(m, n, k) == want
+    assert lib.xpuint8_linear_dx_int8_workspace_size(3, 16, 256) == 256 + 256 + 16 * 256 + up(2 * 3 * 256)
+    assert lib.xpuint8_linear_dx_int8_workspace_size(4, 24, 512) == -1
+    assert lib.xpuint8_linear_dx_int8_workspace_size(4, 32, 300) == -1
