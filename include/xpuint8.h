@@ -175,6 +175,21 @@ int xpuint8_linear_dx_int8_stream(const void *stream, const void *dy, const floa
  * above, with no counterpart in the reference. */
 int64_t xpuint8_linear_dx_int8_workspace_size(int64_t M, int64_t N, int64_t K);
 
+/* xpuint8_linear_dx_int8_stream without the workspace argument and without
+ * allocating anything: for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  No counterpart in the reference.  The workspace is the
+ * library's own fixed array of 64 MiB per device (67108864 bytes, reserved
+ * when the library is loaded and kept until the process ends); a shape whose
+ * xpuint8_linear_dx_int8_workspace_size exceeds it is rejected with code 4
+ * (config 5, M=4096 N=5120 K=1280, needs 38 MB).  Every call on a device
+ * shares that array: calls that overlap on one device (two streams, two
+ * threads) race and must be serialised by the caller.  The result equals
+ * xpuint8_linear_dx_int8_stream's bit for bit. */
+int xpuint8_linear_dx_int8_noalloc_stream(const void *stream, const void *dy, const float *w_scale,
+                                          const int8_t *w8, void *dx, int64_t M, int64_t N,
+                                          int64_t K);
+
 /* prepare_weight in one kernel, bit-identical to the torch chain of
  * python/xpu_kernels/int8/ops.py:93-99: bf16 w[N,K] -> int8 q[N,K] + fp32
  * scale[N].  (xpuint8_convrot_quantize is prepare_weight_fused.) */

@@ -22,6 +22,16 @@ namespace xpuint8 {
 // the address hipGetSymbolAddress returns for the current device.
 __device__ uint16_t g_act_tables[kNumTables * kTabSize];
 
+// The workspace of the no-allocation entry point
+// (xpuint8_linear_dx_int8_noalloc_stream): one 64 MiB array on every device
+// the library runs on, held until the process ends.  In host code `scratch`
+// names a host-side stand-in, not device memory: its device address is taken
+// once per device at set-up (ensure_device, g_scratch) and only that address
+// is ever passed to a kernel.  Every call on a device shares its array, so
+// calls that overlap on one device race.
+constexpr size_t kScratchBytes = size_t(64) << 20;
+static __device__ __align__(256) char scratch[kScratchBytes];
+
 namespace {
 
 thread_local std::string t_error;
@@ -35,6 +45,7 @@ constexpr int kMaxDevices = 64;
 std::mutex g_mutex;
 std::string g_device_name[kMaxDevices];
 const uint16_t* g_tab_dev[kMaxDevices] = {};
+char* g_scratch[kMaxDevices] = {};        // device address of `scratch`, per device
 int g_cus[kMaxDevices] = {};
 std::atomic<bool> g_ready[kMaxDevices] = {};
 
@@ -62,6 +73,11 @@ int ensure_device() {
     if (e != hipSuccess)
         return fail(5, std::string("uploading the activation tables: ") + hipGetErrorString(e));
     g_tab_dev[dev] = static_cast<const uint16_t*>(sym);
+    void* sp = nullptr;
+    e = hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || sp == nullptr)
+        return fail(5, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+    g_scratch[dev] = static_cast<char*>(sp);
     g_cus[dev] = prop.multiProcessorCount;
     g_device_name[dev] = prop.name;
     g_ready[dev].store(true, std::memory_order_release);
@@ -411,6 +427,24 @@ int xpuint8_linear_dx_int8_stream(const void* stream, const void* dy, const floa
         return fail(2, "work must hold xpuint8_linear_dx_int8_workspace_size(M, N, K) bytes");
     XPU_TRY(ensure_device());
     return dx_chain(as_stream(stream), dy, w_scale, w8, dx, M, N, K, static_cast<char*>(work));
+}
+
+int xpuint8_linear_dx_int8_noalloc_stream(const void* stream, const void* dy,
+                                          const float* w_scale, const int8_t* w8, void* dx,
+                                          int64_t M, int64_t N, int64_t K) {
+    XPU_TRY(check_dx(M, N, K));
+    XPU_NONNULL(dy); XPU_NONNULL(w_scale); XPU_NONNULL(w8); XPU_NONNULL(dx);
+    const size_t need = dx_work_layout(M, N, K).total;
+    if (need > kScratchBytes)
+        return fail(4, "linear_dx_int8_noalloc: this shape needs " + std::to_string(need) +
+                           " bytes of workspace, above the library's fixed 64 MiB "
+                           "(67108864 bytes); use xpuint8_linear_dx_int8_stream with a "
+                           "caller workspace");
+    XPU_TRY(ensure_device());
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || g_scratch[dev] == nullptr)
+        return fail(5, "linear_dx_int8_noalloc: no scratch address for the current device");
+    return dx_chain(as_stream(stream), dy, w_scale, w8, dx, M, N, K, g_scratch[dev]);
 }
 
 int xpuint8_linear_dw_stream(const void* stream, const void* dy, const void* x, void* dw,
