@@ -131,6 +131,21 @@ int xpuint8_linear_gemm_stream(const void *stream, const int8_t *xq, const float
                                const int8_t *w8, const float *w_scale, const void *bias,
                                int32_t bias_bf16, void *out, int64_t M, int64_t N, int64_t K);
 
+/* xpuint8_linear_gemm_stream followed by the residual update of
+ * linear(residual=, residual_scale=), fused into the same store:
+ *   d[m,n]   = the linear_gemm result (bf16),
+ *   out[m,n] = bf16(float(residual[m,n]) + float(d[m,n]) * float(residual_scale[n]))
+ * with residual bf16 [M,N] and residual_scale bf16 [N]: torch.addcmul(residual,
+ * d, residual_scale) on bf16 tensors, bit for bit (the bf16 product is exact
+ * in fp32).  out may be residual itself (each element is read before it is
+ * written, by the same thread).  Replaces the dequant + addcmul of
+ * python/xpu_kernels/int8/ops.py:634-644. */
+int xpuint8_linear_gemm_residual_stream(const void *stream, const int8_t *xq,
+                                        const float *x_scale, const int8_t *w8,
+                                        const float *w_scale, const void *bias, int32_t bias_bf16,
+                                        const void *residual, const void *residual_scale,
+                                        void *out, int64_t M, int64_t N, int64_t K);
+
 /* The FFN's up-projection with the dequant and the activation fused into the
  * GEMM's store:
  *   d_j[m,n] = bf16(float(sum_k xq[m,k] w8[j*N+n,k]) * (w_scale[j*N+n] * x_scale[m]))
@@ -210,6 +225,15 @@ int xpuint8_quantize_row_stream(const void *stream, const void *x, const float *
  * N % 16 == 0, K % 16 == 0.  Replaces the torch matmul dy^T @ x of linear_dw
  * (python/xpu_kernels/int8/ops.py:207-238). */
 int xpuint8_linear_dw_stream(const void *stream, const void *dy, const void *x, void *dw,
+                             int64_t M, int64_t N, int64_t K);
+
+/* The activation gradient of a linear with a bf16 weight (the dense-mode
+ * backward): dx[m,k] = sum_n dy[m,n] * w[n,k], dy bf16 [M,N], w bf16 [N,K]
+ * (the unrotated weight, e.g. from xpuint8_dequant_weight_stream), dx bf16
+ * [M,K]; fp32 accumulation, one RNE rounding.  N % 16 == 0, K % 16 == 0.
+ * Replaces the torch matmul dy @ w of linear_dx
+ * (python/xpu_kernels/int8/ops.py:194-204). */
+int xpuint8_linear_dx_stream(const void *stream, const void *dy, const void *w, void *dx,
                              int64_t M, int64_t N, int64_t K);
 
 /* RMSNorm + rotary embedding of q or k read straight from the int32

@@ -384,6 +384,26 @@ int xpuint8_linear_gemm_stream(const void* stream, const int8_t* xq, const float
                     "linear_gemm");
 }
 
+int xpuint8_linear_gemm_residual_stream(const void* stream, const int8_t* xq,
+                                        const float* x_scale, const int8_t* w8,
+                                        const float* w_scale, const void* bias, int32_t bias_bf16,
+                                        const void* residual, const void* residual_scale,
+                                        void* out, int64_t M, int64_t N, int64_t K) {
+    XPU_TRY(check_epilogue(M, N));
+    XPU_TRY(check_gemm(M, N, K));
+    XPU_NONNULL(xq); XPU_NONNULL(x_scale); XPU_NONNULL(w8); XPU_NONNULL(w_scale);
+    XPU_NONNULL(residual); XPU_NONNULL(residual_scale); XPU_NONNULL(out);
+    XPU_ALIGNED_OPT(bias);
+    if (bias_bf16 != 0 && bias_bf16 != 1) return fail(2, "bias_bf16 must be 0 or 1");
+    XPU_TRY(ensure_device());
+    const float* b32 = bias_bf16 ? nullptr : static_cast<const float*>(bias);
+    const uint16_t* b16 = bias_bf16 ? static_cast<const uint16_t*>(bias) : nullptr;
+    return launched(gemm_dequant_residual(as_stream(stream), xq, K, w8, K, out, N, x_scale, w_scale,
+                                          b32, b16, residual, N, residual_scale, int(M), int(N),
+                                          int(K)),
+                    "linear_gemm_residual");
+}
+
 int xpuint8_ffn_up_stream(const void* stream, const int8_t* xq, const float* x_scale,
                           const int8_t* w8, const float* w_scale, void* out, int64_t M, int64_t N,
                           int64_t K, int32_t activation) {
@@ -456,6 +476,17 @@ int xpuint8_linear_dw_stream(const void* stream, const void* dy, const void* x, 
     XPU_TRY(ensure_device());
     return launched(gemm_bf16_tn(as_stream(stream), dy, N, x, K, dw, K, int(M), int(N), int(K)),
                     "linear_dw");
+}
+
+int xpuint8_linear_dx_stream(const void* stream, const void* dy, const void* w, void* dx,
+                             int64_t M, int64_t N, int64_t K) {
+    if (M <= 0 || N <= 0 || K <= 0) return fail(2, "M, N and K must be positive");
+    if (N % 16 != 0 || K % 16 != 0) return fail(2, "N and K must be multiples of 16");
+    if (M > kMaxDim || N > kMaxDim || K > kMaxDim) return fail(4, "M, N and K must be < 2^31");
+    XPU_NONNULL(dy); XPU_NONNULL(w); XPU_NONNULL(dx);
+    XPU_TRY(ensure_device());
+    return launched(gemm_bf16_nn(as_stream(stream), dy, N, w, K, dx, K, int(M), int(N), int(K)),
+                    "linear_dx");
 }
 
 // ------------------------------------------------------------- rms + rope

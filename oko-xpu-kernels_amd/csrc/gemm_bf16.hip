@@ -212,7 +212,172 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_tn_kernel(
     }
 }
 
+// The activation gradient of a linear with a bf16 weight, the dense-mode dx:
+//
+//   out[m, k] = sum_n dy[m, n] * w[n, k]      dy bf16 [M, N], w bf16 [N, K]
+//
+// (python/xpu_kernels/int8/ops.py:194-204, dy @ w).  The weight is contracted
+// along its rows, like both operands above, and goes through the same x
+// region and transposing reads (D rows = k).  dy is contracted along its
+// contiguous dimension: its region holds 128 rows (m) of one 32-element
+// (64-byte) step, and lane l's B fragment, dy[m][8(l/16)..+7] of row
+// m = l%16 of a block, is one plain 16-byte read.  Chunk c of region row r
+// sits at position c ^ swz_dy(r); the 16 rows a read touches then cover the
+// 64 banks exactly once.  Lane l of a 16x16 block holds D[4(l/16)+i][l%16]:
+// four consecutive k of one output row, one 8-byte store.
+__device__ __forceinline__ int swz_dy(int r) { return (r >> 2) & 3; }
+
+__device__ __forceinline__ v8bf plain_read(uint32_t addr) {
+    v8s r;
+    asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(addr));
+    return __builtin_bit_cast(v8bf, r);
+}
+
+template <int STAGES>
+__global__ __launch_bounds__(256, 2) void gemm_bf16_nn_kernel(
+    const uint16_t* __restrict__ W, int64_t ldw, const uint16_t* __restrict__ Y, int64_t ldy,
+    uint16_t* __restrict__ out, int64_t ldo, int R, int K, int M, int tiles_k, int tiles_m) {
+    constexpr int BKD = 128, BMD = 128;                 // D rows (k), D columns (m) per tile
+    constexpr int TM = 4, TN = 4;                       // 16x16 blocks per wave
+    constexpr int STAGE = 2 * kRegion;
+    __shared__ __attribute__((aligned(1024))) int8_t smem[STAGES * STAGE];
+
+    const int tiles = tiles_k * tiles_m;
+    int t = blockIdx.x;
+    if (tiles % 8 == 0) t = (t % 8) * (tiles / 8) + t / 8;   // each XCD a contiguous range
+    const int k0 = (t % tiles_k) * BKD, m0 = (t / tiles_k) * BMD;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+
+    // DMA: blocks 0..7 of a stage are the weight region (as in the TN kernel:
+    // 4 rows x 256 bytes each), blocks 8..15 the dy region (16 rows x 64
+    // bytes each).  Lane l of a dy block fills row r = 16*(b-8) + l/4,
+    // position l%4, i.e. chunk (l%4) ^ swz_dy(r) of the step: columns past R
+    // read zeros, rows past M repeat the last row (not stored).
+    const int8_t* src[4];
+    int srow[4];
+    int scol[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int b = wave + 4 * i;
+        if (i < 2) {
+            srow[i] = 4 * (b & 7) + (lane >> 4);
+            const int dchunk = (lane & 15) ^ swz(srow[i]);
+            const int col = min(k0 + dchunk * 8, K - 8);
+            src[i] = reinterpret_cast<const int8_t*>(W + col);
+            scol[i] = 0;
+        } else {
+            const int r = 16 * (b - 8) + (lane >> 2);
+            srow[i] = r;
+            const int m = min(m0 + r, M - 1);
+            src[i] = reinterpret_cast<const int8_t*>(Y + int64_t(m) * ldy);
+            scol[i] = 8 * ((lane & 3) ^ swz_dy(r));
+        }
+    }
+    auto issue = [&](int buf, int step) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int8_t* p;
+            if (i < 2) {
+                const int row = step * kStepRows + srow[i];
+                p = row < R ? src[i] + int64_t(row) * ldw * 2 : g_zero_line;
+            } else {
+                const int col = step * kStepRows + scol[i];
+                p = col < R ? src[i] + int64_t(col) * 2 : g_zero_line;
+            }
+            dma16(p, smem + buf * STAGE + (wave + 4 * i) * 1024);
+        }
+    };
+
+    // weight fragments: the TN kernel's transposing reads
+    const int g = lane >> 4, j = lane & 15;
+    uint32_t roff[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) roff[h] = (8 * g + 4 * h + (j >> 2)) * 256 + 8 * (j & 1);
+    const int cpair = (j & 3) >> 1;
+    const int rs = swz(8 * g + (j >> 2));
+    const uint32_t sbase = lds_addr(smem);
+    auto frag_read = [&](uint32_t region, int blk, v4s& lo, v4s& hi) {
+        const uint32_t pos = ((2 * blk + cpair) ^ rs) * 16;
+        lo = tr_read(region + roff[0] + pos);
+        hi = tr_read(region + roff[1] + pos);
+    };
+    auto join = [](const v4s& lo, const v4s& hi) {
+        const v8s v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        return __builtin_bit_cast(v8bf, v);
+    };
+    // dy fragments: row 16*blk + j of the region, chunk g
+    const uint32_t dyoff = j * 64 + ((g ^ swz_dy(j)) * 16);
+
+    v4f acc[TN][TM];
+#pragma unroll
+    for (int a = 0; a < TN; ++a)
+#pragma unroll
+        for (int b = 0; b < TM; ++b) acc[a][b] = v4f{0.f, 0.f, 0.f, 0.f};
+
+    const int RS = (R + kStepRows - 1) / kStepRows;
+#pragma unroll
+    for (int s = 0; s < STAGES - 1; ++s)
+        if (s < RS) issue(s, s);
+#pragma clang loop unroll(disable)
+    for (int st = 0; st < RS; ++st) {
+        const int later = min(RS - 1 - st, STAGES - 2);
+        if (later >= 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(8));
+        else if (later == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(4));
+        else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        __builtin_amdgcn_s_barrier();
+        if (st + STAGES - 1 < RS) issue((st + STAGES - 1) % STAGES, st + STAGES - 1);
+        const uint32_t sb = sbase + (st % STAGES) * STAGE;
+        v4s al[TM], ah[TM];
+        v8bf bf[TN];
+#pragma unroll
+        for (int b = 0; b < TM; ++b) frag_read(sb, wm * TM + b, al[b], ah[b]);
+#pragma unroll
+        for (int a = 0; a < TN; ++a) bf[a] = plain_read(sb + kRegion + (wn * TN + a) * 1024 + dyoff);
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(al[0]), "+v"(al[1]), "+v"(al[2]), "+v"(al[3]), "+v"(ah[0]),
+                       "+v"(ah[1]), "+v"(ah[2]), "+v"(ah[3]), "+v"(bf[0]), "+v"(bf[1]),
+                       "+v"(bf[2]), "+v"(bf[3]));
+        v8bf af[TM];
+#pragma unroll
+        for (int b = 0; b < TM; ++b) af[b] = join(al[b], ah[b]);
+#pragma unroll
+        for (int a = 0; a < TN; ++a)
+#pragma unroll
+            for (int b = 0; b < TM; ++b)
+                acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[b], bf[a], acc[a][b], 0, 0, 0);
+    }
+
+    // lane l of block (a, b): output row m = m0 + 64 wn + 16a + l%16,
+    // columns k = k0 + 64 wm + 16b + 4(l/16) .. +3
+#pragma unroll
+    for (int a = 0; a < TN; ++a) {
+        const int m = m0 + wn * 64 + 16 * a + (lane & 15);
+        if (m >= M) continue;
+#pragma unroll
+        for (int b = 0; b < TM; ++b) {
+            const int k = k0 + wm * 64 + 16 * b + 4 * (lane >> 4);
+            if (k < K) {
+                const v4f v = acc[a][b];
+                *reinterpret_cast<uint2*>(out + int64_t(m) * ldo + k) =
+                    make_uint2(cvt_pk_bf16(v[0], v[1]), cvt_pk_bf16(v[2], v[3]));
+            }
+        }
+    }
+}
+
 }  // namespace
+
+hipError_t gemm_bf16_nn(hipStream_t st, const void* dy, int64_t ldy, const void* w, int64_t ldw,
+                        void* out, int64_t ldo, int M, int N, int K) {
+    const int tiles_k = (K + 127) / 128, tiles_m = (M + 127) / 128;
+    hipLaunchKernelGGL((gemm_bf16_nn_kernel<2>), dim3(unsigned(tiles_k * tiles_m)), dim3(256), 0,
+                       st, static_cast<const uint16_t*>(w), ldw, static_cast<const uint16_t*>(dy),
+                       ldy, static_cast<uint16_t*>(out), ldo, N, K, M, tiles_k, tiles_m);
+    return hipGetLastError();
+}
 
 hipError_t gemm_bf16_tn(hipStream_t st, const void* dy, int64_t ldy, const void* x, int64_t ldx,
                         void* dw, int64_t ldo, int R, int N, int K) {

@@ -130,6 +130,39 @@ struct EpiDequant {
     }
 };
 
+// The dequant epilogue followed by the residual update of the reference's
+// linear(residual=, residual_scale=) (python/xpu_kernels/int8/ops.py:639-644):
+//   d = bf16(float(acc) * (ws[n] * xs[m]) + bias[n])     (EpiDequant)
+//   out[m, n] = bf16(float(res[m, n]) + float(d) * float(rscale[n]))
+// which is torch.addcmul(res, d, rscale) on bf16 tensors: the product of two
+// bf16 values is exact in fp32, so the fp32 sum is the only rounding before
+// the bf16 one, with or without a fused multiply-add.  res is bf16 [M, N]
+// (row stride ldr); rscale bf16 [N].
+struct EpiDequantRes : EpiDequant {
+    const uint16_t* res;
+    int64_t ldr;
+    const uint16_t* rscale;
+    __device__ __forceinline__ static uint32_t upd2(uint32_t d, uint32_t r, uint32_t s) {
+        const float lo = bf16lo(r) + bf16lo(d) * bf16lo(s);
+        const float hi = bf16hi(r) + bf16hi(d) * bf16hi(s);
+        return cvt_pk_bf16(lo, hi);
+    }
+    __device__ __forceinline__ void store16(int m, int n, const uint4& v) const {
+        const uint4 r = *reinterpret_cast<const uint4*>(res + int64_t(m) * ldr + n);
+        const uint4 sc = *reinterpret_cast<const uint4*>(rscale + n);
+        *reinterpret_cast<uint4*>(out + int64_t(m) * ldo + n) =
+            make_uint4(upd2(v.x, r.x, sc.x), upd2(v.y, r.y, sc.y), upd2(v.z, r.z, sc.z),
+                       upd2(v.w, r.w, sc.w));
+    }
+    __device__ __forceinline__ void operator()(int m, int n, const v4i& v) const {
+        const uint2 d = convert(v, row(m), col(n));
+        const uint2 r = *reinterpret_cast<const uint2*>(res + int64_t(m) * ldr + n);
+        const uint2 sc = *reinterpret_cast<const uint2*>(rscale + n);
+        *reinterpret_cast<uint2*>(out + int64_t(m) * ldo + n) =
+            make_uint2(upd2(d.x, r.x, sc.x), upd2(d.y, r.y, sc.y));
+    }
+};
+
 // The FFN up-projection's epilogue: dequant, then the activation, written as
 // bf16 (src/xpuint8.cpp:238-261, the load side of the reference's fused
 // dequant+activation+quantize kernel, moved into the GEMM's store):
@@ -1467,6 +1500,20 @@ hipError_t gemm_dequant(hipStream_t st, const int8_t* A, int64_t lda, const int8
                         const uint16_t* bias16, int M, int N, int K) {
     return launch_gemm(st, A, lda, B, ldb, M, N, K,
                        EpiDequant{static_cast<uint16_t*>(out), ldo, xs, ws, bias, bias16});
+}
+
+hipError_t gemm_dequant_residual(hipStream_t st, const int8_t* A, int64_t lda, const int8_t* B,
+                                 int64_t ldb, void* out, int64_t ldo, const float* xs,
+                                 const float* ws, const float* bias, const uint16_t* bias16,
+                                 const void* res, int64_t ldr, const void* rscale, int M, int N,
+                                 int K) {
+    EpiDequantRes e;
+    static_cast<EpiDequant&>(e) =
+        EpiDequant{static_cast<uint16_t*>(out), ldo, xs, ws, bias, bias16};
+    e.res = static_cast<const uint16_t*>(res);
+    e.ldr = ldr;
+    e.rscale = static_cast<const uint16_t*>(rscale);
+    return launch_gemm(st, A, lda, B, ldb, M, N, K, e);
 }
 
 hipError_t gemm_act(hipStream_t st, const int8_t* A, int64_t lda, const int8_t* B, int64_t ldb,

@@ -28,6 +28,12 @@ hipError_t gemm_i32(hipStream_t st, const int8_t* A, int64_t lda, const int8_t* 
 hipError_t gemm_dequant(hipStream_t st, const int8_t* A, int64_t lda, const int8_t* B, int64_t ldb,
                         void* out, int64_t ldo, const float* xs, const float* ws, const float* bias,
                         const uint16_t* bias16, int M, int N, int K);
+// the same with the residual update out = bf16(res + d * rscale[n]) (bf16 res, rscale)
+hipError_t gemm_dequant_residual(hipStream_t st, const int8_t* A, int64_t lda, const int8_t* B,
+                                 int64_t ldb, void* out, int64_t ldo, const float* xs,
+                                 const float* ws, const float* bias, const uint16_t* bias16,
+                                 const void* res, int64_t ldr, const void* rscale, int M, int N,
+                                 int K);
 // out[m, n] = act(bf16(acc(n) * ws[n] * xs[m]), bf16(acc(N + n) * ws[N + n] * xs[m])) for the
 // paired activations 3 (situ) and 4 (GEGLU), whose B has 2N rows; act 5 (GELU) takes N rows
 hipError_t gemm_act(hipStream_t st, const int8_t* A, int64_t lda, const int8_t* B, int64_t ldb,
@@ -41,6 +47,9 @@ hipError_t transpose_i8(hipStream_t st, const int8_t* in, int8_t* out, int64_t R
 // gemm_bf16.hip: dw[n, k] = sum_m dy[m, n] * x[m, k] (bf16, fp32 accumulate)
 hipError_t gemm_bf16_tn(hipStream_t st, const void* dy, int64_t ldy, const void* x, int64_t ldx,
                         void* dw, int64_t ldo, int R, int N, int K);
+// gemm_bf16.hip: out[m, k] = sum_n dy[m, n] * w[n, k] (bf16, fp32 accumulate)
+hipError_t gemm_bf16_nn(hipStream_t st, const void* dy, int64_t ldy, const void* w, int64_t ldw,
+                        void* out, int64_t ldo, int M, int N, int K);
 
 // rope.hip: RMSNorm + rotary embedding of an int32 accumulator slice
 hipError_t rms_rope_dequant(hipStream_t st, const int32_t* acc, int64_t a_sb, int64_t a_ss,

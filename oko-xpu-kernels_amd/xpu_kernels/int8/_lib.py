@@ -68,6 +68,7 @@ def _signatures():
         "xpuint8_int8_gemm_stream": ([vp] * 4 + [i64] * 3, c_int),
         "xpuint8_int8_gemm_nn_stream": ([vp] * 4 + [i64] * 3 + [vp], c_int),
         "xpuint8_linear_gemm_stream": ([vp] * 6 + [i32, vp] + [i64] * 3, c_int),
+        "xpuint8_linear_gemm_residual_stream": ([vp] * 6 + [i32] + [vp] * 3 + [i64] * 3, c_int),
         "xpuint8_ffn_up_stream": ([vp] * 6 + [i64] * 3 + [i32], c_int),
         "xpuint8_dx_gemm_stream": ([vp] * 5 + [i64] * 3 + [vp], c_int),
         "xpuint8_linear_dx_int8_stream": ([vp] * 5 + [i64] * 3 + [vp, i64], c_int),
@@ -76,6 +77,7 @@ def _signatures():
         "xpuint8_prepare_weight_stream": ([vp] * 4 + [i64] * 2, c_int),
         "xpuint8_quantize_row_stream": ([vp] * 5 + [i64] * 2, c_int),
         "xpuint8_linear_dw_stream": ([vp] * 4 + [i64] * 3, c_int),
+        "xpuint8_linear_dx_stream": ([vp] * 4 + [i64] * 3, c_int),
         "xpuint8_rms_rope_dequant_stream": ([vp, vp] + [i64] * 3 + [vp] + [i64] * 2 + [vp, vp]
                                             + [i64] * 7 + [vp, vp] + [i64] * 4
                                             + [ctypes.c_float, i32], c_int),

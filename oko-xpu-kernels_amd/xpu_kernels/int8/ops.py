@@ -6,7 +6,13 @@ numbers cited per function): the same names, arguments, error types and
 message substrings, with every kernel -- including the GEMMs and the chains the
 reference left to torch -- running in ``libxpuint8.so`` on the caller's
 current HIP stream.  Nothing here synchronises, and nothing falls back to a
-torch or CPU implementation: without the library every kernel call raises.
+CPU implementation: without the library every kernel call raises.
+
+Two functions keep a torch path, for inputs the bf16 kernels do not take:
+:func:`linear_dx` and :func:`linear_dw` compute ``dy @ w`` and ``dy^T @ x``
+with torch's matmul (as the reference always does) when an operand is not a
+bf16 GPU tensor (an fp32 training model) or a dimension is not a multiple of
+16.  Every bf16 backward of the INT8 layers takes the kernels.
 """
 
 from __future__ import annotations
@@ -150,9 +156,27 @@ def dequant_weight_torch(w8, w_scale):
 
 
 def linear_dx(dy, w):
-    """``dL/dx = dy [.., N] @ w [N, K]`` for an unrotated weight (ops.py:194-204)."""
+    """``dL/dx = dy [.., N] @ w [N, K]`` for an unrotated weight (ops.py:194-204).
+
+    bf16 operands on the GPU with N and K multiples of 16 take the bf16 MFMA
+    kernel (fp32 accumulation, one rounding, like the matmul it replaces);
+    other dtypes and shapes are torch's matmul in their dtype, the
+    reference's own computation."""
     if dy.shape[-1] != w.shape[0]:
         raise ValueError(f"dy has {dy.shape[-1]} columns but w has {w.shape[0]} rows")
+    n, k = int(w.shape[0]), int(w.shape[1])
+    if (dy.dtype == torch.bfloat16 and w.dtype == torch.bfloat16 and dy.is_cuda
+            and w.device == dy.device and w.dim() == 2 and n % 16 == 0 and k % 16 == 0):
+        lib = _lib()
+        dy2, w2 = _c(dy.reshape(-1, n)), _c(w)
+        m = dy2.shape[0]
+        dx = torch.empty((m, k), device=dy.device, dtype=torch.bfloat16)
+        if m:
+            rc = lib.xpuint8_linear_dx_stream(_stream(dy.device), _ptr(dy2), _ptr(w2), _ptr(dx),
+                                              m, n, k)
+            if rc != 0:
+                _err(lib, "linear_dx")
+        return dx.reshape(*dy.shape[:-1], k)
     return dy @ w
 
 
@@ -514,11 +538,25 @@ def linear(x, w8, w_scale, bias=None, act: Optional[str] = None, residual=None,
     ws = expand_scale(w_scale, n, x.device)
     b, b16 = _bias_arg(bias, n, x.device)
     out = torch.empty((m, n), device=x.device, dtype=torch.bfloat16)
+    rs = _fused_residual_scale(residual, residual_scale, input_dtype, n, x.device)
+    if rs is not None:
+        # the residual update in the GEMM's store: bf16 activation, residual
+        # and per-column scale, the case whose addcmul result is bf16
+        res = _c(residual.reshape(m, n).to(torch.bfloat16))
+        rc = lib.xpuint8_linear_gemm_residual_stream(
+            _stream(x.device), _ptr(xq), _ptr(xs), _ptr(w8c), _ptr(ws), _opt(b), b16,
+            _ptr(res), _ptr(rs), _ptr(out), m, n, k)
+        if rc != 0:
+            _err(lib, "linear")
+        return out.reshape(*x.shape[:-1], n)
     rc = lib.xpuint8_linear_gemm_stream(_stream(x.device), _ptr(xq), _ptr(xs), _ptr(w8c),
                                         _ptr(ws), _opt(b), b16, _ptr(out), m, n, k)
     if rc != 0:
         _err(lib, "linear")
     if residual is not None:
+        # any other residual form (an fp32 model, a per-row or full-size
+        # scale, an fp32 scale whose addcmul promotes to fp32): the
+        # reference's own torch chain
         residual = residual.reshape(m, n).to(
             out.dtype if input_dtype == torch.bfloat16 else input_dtype)
         if input_dtype != torch.bfloat16:
@@ -526,6 +564,28 @@ def linear(x, w8, w_scale, bias=None, act: Optional[str] = None, residual=None,
         out = torch.addcmul(residual, out, residual_scale)
     out = out.reshape(*x.shape[:-1], n)
     return out if input_dtype == torch.bfloat16 else out.to(dtype=input_dtype)
+
+
+def _fused_residual_scale(residual, residual_scale, input_dtype, n, device):
+    """The flat bf16 [n] residual scale when ``residual + residual_scale * out``
+    can run in the GEMM's epilogue, else None: a bf16 activation, a residual
+    tensor on the device, and a bf16 scale tensor that is one value or one per
+    output column (shape [.., n] with every leading dim 1), so the reference's
+    addcmul is bf16 and broadcasts the scale along rows only."""
+    if residual is None or input_dtype != torch.bfloat16:
+        return None
+    if not isinstance(residual, torch.Tensor) or residual.device != device:
+        return None
+    s = residual_scale
+    if not isinstance(s, torch.Tensor) or s.dtype != torch.bfloat16 or s.device != device:
+        return None
+    if residual.dtype not in (torch.bfloat16, torch.float32, torch.float16):
+        return None
+    if s.numel() == 1:
+        return _c(s.reshape(1).expand(n))
+    if s.dim() >= 1 and s.shape[-1] == n and s.numel() == n:
+        return _c(s.reshape(n))
+    return None
 
 
 def ffn(x, up_w8, up_scale, down_w8, down_scale, down_bias=None, act="situ"):
@@ -655,8 +715,11 @@ class _TrainableInt8LinearFn(torch.autograd.Function):
         dy = dy.reshape(-1, dy.shape[-1])
         x2 = x.reshape(-1, x.shape[-1])
         w = dequant_weight(w8, ws) if ctx.mode == "dense" else weight
-        dx = dy.to(w.dtype) @ w
-        dw = linear_dw(dy.to(torch.bfloat16), x2.to(torch.bfloat16))
+        # the reference multiplies dy @ w as they are (ops.py:815-820); the
+        # dense weight is bf16, so an fp32 dy is cast to it (where the
+        # reference's matmul would refuse the mixed dtypes)
+        dx = linear_dx(dy if dy.dtype == w.dtype else dy.to(w.dtype), w)
+        dw = linear_dw(dy, x2)
         db = dy.sum(dim=0) if ctx.has_bias else None
         if dw.dtype != weight.dtype:
             dw = dw.to(weight.dtype)

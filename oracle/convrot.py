@@ -14,7 +14,7 @@ __all__ = [
     "GS", "H4", "bf16_to_f32", "f32_to_bf16", "bf16_round", "hadamard256",
     "hadamard256_matrix", "rotate_bf16", "convrot_quantize", "quantize_from_rotated",
     "prepare_weight", "prepare_weight_fused", "quantize_row", "int_mm", "dequant",
-    "linear_acc", "linear", "dequant_weight", "linear_dx_int8", "linear_dw",
+    "linear_acc", "linear", "dequant_weight", "linear_dx_int8", "linear_dx", "linear_dw",
     "convrot_int8_linear", "expand_scale",
 ]
 
@@ -269,6 +269,15 @@ def linear_dx_int8(dy_bf16, w8, w_scale) -> np.ndarray:
     acc = int_mm(q, np.ascontiguousarray(np.asarray(w8, dtype=np.int8).T))
     dx = dequant(acc, a, np.ones(acc.shape[1], dtype=np.float32))
     return rotate_bf16(dx)
+
+
+def linear_dx(dy_bf16, w_bf16) -> np.ndarray:
+    """``dy @ w`` in float64 (python/xpu_kernels/int8/ops.py:194-204, the
+    dense-mode dL/dx against an unrotated bf16 weight); the build's bf16 GEMM
+    is compared to this within a bf16 tolerance."""
+    dy = bf16_to_f32(dy_bf16).astype(np.float64).reshape(-1, np.asarray(dy_bf16).shape[-1])
+    w = bf16_to_f32(w_bf16).astype(np.float64)
+    return dy @ w
 
 
 def linear_dw(dy_bf16, x_bf16) -> np.ndarray:

@@ -92,6 +92,21 @@ def test_linear_dx_int8_approximates_dy_times_w():
     assert _rel(O.bf16_to_f32(O.linear_dx_int8(dy, w8, ws)), exact) < 0.03
 
 
+def test_linear_dx_is_torch_matmul():
+    """dy @ w (reference ops.py:204) in float64, and the transposed-operand
+    identity dy @ w == (w^T dy^T)^T == linear_dw(w, dy^T)^T, which a swapped
+    operand or a dropped transpose would break."""
+    g = torch.Generator().manual_seed(7)
+    dy = (torch.randn(33, 48, generator=g) * 1e-2).to(torch.bfloat16)
+    w = (torch.randn(48, 80, generator=g) * 0.05).to(torch.bfloat16)
+    b = lambda t: t.view(torch.int16).numpy().view(np.uint16)
+    want = (dy.double() @ w.double()).numpy()
+    assert np.allclose(O.linear_dx(b(dy), b(w)), want, rtol=0, atol=1e-12)
+    assert O.linear_dx(b(dy), b(w)).shape == (33, 80)
+    via_dw = O.linear_dw(np.ascontiguousarray(b(w)), np.ascontiguousarray(b(dy).T)).T
+    assert np.allclose(O.linear_dx(b(dy), b(w)), via_dw, rtol=0, atol=1e-12)
+
+
 def test_linear_dw_is_torch_matmul():
     rng = np.random.default_rng(6)
     dy = O.f32_to_bf16(rng.standard_normal((64, 48)).astype(np.float32))
