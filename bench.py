@@ -7,17 +7,23 @@ A *step* is one ``xpu_kernels.int8.linear`` at config 3 of BASELINE.json
 (x bf16 [4096,1280] with 1% outlier channels x30, W prepared from bf16
 [10240,1280], bias bf16 [10240]): rotate+quantize of x, then the int8 MFMA
 GEMM with the dequant+bias epilogue fused into its store.  Inputs are resident
-in HBM before the timed region; W is prepared once, untimed.  An untimed run-in
-of S seconds (default 0.25, so the GPU clock reaches its sustained level), W
-warm-up steps, then exactly K steps between two ``torch.cuda.synchronize()`` calls, timed with
-HIP events on the stream the kernels run on (torch's current stream).
+in HBM before the timed region and *cold*: each call takes its own set of
+(x, w8, w_scale, bias), and the sets together exceed 640 MB, so no call finds
+its operands in the 256 MB Infinity Cache or the L2s (the buffer-warmth trap
+the reference's docs/performance.md:104-114 warns about).  The same call on
+one set of buffers is reported beside it as the warm figure.  Weights are
+prepared once, untimed.  An untimed run-in of S seconds (default 0.25, so the
+GPU clock reaches its sustained level), W warm-up steps, then exactly K steps
+between two ``torch.cuda.synchronize()`` calls, timed with HIP events on the
+stream the kernels run on (torch's current stream).
 
 ``value`` is end-to-end TOP/s at config 3 (2*M*N*K = 107.37 GOP per step).
-The other configurations are measured after it and reported under ``extra``.
-``roofline`` is the GEMM kernel's own average duration against the dense INT8
-MFMA peak; ``cpu_baseline`` times the oracle (a numpy port of the reference
-chain) on a bounded row sample of config 3 on this host.  One JSON line on
-stdout; progress goes to stderr.
+The other configurations are measured after it and reported under ``extra``,
+the HBM-bound ones cold and warm.  ``roofline`` is the GEMM kernel's own
+average duration (cold operands) against the dense INT8 MFMA peak;
+``cpu_baseline`` times the reference's oracle (reference/convrot_linear.py,
+restated in torch with the real rotation: oracle/torch_chain.py) on this
+host's cores.  One JSON line on stdout; progress goes to stderr.
 """
 
 from __future__ import annotations
@@ -91,67 +97,116 @@ def settle(torch, fn, seconds):
 
 
 def timed(torch, fn, steps, warmup, settle_s=0.0):
-    """Average ms per call of ``fn`` over ``steps`` calls (HIP events on the
-    current stream, after a ``settle_s`` run-in and ``warmup`` untimed calls)."""
-    settle(torch, fn, settle_s)
-    for _ in range(warmup):
-        fn()
+    """Average ms per call of ``fn(i)`` over calls i = 0 .. steps-1 (HIP events
+    on the current stream, after a ``settle_s`` run-in and ``warmup`` untimed
+    calls).  ``fn`` takes the call index so that a cold measurement can walk
+    through several buffer sets."""
+    settle(torch, lambda: fn(0), settle_s)
+    for i in range(warmup):
+        fn(i)
     torch.cuda.synchronize()
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     a.record()
-    for _ in range(steps):
-        fn()
+    for i in range(steps):
+        fn(i)
     b.record()
     torch.cuda.synchronize()
     return a.elapsed_time(b) / steps
 
 
+COLD_BYTES = 640 << 20           # buffer sets per cold measurement: > 2.5x the 256 MB MALL
+
+
+def n_sets(bytes_per_set, cap=48):
+    """How many distinct buffer sets a cold measurement rotates through, so
+    that the bytes touched between two uses of one set exceed the MI355X's
+    256 MB Infinity Cache (and the 4 MB L2s): each call then reads its inputs
+    from HBM, as the reference's own measurement notes require (fresh
+    buffers, docs/performance.md:104-114)."""
+    return max(2, min(cap, -(-COLD_BYTES // int(bytes_per_set))))
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(seconds):
-    """The oracle's chain (rotate+quantize, int_mm, dequant) on a row sample
-    of config 3, on this host's cores."""
-    import numpy as np
-    import oracle as O
-    rng = np.random.default_rng(0)
-    m, k, n = 256, 1280, 10240
-    x = rng.standard_normal((m, k)).astype(np.float32)
-    x[:, rng.permutation(k)[:13]] *= 30
-    xb = O.f32_to_bf16(x)
-    w8 = rng.integers(-127, 128, (n, k), dtype=np.int8)
-    ws = rng.uniform(1e-4, 1e-3, n).astype(np.float32)
-    bias = rng.standard_normal(n).astype(np.float32) * 0.01
-    O.linear(xb, w8, ws, bias)                       # warm-up
-    times = []
-    t_end = time.perf_counter() + seconds
-    while time.perf_counter() < t_end or len(times) < 3:
-        t0 = time.perf_counter()
-        O.linear(xb, w8, ws, bias)
-        times.append(time.perf_counter() - t0)
-    med = sorted(times)[len(times) // 2]
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    """The reference's own oracle, reference/convrot_linear.py:5-23, as a
+    torch-CPU chain with the real rotation in place of its identity
+    (oracle/torch_chain.py), on this host's cores: the full config 1 and a
+    row sample of config 3, median of >= 5 runs each."""
+    import statistics
+    import torch
+    from oracle import torch_chain as TC
+    affinity = len(os.sched_getaffinity(0))
+    share = int(os.environ.get("OMP_NUM_THREADS", affinity) or affinity)
+    threads = max(1, min(affinity, share))
+    torch.set_num_threads(threads)
+    h = TC.hadamard_matrix()
+
+    def case(m, k, n, seed):
+        x = activation(torch, m, k, seed=seed, n_out=8 if m == 1024 and n == 1280 else None,
+                       mult=20.0 if m == 1024 and n == 1280 else 30.0)
+        g = torch.Generator().manual_seed(seed + 1)
+        w8 = torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8)
+        ws = torch.rand(n, generator=g) * 1e-3 + 1e-4
+        bias = (torch.randn(n, generator=g) * 0.01).to(torch.bfloat16)
+        return x, w8, ws, bias
+
+    def median_ms(args, budget):
+        TC.convrot_int8_linear(*args, h=h)                   # warm-up
+        times = []
+        t_end = time.perf_counter() + budget
+        while time.perf_counter() < t_end or len(times) < 5:
+            t0 = time.perf_counter()
+            TC.convrot_int8_linear(*args, h=h)
+            times.append(time.perf_counter() - t0)
+        return statistics.median(times) * 1e3, len(times)
+
+    c1 = case(1024, 1280, 1280, 0)
+    ms1, n1 = median_ms(c1, seconds * 0.25)
+    m3 = 1024
+    c3 = case(m3, 1280, 10240, 3)
+    ms3, n3 = median_ms(c3, seconds * 0.75)
+    ops3 = 2.0 * m3 * 10240 * 1280
     return {
-        "value": round(2.0 * m * n * k / med / 1e12, 5),
+        "value": round(ops3 / (ms3 * 1e-3) / 1e12, 5),
         "unit": "TOP/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"oracle.linear (numpy: Hadamard+quantize, exact float64 BLAS int_mm, "
-                  f"dequant) on {m} of config 3's 4096 rows, K=1280, N=10240; median of "
-                  f"{len(times)} runs ({med * 1e3:.1f} ms each)",
+        "cpu": cpu_model(),
+        "affinity_cpus": affinity,
+        "config1_ms": round(ms1, 3),
+        "config1_GOP/s": round(2.0 * 1024 * 1280 * 1280 / (ms1 * 1e-3) / 1e9, 2),
+        "sample": f"reference/convrot_linear.py restated in torch on the CPU (fp32 256x256 "
+                  f"Hadamard matmul, fp32 scale, IEEE division, torch._int_mm, dequant, bf16 "
+                  f"bias) at {threads} threads: config 3 on {m3} of its 4096 rows "
+                  f"(K=1280, N=10240), median of {n3} runs ({ms3:.1f} ms each); config 1 "
+                  f"(1024x1280x1280) in full, median of {n1} runs",
     }
 
 
 def main():
-    ap = argparse.ArgumentParser()
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--settle", type=float, default=SETTLE_S,
-                    help="untimed run-in (seconds) before each measurement's warm-up, so the "
-                         "GPU clock has reached its sustained level (0 = none)")
+                    help="untimed run-in before each measurement, seconds (GPU clock ramp)")
     ap.add_argument("--only-main", action="store_true", help="config 3 only (for profiling)")
+    ap.add_argument("--only-rowquant", action="store_true",
+                    help="config 2 rotate+quantize only, cold then warm (for profiling)")
     ap.add_argument("--calibrate-copy", action="store_true",
-                    help="first run an elementwise int8 kernel over 256 MiB (reads and writes "
+                    help="first run a plain copy kernel (torch neg over 256 MiB in and out, "
                          "exactly 256 MiB) so counter runs can scale FETCH_SIZE/WRITE_SIZE")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -166,6 +221,8 @@ def main():
         raise SystemExit(f"libxpuint8 unavailable: {L._ERR}")
     dev = torch.device("cuda", 0)
     K, W, SET = args.steps, args.warmup, args.settle
+    lib = L._lib()
+    st = L._stream(dev)
     if args.calibrate_copy:
         src = torch.ones(CALIB_BYTES, dtype=torch.int8, device=dev)
         dst = torch.empty_like(src)
@@ -174,65 +231,134 @@ def main():
         torch.cuda.synchronize()
         del src, dst
 
+    def gbs(nbytes, ms):
+        return nbytes / (ms * 1e-3) / 1e9
+
+    def hbm_line(nbytes, ms_cold, ms_warm, **more):
+        d = {"ms_cold": round(ms_cold, 5), "GB/s_cold": round(gbs(nbytes, ms_cold), 1),
+             "frac_hbm_peak_cold": round(gbs(nbytes, ms_cold) / PEAK_HBM_GBPS, 4),
+             "ms_warm": round(ms_warm, 5), "GB/s_warm": round(gbs(nbytes, ms_warm), 1),
+             "bytes": int(nbytes)}
+        d.update(more)
+        return d
+
+    def dev_gen(seed):
+        return torch.Generator(device=dev).manual_seed(seed)
+
+    def dev_act(m, k, seed):
+        """activation() drawn on the device (extra buffer sets of a cold run)"""
+        x = torch.randn(m, k, device=dev, generator=dev_gen(seed))
+        cols = torch.randperm(k, device=dev, generator=dev_gen(seed + 7))[:max(1, round(0.01 * k))]
+        x[:, cols] *= 30
+        return x.to(torch.bfloat16)
+
+    def dev_weight(n, k, seed, std=0.02):
+        return (torch.randn(n, k, device=dev, generator=dev_gen(seed)) * std).to(torch.bfloat16)
+
+    extra = {}
     # ---------------------------------------------------------- config 3
     M, Kd, N = 4096, 1280, 10240
+    ops3 = 2.0 * M * N * Kd
     x = activation(torch, M, Kd).to(dev)
     w8, ws = int8.prepare_weight(weight(torch, N, Kd).to(dev))
     bias = weight(torch, 1, N, seed=2, std=0.01)[0].to(dev)
-    ops3 = 2.0 * M * N * Kd
-    log(f"[bench] config 3 linear {M}x{Kd}x{N}: {W} warm-up + {K} timed steps")
-    ms = timed(torch, lambda: int8.linear(x, w8, ws, bias), K, W, SET)
+    # cold: distinct (x, w8, ws, bias) per call, set 0 the recipe's own inputs
+    n3 = n_sets(2 * M * Kd + N * Kd + 6 * N)
+    sets3 = [(x, w8, ws, bias)]
+    for i in range(1, n3):
+        wi8, wis = int8.prepare_weight(dev_weight(N, Kd, 100 + i))
+        sets3.append((dev_act(M, Kd, 200 + i), wi8, wis, dev_weight(1, N, 300 + i, 0.01)[0]))
+    log(f"[bench] config 3 linear {M}x{Kd}x{N}: {W} warm-up + {K} timed steps, "
+        f"cold over {n3} input sets")
+    ms = timed(torch, lambda i: int8.linear(*sets3[i % n3]), K, W, SET)
+    ms_warm = timed(torch, lambda i: int8.linear(x, w8, ws, bias), K, W, SET)
     value = ops3 / (ms * 1e-3) / 1e12
 
-    # the dominant kernel alone: the GEMM with the fused epilogue
-    xq, xs = int8.quantize(x)
-    out = torch.empty((M, N), device=dev, dtype=torch.bfloat16)
-    lib = L._lib()
+    # the dominant kernel alone: the GEMM with the fused epilogue, each call on
+    # its own operands and output
+    ng = n_sets(M * Kd + N * Kd + 2 * M * N + 8 * N + 4 * M)
+    gsets = []
+    for i in range(ng):
+        xi, wi8, wis, bi = sets3[i % n3]
+        xq, xs = int8.quantize(xi)
+        gsets.append((xq, xs, wi8, wis, bi, torch.empty((M, N), device=dev, dtype=torch.bfloat16)))
 
-    def gemm():
-        lib.xpuint8_linear_gemm_stream(L._stream(dev), L._ptr(xq), L._ptr(xs), L._ptr(w8),
-                                       L._ptr(ws), L._ptr(bias), 1, L._ptr(out), M, N, Kd)
+    def gemm(i):
+        xq, xs, wi8, wis, bi, out = gsets[i % ng]
+        lib.xpuint8_linear_gemm_stream(st, L._ptr(xq), L._ptr(xs), L._ptr(wi8), L._ptr(wis),
+                                       L._ptr(bi), 1, L._ptr(out), M, N, Kd)
     ms_gemm = timed(torch, gemm, K, W, SET)
+    ms_gemm_warm = timed(torch, lambda i: gemm(0), K, W, SET)
     gemm_tops = ops3 / (ms_gemm * 1e-3) / 1e12
-    ms_q3 = timed(torch, lambda: int8.quantize(x), K, W, SET)
-    log(f"[bench] step {ms:.4f} ms = {value:.1f} TOP/s; GEMM {ms_gemm:.4f} ms = "
-        f"{gemm_tops:.1f} TOP/s; quantize {ms_q3:.4f} ms")
+    q3 = [(torch.empty((M, Kd), device=dev, dtype=torch.int8),
+           torch.empty(M, device=dev, dtype=torch.float32)) for _ in range(n3)]
 
-    extra = {"config3_gemm_ms": round(ms_gemm, 5), "config3_quantize_ms": round(ms_q3, 5)}
+    def quant3(i):
+        xi = sets3[i % n3][0]
+        qi, si = q3[i % n3]
+        lib.xpuint8_convrot_quantize_stream(st, L._ptr(xi), L._ptr(qi), L._ptr(si), M, Kd)
+    bytes_q3 = 3 * M * Kd + 4 * M
+    ms_q3 = timed(torch, quant3, K, W, SET)
+    ms_q3_warm = timed(torch, lambda i: quant3(0), K, W, SET)
+    log(f"[bench] step {ms:.4f} ms cold / {ms_warm:.4f} warm = {value:.1f} TOP/s; GEMM "
+        f"{ms_gemm:.4f} / {ms_gemm_warm:.4f} ms = {gemm_tops:.1f} TOP/s; quantize "
+        f"{ms_q3:.4f} / {ms_q3_warm:.4f} ms")
+    extra["config3_step_ms_warm"] = round(ms_warm, 5)
+    extra["config3_TOP/s_warm"] = round(ops3 / (ms_warm * 1e-3) / 1e12, 2)
+    extra["config3_gemm"] = {"ms_cold": round(ms_gemm, 5), "ms_warm": round(ms_gemm_warm, 5),
+                             "TOP/s_cold": round(gemm_tops, 1),
+                             "TOP/s_warm": round(ops3 / (ms_gemm_warm * 1e-3) / 1e12, 1)}
+    extra["config3_quantize"] = hbm_line(bytes_q3, ms_q3, ms_q3_warm)
+    del gsets
+
     if not args.only_main:
         # ------------------------------------------------------ config 2
-        # kernel throughput: the C entry point on preallocated outputs (the
+        # kernel throughput: the C entry points on preallocated outputs (the
         # python wrapper's own host cost, ~10 us per call, would otherwise
         # bound these ~10 us kernels); the API-level time is reported beside it
-        st = L._stream(dev)
-        x2 = activation(torch, 4096, 5120).to(dev)
-        q2 = torch.empty((4096, 5120), device=dev, dtype=torch.int8)
-        s2 = torch.empty(4096, device=dev, dtype=torch.float32)
-        ms_q = timed(torch, lambda: lib.xpuint8_convrot_quantize_stream(
-            st, L._ptr(x2), L._ptr(q2), L._ptr(s2), 4096, 5120), K, W, SET)
-        ms_q_api = timed(torch, lambda: int8.quantize(x2), K, W, SET)
-        bytes_q = 2 * 4096 * 5120 + 4096 * 5120 + 4 * 4096
-        w2 = weight(torch, 10240, 1280).to(dev)
-        q2w = torch.empty((10240, 1280), device=dev, dtype=torch.int8)
-        s2w = torch.empty(10240, device=dev, dtype=torch.float32)
-        ms_p = timed(torch, lambda: lib.xpuint8_prepare_weight_stream(
-            st, L._ptr(w2), L._ptr(q2w), L._ptr(s2w), 10240, 1280), K, W, SET)
-        bytes_p = 3 * 10240 * 1280 + 4 * 10240
-        extra["config2_rotate_quant"] = {
-            "ms": round(ms_q, 5), "GB/s": round(bytes_q / (ms_q * 1e-3) / 1e9, 1),
-            "frac_hbm_peak": round(bytes_q / (ms_q * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
-            "api_ms": round(ms_q_api, 5)}
-        extra["config2_prepare_weight"] = {
-            "ms": round(ms_p, 5), "GB/s": round(bytes_p / (ms_p * 1e-3) / 1e9, 1),
-            "frac_hbm_peak": round(bytes_p / (ms_p * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4)}
-        log(f"[bench] config 2: rotate+quant {ms_q:.4f} ms (API {ms_q_api:.4f}), "
-            f"prepare_weight {ms_p:.4f} ms")
+        Mr, Kr = 4096, 5120
+        bytes_q = 2 * Mr * Kr + Mr * Kr + 4 * Mr
+        n2 = n_sets(bytes_q)
+        x2 = activation(torch, Mr, Kr).to(dev)
+        sets2 = [(x2 if i == 0 else dev_act(Mr, Kr, 400 + i),
+                  torch.empty((Mr, Kr), device=dev, dtype=torch.int8),
+                  torch.empty(Mr, device=dev, dtype=torch.float32)) for i in range(n2)]
+
+        def rq(i):
+            xi, qi, si = sets2[i % n2]
+            lib.xpuint8_convrot_quantize_stream(st, L._ptr(xi), L._ptr(qi), L._ptr(si), Mr, Kr)
+        ms_q = timed(torch, rq, K, W, SET)
+        ms_q_warm = timed(torch, lambda i: rq(0), K, W, SET)
+        ms_q_api = timed(torch, lambda i: int8.quantize(x2), K, W, SET)
+        extra["config2_rotate_quant"] = hbm_line(bytes_q, ms_q, ms_q_warm, api_ms_warm=round(ms_q_api, 5),
+                                                 sets=n2)
+        del sets2
+        if args.only_rowquant:
+            pass
+        else:
+            bytes_p = 3 * 10240 * 1280 + 4 * 10240
+            npw = n_sets(bytes_p)
+            w2 = weight(torch, 10240, 1280).to(dev)
+            setsp = [(w2 if i == 0 else dev_weight(10240, 1280, 500 + i),
+                      torch.empty((10240, 1280), device=dev, dtype=torch.int8),
+                      torch.empty(10240, device=dev, dtype=torch.float32)) for i in range(npw)]
+
+            def pw(i):
+                wi, qi, si = setsp[i % npw]
+                lib.xpuint8_prepare_weight_stream(st, L._ptr(wi), L._ptr(qi), L._ptr(si), 10240, 1280)
+            ms_p = timed(torch, pw, K, W, SET)
+            ms_p_warm = timed(torch, lambda i: pw(0), K, W, SET)
+            extra["config2_prepare_weight"] = hbm_line(bytes_p, ms_p, ms_p_warm, sets=npw)
+            del setsp
+            log(f"[bench] config 2: rotate+quant {ms_q:.4f} ms cold / {ms_q_warm:.4f} warm "
+                f"(API {ms_q_api:.4f}), prepare_weight {ms_p:.4f} / {ms_p_warm:.4f} ms")
+    if not (args.only_main or args.only_rowquant):
         # ------------------------------------------------------ config 4
         xf = activation(torch, 4096, 1280, seed=3).to(dev)
         up8, ups = int8.prepare_weight(weight(torch, 10240, 1280, seed=4).to(dev))
         dn8, dns = int8.prepare_weight(weight(torch, 1280, 5120, seed=5).to(dev))
         db = weight(torch, 1, 1280, seed=6, std=0.01)[0].to(dev)
-        ms_f = timed(torch, lambda: int8.ffn(xf, up8, ups, dn8, dns, db, act="geglu_erf"), K, W, SET)
+        ms_f = timed(torch, lambda i: int8.ffn(xf, up8, ups, dn8, dns, db, act="geglu_erf"), K, W, SET)
         ops4 = 2.0 * 4096 * 1280 * 10240 + 2.0 * 4096 * 5120 * 1280
         extra["config4_ffn"] = {"ms": round(ms_f, 5), "TOP/s": round(ops4 / (ms_f * 1e-3) / 1e12, 1)}
         log(f"[bench] config 4: ffn {ms_f:.4f} ms")
@@ -241,55 +367,92 @@ def main():
         dy = (torch.randn(4096, 5120, generator=torch.Generator().manual_seed(8)) * 1e-3
               ).to(torch.bfloat16).to(dev)
         x5 = activation(torch, 4096, 1280, seed=9).to(dev)
-        ms_dx = timed(torch, lambda: int8.linear_dx_int8(dy, w5_8, w5_s), K, W, SET)
-        ms_dw = timed(torch, lambda: int8.linear_dw(dy, x5), K, W, SET)
-        q5 = torch.empty((4096, 5120), device=dev, dtype=torch.int8)
-        s5 = torch.empty(4096, device=dev, dtype=torch.float32)
-        ms_rq = timed(torch, lambda: lib.xpuint8_quantize_row_stream(
-            st, L._ptr(dy), L._ptr(w5_s), L._ptr(q5), L._ptr(s5), 4096, 5120), K, W, SET)
+        ms_dx = timed(torch, lambda i: int8.linear_dx_int8(dy, w5_8, w5_s), K, W, SET)
+        ms_dw = timed(torch, lambda i: int8.linear_dw(dy, x5), K, W, SET)
+        w5d = int8.dequant_weight(w5_8, w5_s)
+        ms_dxd = timed(torch, lambda i: int8.linear_dx(dy, w5d), K, W, SET)
         ops5 = 2.0 * 4096 * 5120 * 1280
-        bytes_rq = 3 * 4096 * 5120 + 4 * 4096
         extra["config5_dx_int8"] = {"ms": round(ms_dx, 5), "TOP/s": round(ops5 / (ms_dx * 1e-3) / 1e12, 1)}
         extra["config5_dw"] = {"ms": round(ms_dw, 5), "TFLOP/s": round(ops5 / (ms_dw * 1e-3) / 1e12, 1)}
-        extra["config5_quantize_row"] = {"ms": round(ms_rq, 5),
-                                         "GB/s": round(bytes_rq / (ms_rq * 1e-3) / 1e9, 1)}
-        xs16 = activation(torch, 16, 4096, seed=10).to(dev)
-        sk8, sks = int8.prepare_weight(weight(torch, 4096, 4096, seed=11).to(dev))
-        ms_sk_api = timed(torch, lambda: int8.linear(xs16, sk8, sks), K, W, SET)
-        # the weight-streaming GEMM itself (quantized x resident, preallocated out)
-        q16, s16 = int8.quantize(xs16)
-        o16 = torch.empty((16, 4096), device=dev, dtype=torch.bfloat16)
-        ms_sk = timed(torch, lambda: lib.xpuint8_linear_gemm_stream(
-            st, L._ptr(q16), L._ptr(s16), L._ptr(sk8), L._ptr(sks), None, 0, L._ptr(o16),
-            16, 4096, 4096), K, W, SET)
+        extra["config5_dx_dense"] = {"ms": round(ms_dxd, 5),
+                                     "TFLOP/s": round(ops5 / (ms_dxd * 1e-3) / 1e12, 1)}
+        bytes_rq = 3 * 4096 * 5120 + 4 * 4096
+        nrq = n_sets(bytes_rq)
+        setsr = [(dy if i == 0 else (torch.randn(4096, 5120, device=dev, generator=dev_gen(600 + i))
+                                     * 1e-3).to(torch.bfloat16),
+                  torch.empty((4096, 5120), device=dev, dtype=torch.int8),
+                  torch.empty(4096, device=dev, dtype=torch.float32)) for i in range(nrq)]
+
+        def qrow(i):
+            di, qi, si = setsr[i % nrq]
+            lib.xpuint8_quantize_row_stream(st, L._ptr(di), L._ptr(w5_s), L._ptr(qi), L._ptr(si),
+                                            4096, 5120)
+        ms_rq = timed(torch, qrow, K, W, SET)
+        ms_rq_warm = timed(torch, lambda i: qrow(0), K, W, SET)
+        extra["config5_quantize_row"] = hbm_line(bytes_rq, ms_rq, ms_rq_warm, sets=nrq)
+        del setsr
+        # skinny M=16: the weight streamed once per call
         bytes_sk = 4096 * 4096 + 16 * 4096 + 2 * 16 * 4096 + 4 * 4096 + 4 * 16
-        extra["config5_skinny_m16"] = {
-            "ms": round(ms_sk, 5), "GB/s": round(bytes_sk / (ms_sk * 1e-3) / 1e9, 1),
-            "frac_hbm_peak": round(bytes_sk / (ms_sk * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
-            "api_ms": round(ms_sk_api, 5)}
-        log(f"[bench] config 5: dx {ms_dx:.4f} ms, dW {ms_dw:.4f} ms, quantize_row {ms_rq:.4f} ms, "
-            f"skinny {ms_sk:.4f} ms")
+        nsk = n_sets(bytes_sk)
+        xs16 = activation(torch, 16, 4096, seed=10).to(dev)
+        sk = [int8.prepare_weight(weight(torch, 4096, 4096, seed=11).to(dev))]
+        sk += [int8.prepare_weight(dev_weight(4096, 4096, 700 + i)) for i in range(1, nsk)]
+        q16, s16 = int8.quantize(xs16)
+        o16 = [torch.empty((16, 4096), device=dev, dtype=torch.bfloat16) for _ in range(nsk)]
+
+        def skinny(i):
+            w_i, s_i = sk[i % nsk]
+            lib.xpuint8_linear_gemm_stream(st, L._ptr(q16), L._ptr(s16), L._ptr(w_i), L._ptr(s_i),
+                                           None, 0, L._ptr(o16[i % nsk]), 16, 4096, 4096)
+        ms_sk = timed(torch, skinny, K, W, SET)
+        ms_sk_warm = timed(torch, lambda i: skinny(0), K, W, SET)
+        ms_sk_api = timed(torch, lambda i: int8.linear(xs16, *sk[0]), K, W, SET)
+        # the same API call captured once in a HIP graph and replayed: what a
+        # serving loop pays per call without the Python host cost
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(3):
+                int8.linear(xs16, *sk[0])
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            int8.linear(xs16, *sk[0])
+        ms_sk_graph = timed(torch, lambda i: graph.replay(), K, W, SET)
+        extra["config5_skinny_m16"] = hbm_line(bytes_sk, ms_sk, ms_sk_warm, sets=nsk,
+                                               api_ms=round(ms_sk_api, 5),
+                                               api_graph_replay_ms=round(ms_sk_graph, 5))
+        del sk, graph
+        log(f"[bench] config 5: dx {ms_dx:.4f} ms, dW {ms_dw:.4f} ms, dense dx {ms_dxd:.4f} ms, "
+            f"quantize_row {ms_rq:.4f} / {ms_rq_warm:.4f} ms, skinny {ms_sk:.4f} / "
+            f"{ms_sk_warm:.4f} ms (API {ms_sk_api:.4f}, graph replay {ms_sk_graph:.4f})")
 
         # ------------------------------------ accumulator consumer: rms + rope
         # q slice [1, 4096, 24, 128] of a qkv accumulator [4096, 3*3072]
         from xpu_kernels import rope
         S_r, H_r, D_r = 4096, 24, 128
         g_r = torch.Generator().manual_seed(12)
-        acc_r = torch.randint(-2 ** 17, 2 ** 17, (1, S_r, 3 * H_r * D_r), generator=g_r,
-                              dtype=torch.int32).to(dev)
-        q_acc = acc_r[..., : H_r * D_r].unflatten(-1, (H_r, D_r))
+        bytes_rope = S_r * H_r * D_r * (4 + 2) + 4 * S_r + 4 * H_r * D_r
+        nro = n_sets(S_r * 3 * H_r * D_r * 4)
+        accs = [torch.randint(-2 ** 17, 2 ** 17, (1, S_r, 3 * H_r * D_r), generator=g_r,
+                              dtype=torch.int32).to(dev)]
+        accs += [torch.randint(-2 ** 17, 2 ** 17, (1, S_r, 3 * H_r * D_r), device=dev,
+                               generator=dev_gen(800 + i), dtype=torch.int32) for i in range(1, nro)]
         xs_r = (torch.rand(1, S_r, generator=g_r) * 0.05).to(dev)
         ws_r = (torch.rand(H_r * D_r, generator=g_r) * 1e-4).to(dev)
         th = torch.rand(1, S_r, 1, D_r // 2, generator=g_r) * 6.28
         f_r = torch.stack([torch.stack([th.cos(), -th.sin()], -1),
                            torch.stack([th.sin(), th.cos()], -1)], -2).to(dev)
         sc_r = torch.ones(D_r, device=dev)
-        ms_rope = timed(torch, lambda: rope.rows_dq(q_acc, f_r, sc_r, 1e-6, xs_r, ws_r), K, W, SET)
-        bytes_rope = S_r * H_r * D_r * (4 + 2) + 4 * S_r + 4 * H_r * D_r
-        extra["rms_rope_dequant_s4096_h24_d128"] = {
-            "ms": round(ms_rope, 5), "GB/s": round(bytes_rope / (ms_rope * 1e-3) / 1e9, 1),
-            "frac_hbm_peak": round(bytes_rope / (ms_rope * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4)}
-        log(f"[bench] rms+rope dequant: {ms_rope:.4f} ms")
+        qsl = [a[..., : H_r * D_r].unflatten(-1, (H_r, D_r)) for a in accs]
+        ms_rope = timed(torch, lambda i: rope.rows_dq(qsl[i % nro], f_r, sc_r, 1e-6, xs_r, ws_r),
+                        K, W, SET)
+        ms_rope_warm = timed(torch, lambda i: rope.rows_dq(qsl[0], f_r, sc_r, 1e-6, xs_r, ws_r),
+                             K, W, SET)
+        extra["rms_rope_dequant_s4096_h24_d128"] = hbm_line(bytes_rope, ms_rope, ms_rope_warm,
+                                                            sets=nro)
+        del accs, qsl
+        log(f"[bench] rms+rope dequant: {ms_rope:.4f} / {ms_rope_warm:.4f} ms")
 
     line = {
         "metric": "int8_linear TOPS (M=4096,K=1280,N=10240); rotate+quant HBM GB/s",
@@ -304,15 +467,17 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8",
-        "data": "synthetic (BASELINE.json config 3 recipe, torch CPU generator seed 0)",
+        "data": f"synthetic (BASELINE.json config 3 recipe, torch CPU generator seed 0; "
+                f"cold: {n3} input sets, > 640 MB between reuses)",
         "config": {"workload": "config 3: int8_linear forward M=4096 K=1280 N=10240 "
-                               "(rotate+quantize + int8 MFMA GEMM with fused dequant+bias)",
+                               "(rotate+quantize + int8 MFMA GEMM with fused dequant+bias), "
+                               "inputs cold in HBM",
                    "M": M, "K": Kd, "N": N, "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": round(gemm_tops, 2), "peak": PEAK_INT8_TOPS,
                      "unit": "TOP/s", "frac": round(gemm_tops / PEAK_INT8_TOPS, 4),
                      "traffic": measured_traffic(),
                      "kernel": "gemm_i8_pp_kernel (persistent 256x320 ping-pong) with dequant epilogue "
-                               "(2*M*N*K int ops per launch)"},
+                               "(2*M*N*K int ops per launch, cold operands)"},
         "extra": extra,
     }
     if not args.no_cpu:
