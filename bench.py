@@ -205,6 +205,9 @@ def main():
     ap.add_argument("--only-main", action="store_true", help="config 3 only (for profiling)")
     ap.add_argument("--only-rowquant", action="store_true",
                     help="config 2 rotate+quantize only, cold then warm (for profiling)")
+    ap.add_argument("--only-gemm", action="store_true",
+                    help="the config-3 GEMM alone, cold, and nothing else (for profiling: its "
+                         "launches are then the only ones of that kernel in the run)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run a plain copy kernel (torch neg over 256 MiB in and out, "
                          "exactly 256 MiB) so counter runs can scale FETCH_SIZE/WRITE_SIZE")
@@ -270,8 +273,11 @@ def main():
         sets3.append((dev_act(M, Kd, 200 + i), wi8, wis, dev_weight(1, N, 300 + i, 0.01)[0]))
     log(f"[bench] config 3 linear {M}x{Kd}x{N}: {W} warm-up + {K} timed steps, "
         f"cold over {n3} input sets")
-    ms = timed(torch, lambda i: int8.linear(*sets3[i % n3]), K, W, SET)
-    ms_warm = timed(torch, lambda i: int8.linear(x, w8, ws, bias), K, W, SET)
+    if args.only_gemm or args.only_rowquant:
+        ms = ms_warm = float("nan")
+    else:
+        ms = timed(torch, lambda i: int8.linear(*sets3[i % n3]), K, W, SET)
+        ms_warm = timed(torch, lambda i: int8.linear(x, w8, ws, bias), K, W, SET)
     value = ops3 / (ms * 1e-3) / 1e12
 
     # the dominant kernel alone: the GEMM with the fused epilogue, each call on
@@ -287,8 +293,16 @@ def main():
         xq, xs, wi8, wis, bi, out = gsets[i % ng]
         lib.xpuint8_linear_gemm_stream(st, L._ptr(xq), L._ptr(xs), L._ptr(wi8), L._ptr(wis),
                                        L._ptr(bi), 1, L._ptr(out), M, N, Kd)
-    ms_gemm = timed(torch, gemm, K, W, SET)
-    ms_gemm_warm = timed(torch, lambda i: gemm(0), K, W, SET)
+    ms_gemm = ms_gemm_warm = float("nan")
+    if not args.only_rowquant:
+        ms_gemm = timed(torch, gemm, K, W, SET)
+    if args.only_gemm:
+        print(json.dumps({"only_gemm": True, "gemm_ms_cold": round(ms_gemm, 5),
+                          "TOP/s": round(ops3 / (ms_gemm * 1e-3) / 1e12, 1),
+                          "steps": K, "warmup": W, "sets": ng}), flush=True)
+        return
+    if not args.only_rowquant:
+        ms_gemm_warm = timed(torch, lambda i: gemm(0), K, W, SET)
     gemm_tops = ops3 / (ms_gemm * 1e-3) / 1e12
     q3 = [(torch.empty((M, Kd), device=dev, dtype=torch.int8),
            torch.empty(M, device=dev, dtype=torch.float32)) for _ in range(n3)]
@@ -298,8 +312,10 @@ def main():
         qi, si = q3[i % n3]
         lib.xpuint8_convrot_quantize_stream(st, L._ptr(xi), L._ptr(qi), L._ptr(si), M, Kd)
     bytes_q3 = 3 * M * Kd + 4 * M
-    ms_q3 = timed(torch, quant3, K, W, SET)
-    ms_q3_warm = timed(torch, lambda i: quant3(0), K, W, SET)
+    ms_q3 = ms_q3_warm = float("nan")
+    if not args.only_rowquant:
+        ms_q3 = timed(torch, quant3, K, W, SET)
+        ms_q3_warm = timed(torch, lambda i: quant3(0), K, W, SET)
     log(f"[bench] step {ms:.4f} ms cold / {ms_warm:.4f} warm = {value:.1f} TOP/s; GEMM "
         f"{ms_gemm:.4f} / {ms_gemm_warm:.4f} ms = {gemm_tops:.1f} TOP/s; quantize "
         f"{ms_q3:.4f} / {ms_q3_warm:.4f} ms")
@@ -328,30 +344,40 @@ def main():
             xi, qi, si = sets2[i % n2]
             lib.xpuint8_convrot_quantize_stream(st, L._ptr(xi), L._ptr(qi), L._ptr(si), Mr, Kr)
         ms_q = timed(torch, rq, K, W, SET)
+        if args.only_rowquant:
+            print(json.dumps({"only_rowquant": True, "rotate_quant_ms_cold": round(ms_q, 5),
+                              "GB/s": round(gbs(bytes_q, ms_q), 1), "steps": K, "warmup": W,
+                              "sets": n2}), flush=True)
+            return
         ms_q_warm = timed(torch, lambda i: rq(0), K, W, SET)
         ms_q_api = timed(torch, lambda i: int8.quantize(x2), K, W, SET)
-        extra["config2_rotate_quant"] = hbm_line(bytes_q, ms_q, ms_q_warm, api_ms_warm=round(ms_q_api, 5),
-                                                 sets=n2)
-        del sets2
-        if args.only_rowquant:
-            pass
-        else:
-            bytes_p = 3 * 10240 * 1280 + 4 * 10240
-            npw = n_sets(bytes_p)
-            w2 = weight(torch, 10240, 1280).to(dev)
-            setsp = [(w2 if i == 0 else dev_weight(10240, 1280, 500 + i),
-                      torch.empty((10240, 1280), device=dev, dtype=torch.int8),
-                      torch.empty(10240, device=dev, dtype=torch.float32)) for i in range(npw)]
+        # the same traffic through torch's vectorized elementwise kernel (read
+        # the bf16 tensor, write one byte per element: x != 0 into a bool
+        # tensor), on the same cold sets: what a plain streaming kernel
+        # reaches for this pattern on this box
+        ne_out = [torch.empty((Mr, Kr), device=dev, dtype=torch.bool) for _ in range(n2)]
+        ms_copy = timed(torch, lambda i: torch.ne(sets2[i % n2][0], 0, out=ne_out[i % n2]), K, W, SET)
+        extra["config2_rotate_quant"] = hbm_line(
+            bytes_q, ms_q, ms_q_warm, api_ms_warm=round(ms_q_api, 5), sets=n2,
+            streaming_ceiling_ms_cold=round(ms_copy, 5),
+            streaming_ceiling_frac_hbm_peak_cold=round(gbs(3 * Mr * Kr, ms_copy) / PEAK_HBM_GBPS, 4))
+        del sets2, ne_out
+        bytes_p = 3 * 10240 * 1280 + 4 * 10240
+        npw = n_sets(bytes_p)
+        w2 = weight(torch, 10240, 1280).to(dev)
+        setsp = [(w2 if i == 0 else dev_weight(10240, 1280, 500 + i),
+                  torch.empty((10240, 1280), device=dev, dtype=torch.int8),
+                  torch.empty(10240, device=dev, dtype=torch.float32)) for i in range(npw)]
 
-            def pw(i):
-                wi, qi, si = setsp[i % npw]
-                lib.xpuint8_prepare_weight_stream(st, L._ptr(wi), L._ptr(qi), L._ptr(si), 10240, 1280)
-            ms_p = timed(torch, pw, K, W, SET)
-            ms_p_warm = timed(torch, lambda i: pw(0), K, W, SET)
-            extra["config2_prepare_weight"] = hbm_line(bytes_p, ms_p, ms_p_warm, sets=npw)
-            del setsp
-            log(f"[bench] config 2: rotate+quant {ms_q:.4f} ms cold / {ms_q_warm:.4f} warm "
-                f"(API {ms_q_api:.4f}), prepare_weight {ms_p:.4f} / {ms_p_warm:.4f} ms")
+        def pw(i):
+            wi, qi, si = setsp[i % npw]
+            lib.xpuint8_prepare_weight_stream(st, L._ptr(wi), L._ptr(qi), L._ptr(si), 10240, 1280)
+        ms_p = timed(torch, pw, K, W, SET)
+        ms_p_warm = timed(torch, lambda i: pw(0), K, W, SET)
+        extra["config2_prepare_weight"] = hbm_line(bytes_p, ms_p, ms_p_warm, sets=npw)
+        del setsp
+        log(f"[bench] config 2: rotate+quant {ms_q:.4f} ms cold / {ms_q_warm:.4f} warm "
+            f"(API {ms_q_api:.4f}), prepare_weight {ms_p:.4f} / {ms_p_warm:.4f} ms")
     if not (args.only_main or args.only_rowquant):
         # ------------------------------------------------------ config 4
         xf = activation(torch, 4096, 1280, seed=3).to(dev)
