@@ -25,6 +25,7 @@
 // the 8 XCDs (blockIdx % 8) works on a compact rectangle of the output,
 // keeping its X rows and W rows in its own L2.
 #include <algorithm>
+#include <type_traits>
 
 #include "activations.hpp"
 #include "common.hpp"
@@ -1242,17 +1243,23 @@ hipError_t launch_splitk(hipStream_t st, const int8_t* X, int64_t ldx, const int
 // ------------------------------------------------------------ skinny M
 // M <= 64: the product streams the weight once, so it is bound by HBM
 // bandwidth, and tiles of 128+ rows would leave most CUs idle.  A block owns 16
-// weight rows (one MFMA row block) and all MB 16-row blocks of X; its 4 waves
-// take every 4th 64-byte K step and keep their operands in registers, loaded
+// weight rows (one MFMA row block) and all MB 16-row blocks of X; its NW waves
+// take every NW-th 64-byte K step and keep their operands in registers, loaded
 // straight from global memory in the MFMA layout (lane l: row l%16, bytes
-// 16*(l/16) of the step) D steps ahead.  The four partial accumulators meet in
-// LDS; the epilogue is the per-block form of the same Epi.
-template <int MB, class Epi>
-__global__ __launch_bounds__(256) void gemm_i8_skinny_kernel(
+// 16*(l/16) of the step) D steps ahead.  With NW = 16 a block requests its
+// whole 64 KB weight slice (K = 4096) at once, one block per CU: the weight is
+// streamed at the HBM rate instead of at the latency of a few steps in flight
+// per wave.  The NW partial accumulators meet in LDS; the epilogue is the
+// per-block form of the same Epi.  NW follows the number of K steps (about
+// four per wave): at M=16, N=4096 and K=4096 sixteen waves cut the cold call
+// from 8.7 to 7.2 us, while at K=1280 four waves stay fastest (6.8 us against
+// 7.7 with eight and 8.6 with sixteen).
+template <int MB, int NW, class Epi>
+__global__ __launch_bounds__(NW * 64) void gemm_i8_skinny_kernel(
     const int8_t* __restrict__ X, int64_t ldx, const int8_t* __restrict__ W, int64_t ldw, int M,
     int N, int K, Epi epi) {
-    constexpr int D = MB <= 2 ? 8 : 4;                       // steps in flight per wave
-    __shared__ v4i part[4][MB][64];
+    constexpr int D = NW >= 16 ? 4 : (MB <= 2 ? 8 : 4);     // steps in flight per wave
+    __shared__ v4i part[NW][MB][64];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int n0 = blockIdx.x * 16;
@@ -1261,7 +1268,10 @@ __global__ __launch_bounds__(256) void gemm_i8_skinny_kernel(
     const int8_t* xrow[MB];
 #pragma unroll
     for (int b = 0; b < MB; ++b) xrow[b] = X + int64_t(min(16 * b + (lane & 15), M - 1)) * ldx + kb;
-    const int S = (K + 63) / 64;                             // K steps; this wave: wave, wave+4, ...
+    const int S = (K + 63) / 64;                             // K steps
+    // the wave's t-th step (pairing consecutive steps in one wave, so it reads
+    // both halves of a 128-byte row segment back to back, measured slower)
+    auto stepidx = [&](int t) { return wave + NW * t; };
     v4i wbuf[D], xbuf[D][MB];
     auto load = [&](int slot, int step) {
         const int k = step * 64;
@@ -1279,23 +1289,25 @@ __global__ __launch_bounds__(256) void gemm_i8_skinny_kernel(
 #pragma unroll
     for (int b = 0; b < MB; ++b) acc[b] = v4i{0, 0, 0, 0};
 #pragma unroll
-    for (int j = 0; j < D; ++j) load(j, wave + 4 * j);
-    for (int s0 = 0; wave + 4 * s0 < S; s0 += D) {
+    for (int j = 0; j < D; ++j) load(j, stepidx(j));
+    for (int s0 = 0; stepidx(s0) < S; s0 += D) {
 #pragma unroll
         for (int j = 0; j < D; ++j) {
 #pragma unroll
             for (int b = 0; b < MB; ++b)
                 acc[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wbuf[j], xbuf[j][b], acc[b], 0, 0, 0);
-            load(j, wave + 4 * (s0 + j + D));
+            load(j, stepidx(s0 + j + D));
         }
     }
 #pragma unroll
     for (int b = 0; b < MB; ++b) part[wave][b][lane] = acc[b];
     __syncthreads();
-    // wave w finishes m-blocks w, w+4, ...: lane l holds rows 4*(l/16)+i of
+    // wave w finishes m-blocks w, w+NW, ...: lane l holds rows 4*(l/16)+i of
     // the weight block (n) for x row l%16 (m)
-    for (int b = wave; b < MB; b += 4) {
-        const v4i v = part[0][b][lane] + part[1][b][lane] + part[2][b][lane] + part[3][b][lane];
+    for (int b = wave; b < MB; b += NW) {
+        v4i v = part[0][b][lane];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) v += part[w][b][lane];
         const int m = 16 * b + (lane & 15);
         const int n = n0 + 4 * (lane >> 4);
         if (m < M && n < N) epi(m, n, v);
@@ -1305,13 +1317,21 @@ __global__ __launch_bounds__(256) void gemm_i8_skinny_kernel(
 template <class Epi>
 hipError_t launch_skinny(hipStream_t st, const int8_t* X, int64_t ldx, const int8_t* W,
                          int64_t ldw, int M, int N, int K, const Epi& epi) {
-    const dim3 grid(unsigned((N + 15) / 16)), block(256);
-    switch ((M + 15) / 16) {
-        case 1: hipLaunchKernelGGL((gemm_i8_skinny_kernel<1, Epi>), grid, block, 0, st, X, ldx, W, ldw, M, N, K, epi); break;
-        case 2: hipLaunchKernelGGL((gemm_i8_skinny_kernel<2, Epi>), grid, block, 0, st, X, ldx, W, ldw, M, N, K, epi); break;
-        case 3: hipLaunchKernelGGL((gemm_i8_skinny_kernel<3, Epi>), grid, block, 0, st, X, ldx, W, ldw, M, N, K, epi); break;
-        default: hipLaunchKernelGGL((gemm_i8_skinny_kernel<4, Epi>), grid, block, 0, st, X, ldx, W, ldw, M, N, K, epi); break;
-    }
+    const dim3 grid(unsigned((N + 15) / 16));
+    const int S = (K + 63) / 64;
+    auto go = [&](auto NWc) {
+        constexpr int NWV = decltype(NWc)::value;
+        const dim3 block(NWV * 64);
+        switch ((M + 15) / 16) {
+            case 1: hipLaunchKernelGGL((gemm_i8_skinny_kernel<1, NWV, Epi>), grid, block, 0, st, X, ldx, W, ldw, M, N, K, epi); break;
+            case 2: hipLaunchKernelGGL((gemm_i8_skinny_kernel<2, NWV, Epi>), grid, block, 0, st, X, ldx, W, ldw, M, N, K, epi); break;
+            case 3: hipLaunchKernelGGL((gemm_i8_skinny_kernel<3, NWV, Epi>), grid, block, 0, st, X, ldx, W, ldw, M, N, K, epi); break;
+            default: hipLaunchKernelGGL((gemm_i8_skinny_kernel<4, NWV, Epi>), grid, block, 0, st, X, ldx, W, ldw, M, N, K, epi); break;
+        }
+    };
+    if (S >= 64) go(std::integral_constant<int, 16>{});
+    else if (S >= 32) go(std::integral_constant<int, 8>{});
+    else go(std::integral_constant<int, 4>{});
     return hipGetLastError();
 }
 
