@@ -173,10 +173,17 @@ int dx_chain(hipStream_t st, const void* dy, const float* w_scale, const int8_t*
     int8_t* wt = reinterpret_cast<int8_t*>(work + L.wt);
     void* pre = work + L.pre;
     XPU_TRY(launched(quantize_row(st, dy, w_scale, q, a, M, int(N)), "linear_dx_int8 (quantize_row)"));
-    XPU_TRY(launched(transpose_i8(st, w8, wt, N, K), "linear_dx_int8 (transpose)"));
-    XPU_TRY(launched(gemm_dequant(st, q, N, wt, N, pre, K, a, nullptr, nullptr, nullptr, int(M),
-                                  int(K), int(N)),
+    // the split-K kernel reads w8 [N, K] as it is stored (transposing LDS
+    // reads); other shapes take the transposed copy and the NT kernels
+    bool nn = false;
+    XPU_TRY(launched(gemm_dequant_nn(st, q, N, w8, K, pre, K, a, int(M), int(K), int(N), &nn),
                      "linear_dx_int8 (gemm)"));
+    if (!nn) {
+        XPU_TRY(launched(transpose_i8(st, w8, wt, N, K), "linear_dx_int8 (transpose)"));
+        XPU_TRY(launched(gemm_dequant(st, q, N, wt, N, pre, K, a, nullptr, nullptr, nullptr,
+                                      int(M), int(K), int(N)),
+                         "linear_dx_int8 (gemm)"));
+    }
     return launched(rotate_bf16(st, pre, dx, M, int(K)), "linear_dx_int8 (rotate)");
 }
 

@@ -255,6 +255,15 @@ __device__ __forceinline__ v4i lds_read16(uint32_t addr) {
     asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(addr));
     return r;
 }
+// A transposing read of 8-bit elements (gfx950): in each group of 16 lanes,
+// output lane 8a + b receives byte b of the 8 bytes addressed by lanes a,
+// a+2, .., a+14, in that order.
+typedef int v2i __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ v2i lds_read8_tr(uint32_t addr) {
+    v2i r;
+    asm volatile("ds_read_b64_tr_b8 %0, %1" : "=v"(r) : "v"(addr));
+    return r;
+}
 // the same with a constant byte offset in the instruction's offset field (one
 // address register serves a row of fragments)
 template <int OFF>
@@ -1051,7 +1060,7 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_pp_kernel(
 // its stage is refilled only after the phase that consumed it.  Team 1 then
 // hands its accumulators to team 0 through LDS in two halves (exact int32
 // sums), and team 0 runs the epilogue.
-template <int S, bool KTAIL, class Epi>
+template <int S, bool KTAIL, bool WNN, class Epi>
 __global__ __launch_bounds__(512, 1) void gemm_i8_splitk_kernel(
     const int8_t* __restrict__ X, int64_t ldx, const int8_t* __restrict__ W, int64_t ldw, int M,
     int N, int K, int tiles_m, int tiles_n, Epi epi) {
@@ -1100,15 +1109,31 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_splitk_kernel(
     const int lr = lane >> 2;
     const int lc = swz(lr, lane & 3) * 16;
     const int8_t* const xbase = X + int64_t(m0) * ldx;
-    const int8_t* const wbase = W + int64_t(n0) * ldw;
+    // The weight is W[n, k] (NT: row n, K-contiguous) or, with WNN, W[k, n]
+    // (row k of the contraction, n contiguous: the NN product's right operand
+    // as stored).  An NN stage holds the step's 64 contraction rows x 160
+    // columns as 10 blocks of 32 rows x 32 bytes, block 5*rb + cg for rows
+    // 32rb.. and columns 32cg..; row r of a block is 32 bytes at 32r, its two
+    // 16-byte halves swapped when r & 16 (so that the transposing fragment
+    // reads of rows r and r + 16 fall on different banks).  DMA lane l fills
+    // row l/2, stored half l%2.
+    const int8_t* const wbase = WNN ? W + n0 : W + int64_t(n0) * ldw;
     const int8_t* base[PER];
     int off[PER];
+    int krow[PER];                     // WNN: the lane's contraction row within a step
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
         const int j = min(wt + 4 * i, NB - 1);
+        krow[i] = 0;
         if (j < XB) {
             base[i] = xbase;
             off[i] = (min(m0 + 16 * j + lr, M - 1) - m0) * int(ldx) + lc;
+        } else if constexpr (WNN) {
+            const int jj = j - XB, rb = jj / 5, cg = jj - 5 * rb;
+            const int kr = lane >> 1, half = (lane & 1) ^ ((kr >> 4) & 1);
+            krow[i] = 32 * rb + kr;
+            base[i] = wbase;
+            off[i] = krow[i] * int(ldw) + min(32 * cg + 16 * half, N - n0 - 16);
         } else {
             base[i] = wbase;
             off[i] = (min(n0 + 16 * (j - XB) + lr, N - 1) - n0) * int(ldw) + lc;
@@ -1122,9 +1147,16 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_splitk_kernel(
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
             if (i == PER - 1 && !full_share) break;
-            const int8_t* p = base[i] + uint64_t(uint32_t(off[i] + k0));
-            if (KTAIL && k0 + lc >= K) p = g_zero16;
-            dma16(p, st + (wt + 4 * i) * 1024);
+            const int j = wt + 4 * i;
+            const int8_t* p;
+            if (WNN && j >= XB) {
+                p = base[i] + uint64_t(uint32_t(off[i]) + uint32_t(k0) * uint32_t(ldw));
+                if (KTAIL && k0 + krow[i] >= K) p = g_zero16;
+            } else {
+                p = base[i] + uint64_t(uint32_t(off[i] + k0));
+                if (KTAIL && k0 + lc >= K) p = g_zero16;
+            }
+            dma16(p, st + j * 1024);
         }
     };
     auto wait_batches = [&](int later) {
@@ -1142,6 +1174,28 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_splitk_kernel(
     const int xoff = (wm * TM) * 1024 + frag;
     const int woff = (XB + wn * TN) * 1024 + frag;
     const uint32_t rbase = lds_addr(ring);
+    // WNN fragments: a lane of group g = l/16 needs the 16 contraction bytes
+    // 16g.. of its column (l%16 of the 16-column block), which two transposing
+    // reads (ds_read_b64_tr_b8) deliver: in each 16-lane group, output lane
+    // 8a + b receives byte b of the 8 bytes addressed by lanes a, a+2, ..,
+    // a+14, in that order; so source lane j points at row 16(g&1) + 8h + j/2
+    // of its row block, bytes 8(j&1).. of the block's column pair half.  The
+    // swap of halves at r & 16 is (g & 1) here.
+    uint32_t wnn_off[TN][2];
+    if constexpr (WNN) {
+        const int g = lane >> 4, j = lane & 15;
+#pragma unroll
+        for (int a = 0; a < TN; ++a) {
+            const int blk = wn * TN + a, cg = blk >> 1;
+            const int half = (blk & 1) ^ (g & 1);
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int kr = 16 * (g & 1) + 8 * h + (j >> 1);
+                wnn_off[a][h] = uint32_t((XB + 5 * (g >> 1) + cg) * 1024 + kr * 32 + half * 16 +
+                                         8 * (j & 1));
+            }
+        }
+    }
 
     v4i acc[TN][TM];
 #pragma unroll
@@ -1151,8 +1205,17 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_splitk_kernel(
     v4i wf[TN], xf[TM];
     auto read_frags = [&](int s) {
         const uint32_t sb = rbase + (s % S) * STAGE_BYTES;
+        if constexpr (WNN) {
 #pragma unroll
-        for (int i = 0; i < TN; ++i) wf[i] = lds_read16(sb + woff + i * 1024);
+            for (int i = 0; i < TN; ++i) {
+                const v2i lo = lds_read8_tr(sb + wnn_off[i][0]);
+                const v2i hi = lds_read8_tr(sb + wnn_off[i][1]);
+                wf[i] = v4i{lo.x, lo.y, hi.x, hi.y};
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < TN; ++i) wf[i] = lds_read16(sb + woff + i * 1024);
+        }
 #pragma unroll
         for (int i = 0; i < TM; ++i) xf[i] = lds_read16(sb + xoff + i * 1024);
     };
@@ -1226,18 +1289,26 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_splitk_kernel(
                                          n0 + wn * WN, M, N, lane);
 }
 
-template <class Epi>
+template <bool WNN = false, class Epi>
 hipError_t launch_splitk(hipStream_t st, const int8_t* X, int64_t ldx, const int8_t* W,
                          int64_t ldw, int M, int N, int K, const Epi& epi) {
     constexpr int S = 4;                        // 2 x 4 x 18 KB of LDS
     const int tm = (M + 127) / 128, tn = (N + 159) / 160;
     if (K % 64 == 0)
-        hipLaunchKernelGGL((gemm_i8_splitk_kernel<S, false, Epi>), dim3(unsigned(tm * tn)),
+        hipLaunchKernelGGL((gemm_i8_splitk_kernel<S, false, WNN, Epi>), dim3(unsigned(tm * tn)),
                            dim3(512), 0, st, X, ldx, W, ldw, M, N, K, tm, tn, epi);
     else
-        hipLaunchKernelGGL((gemm_i8_splitk_kernel<S, true, Epi>), dim3(unsigned(tm * tn)),
+        hipLaunchKernelGGL((gemm_i8_splitk_kernel<S, true, WNN, Epi>), dim3(unsigned(tm * tn)),
                            dim3(512), 0, st, X, ldx, W, ldw, M, N, K, tm, tn, epi);
     return hipGetLastError();
+}
+
+// Whether launch_gemm takes the split-K kernel for a staged epilogue.
+bool splitk_applies(int M, int N, int K) {
+    if (M <= 64) return false;
+    const int64_t tm = (M + 255) / 256, tn = (N + 159) / 160;
+    const int64_t tiles_split = int64_t((M + 127) / 128) * ((N + 159) / 160);
+    return tm * tn < 192 && K >= 2048 && tiles_split >= 128;
 }
 
 // ------------------------------------------------------------ skinny M
@@ -1377,9 +1448,7 @@ hipError_t launch_gemm(hipStream_t st, const int8_t* X, int64_t ldx, const int8_
         const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
         if constexpr (Epi::kStaged) {
             // narrow output, long K: split K inside 128 x 160 tiles instead
-            const int64_t tiles_split = int64_t((M + 127) / 128) * ((N + 159) / 160);
-            if (int64_t(tm) * tn < 192 && K >= 2048 && tiles_split >= 128)
-                return launch_splitk(st, X, ldx, W, ldw, M, N, K, epi);
+            if (splitk_applies(M, N, K)) return launch_splitk(st, X, ldx, W, ldw, M, N, K, epi);
         }
         // one 256 x 320 ping-pong tile per CU when they fill every CU
         const int tn_pp = (N + 319) / 320;
@@ -1520,6 +1589,18 @@ hipError_t gemm_dequant(hipStream_t st, const int8_t* A, int64_t lda, const int8
                         const uint16_t* bias16, int M, int N, int K) {
     return launch_gemm(st, A, lda, B, ldb, M, N, K,
                        EpiDequant{static_cast<uint16_t*>(out), ldo, xs, ws, bias, bias16});
+}
+
+hipError_t gemm_dequant_nn(hipStream_t st, const int8_t* A, int64_t lda, const int8_t* Bkn,
+                           int64_t ldb, void* out, int64_t ldo, const float* xs, int M, int N,
+                           int K, bool* done) {
+    // B[k, n] as stored (the NN product); the 32-bit DMA offsets of the
+    // weight need K * ldb below 2^32
+    *done = splitk_applies(M, N, K) && N % 16 == 0 && int64_t(K + 64) * ldb < (int64_t(1) << 32);
+    if (!*done) return hipSuccess;
+    return launch_splitk<true>(st, A, lda, Bkn, ldb, M, N, K,
+                               EpiDequant{static_cast<uint16_t*>(out), ldo, xs, nullptr, nullptr,
+                                          nullptr});
 }
 
 hipError_t gemm_dequant_residual(hipStream_t st, const int8_t* A, int64_t lda, const int8_t* B,

@@ -28,6 +28,11 @@ hipError_t gemm_i32(hipStream_t st, const int8_t* A, int64_t lda, const int8_t* 
 hipError_t gemm_dequant(hipStream_t st, const int8_t* A, int64_t lda, const int8_t* B, int64_t ldb,
                         void* out, int64_t ldo, const float* xs, const float* ws, const float* bias,
                         const uint16_t* bias16, int M, int N, int K);
+// the dequant GEMM with B stored [K, N] (the NN product, no column scale), when
+// the split-K kernel takes the shape; *done = false (nothing launched) otherwise
+hipError_t gemm_dequant_nn(hipStream_t st, const int8_t* A, int64_t lda, const int8_t* Bkn,
+                           int64_t ldb, void* out, int64_t ldo, const float* xs, int M, int N,
+                           int K, bool* done);
 // the same with the residual update out = bf16(res + d * rscale[n]) (bf16 res, rscale)
 hipError_t gemm_dequant_residual(hipStream_t st, const int8_t* A, int64_t lda, const int8_t* B,
                                  int64_t ldb, void* out, int64_t ldo, const float* xs,

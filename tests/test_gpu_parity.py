@@ -545,6 +545,19 @@ def test_linear_dx_int8_full_size_c5(dev):
     assert np.array_equal(bits(dx), want), mismatch(bits(dx), want)
 
 
+@pytest.mark.parametrize("m,n,k", [(2048, 2080, 1280), (4096, 4096, 768), (1024, 2048, 1280)])
+def test_linear_dx_int8_split_k_shapes(dev, m, n, k):
+    """Shapes where dx's GEMM reads the weight as stored (the split-K kernel's
+    transposing LDS reads): a contraction that is not a multiple of 64
+    (2080, zero-filled tail), output columns that leave a partial 160-wide
+    tile (768), and a short one (2048)."""
+    dy = activation(m, n, seed=n, scale=1e-3, n_out=0)
+    w8, ws = int8.prepare_weight(weight(n, k, seed=k).to(dev))
+    dx = int8.linear_dx_int8(dy.to(dev), w8, ws)
+    want = O.linear_dx_int8(bits(dy), npy(w8), npy(ws))
+    assert np.array_equal(bits(dx), want), mismatch(bits(dx), want)
+
+
 def test_linear_dx_int8_exact(dev):
     m, n, k = 512, 1280, 1280
     dy = activation(m, n, seed=8, scale=1e-3, n_out=0)
