@@ -92,6 +92,37 @@ def test_persistent_tiles_exact(dev, m, n, k):
         assert np.array_equal(bits(out), want), mismatch(bits(out), want)
 
 
+@pytest.mark.parametrize("m,n,k", [(4096, 10240, 1280), (1000, 9728, 1152), (2560, 4112, 1104),
+                                   (4352, 7808, 2560)])
+def test_dequant_gemm_tiles_exact(dev, m, n, k):
+    """The dequant GEMM entry (xpuint8_linear_gemm_stream) with no bias, an
+    fp32 bias and a bf16 bias on: config 3; 232 rows in the last row tile and
+    K = 1152; a 16-column last column tile and K = 1104 (zeros past K in the
+    last step); 40 K steps over 4352 x 7808.  Each bit-exact against the
+    oracle's dequant of the exact product."""
+    rng = np.random.default_rng(m + 3 * n + k)
+    a = rng.integers(-127, 128, (m, k), dtype=np.int8)
+    b = rng.integers(-127, 128, (n, k), dtype=np.int8)
+    want32 = O.int_mm(a, b)
+    xs = rng.uniform(1e-3, 5e-2, m).astype(np.float32)
+    ws = rng.uniform(1e-5, 1e-3, n).astype(np.float32)
+    bias = (rng.standard_normal(n) * 0.1).astype(np.float32)
+    bias16 = O.f32_to_bf16(bias)
+    lib = L._lib()
+    t = lambda v: torch.from_numpy(v).to(dev)
+    ta, tb, txs, tws = t(a), t(b), t(xs), t(ws)
+    cases = ((None, 0, None), (t(bias), 0, bias),
+             (t(bias16.view(np.int16)), 1, O.bf16_to_f32(bias16)))
+    for bvec, kind, bref in cases:
+        out = torch.full((m, n), -1, device=dev, dtype=torch.int16).view(torch.bfloat16)
+        rc = lib.xpuint8_linear_gemm_stream(L._stream(dev), L._ptr(ta), L._ptr(txs), L._ptr(tb),
+                                            L._ptr(tws), L._ptr(bvec) if bvec is not None else None,
+                                            kind, L._ptr(out), m, n, k)
+        assert rc == 0, lib.xpuint8_last_error()
+        want = O.dequant(want32, xs, ws, bref)
+        assert np.array_equal(bits(out), want), (kind, mismatch(bits(out), want))
+
+
 # ------------------------------------------------------- rotate / quantize
 QSHAPES = [(1, 256), (7, 1280), (64, 5120), (33, 8192), (5, 3072), (3, 10240), (2, 16384),
            (5, 4352), (3, 16896), (2, 32768), (2, 33792), (2, 66560), (3, 16640)]
