@@ -80,4 +80,38 @@ __device__ __forceinline__ float activate_pre(const uint16_t* tab, float a, floa
     }
 }
 
+// activate_pre<ACT> from table words already read (t[] in act_fetch order:
+// the tab_lookup arguments of activate_pre, bf16 bits), with its arithmetic.
+__device__ __forceinline__ float tab_float(uint32_t w) { return __uint_as_float(w << 16); }
+template <int ACT>
+__device__ __forceinline__ float act_combine(float a, float b, const uint32_t* t) {
+    if constexpr (ACT == 0) {
+        return a;
+    } else if constexpr (ACT == 1 || ACT == 5) {
+        return tab_float(t[0]);
+    } else if constexpr (ACT == 2) {
+        return tab_float(t[0]) * b;
+    } else if constexpr (ACT == 3) {
+        return bf16_round(tab_float(t[0]) * tab_float(t[1])) * tab_float(t[2]);
+    } else {
+        return a * tab_float(t[0]);
+    }
+}
+
+// A window of one activation table in LDS: the entries of the bf16 inputs
+// whose exponent field is in [115, 131) (|x| in [2^-12, 2^4)), where the
+// FFN's activations lie: 2048 positive inputs, then the 2048 negative ones.
+// Input bits b sit at position 2048 * (b >> 15) + (b & 0x7FFF) - (115 << 7);
+// inputs outside read the table in global memory.  Used for the GELU (erf)
+// of the FFN's up-projection epilogue (ids 4 and 5, one lookup per value).
+constexpr int kWinLo = 115 << 7, kWinHalf = 16 * 128, kWinSize = 2 * kWinHalf;
+template <int ACT>
+__host__ __device__ constexpr int act_window_table() {
+    return (ACT == 4 || ACT == 5) ? kTabGeluErf : -1;
+}
+// bf16 input bits of window position w
+__device__ __forceinline__ uint32_t win_bits(int w) {
+    return (uint32_t(w >> 11) << 15) | uint32_t(kWinLo + (w & (kWinHalf - 1)));
+}
+
 }  // namespace xpuint8

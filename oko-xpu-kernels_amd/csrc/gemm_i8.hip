@@ -181,6 +181,8 @@ struct EpiAct {
     const float* ws;          // per weight row: [2 * half] paired, [N] otherwise
     int half;                 // row offset of the second half (paired)
     const uint16_t* tab;      // device activation tables
+    uint32_t win = 0;         // LDS address of the table window (0: none)
+    static constexpr int kWinTab = act_window_table<ACT>();
     struct Col { float4 w; };
     __device__ __forceinline__ float row(int m) const { return xs[m]; }
     __device__ __forceinline__ Col col(int n) const {
@@ -214,6 +216,48 @@ struct EpiAct {
         const float r3 = activate_pre<ACT>(tab, deq(a[3], ca.w.w, x), deq(b[3], cb.w.w, x));
         return make_uint2(cvt_pk_bf16(r0, r1), cvt_pk_bf16(r2, r3));
     }
+    // convert / convert2 with the table read from the LDS window (win != 0):
+    // four 16-bit LDS reads at clamped positions, one wait, and the global
+    // table only for inputs outside the window, behind a wave-uniform branch
+    // that is rarely taken.  Same table words, so the same results.
+    __device__ __forceinline__ uint2 win_finish(const float (&a)[4], const float (&b)[4]) const {
+        uint32_t k[4], t[4];
+        bool miss = false;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float x = ACT == 4 ? b[i] : a[i];
+            k[i] = __float_as_uint(x) >> 16;
+            const uint32_t rel = (k[i] & 0x7FFFu) - uint32_t(kWinLo);
+            miss = miss || rel >= uint32_t(kWinHalf);
+            const uint32_t addr = win + ((k[i] >> 15) << 12) + 2 * min(rel, uint32_t(kWinHalf - 1));
+            asm volatile("ds_read_u16 %0, %1" : "=v"(t[i]) : "v"(addr));
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(t[0]), "+v"(t[1]), "+v"(t[2]), "+v"(t[3]));
+        if (__builtin_amdgcn_ballot_w64(miss)) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if ((k[i] & 0x7FFFu) - uint32_t(kWinLo) >= uint32_t(kWinHalf))
+                    t[i] = tab[kWinTab * kTabSize + k[i]];
+        }
+        float r[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) r[i] = act_combine<ACT>(a[i], b[i], &t[i]);
+        return make_uint2(cvt_pk_bf16(r[0], r[1]), cvt_pk_bf16(r[2], r[3]));
+    }
+    __device__ __forceinline__ uint2 convert_w(const v4i& v, float x, const Col& c) const {
+        const float a[4] = {deq(v[0], c.w.x, x), deq(v[1], c.w.y, x), deq(v[2], c.w.z, x),
+                            deq(v[3], c.w.w, x)};
+        const float b[4] = {0.f, 0.f, 0.f, 0.f};
+        return win_finish(a, b);
+    }
+    __device__ __forceinline__ uint2 convert2_w(const v4i& av, const v4i& bv, float x, const Col& ca,
+                                                const Col& cb) const {
+        const float a[4] = {deq(av[0], ca.w.x, x), deq(av[1], ca.w.y, x), deq(av[2], ca.w.z, x),
+                            deq(av[3], ca.w.w, x)};
+        const float b[4] = {deq(bv[0], cb.w.x, x), deq(bv[1], cb.w.y, x), deq(bv[2], cb.w.z, x),
+                            deq(bv[3], cb.w.w, x)};
+        return win_finish(a, b);
+    }
     __device__ __forceinline__ void store16(int m, int n, const uint4& v) const {
         *reinterpret_cast<uint4*>(out + int64_t(m) * ldo + n) = v;
     }
@@ -222,6 +266,32 @@ struct EpiAct {
         *reinterpret_cast<uint2*>(out + int64_t(m) * ldo + n) = convert(v, row(m), col(n));
     }
 };
+
+// Whether an epilogue reads an activation table through an LDS window
+// (EpiAct of a single-lookup activation).
+template <class Epi, class = void>
+struct HasWindow : std::false_type {};
+template <class Epi>
+struct HasWindow<Epi, std::void_t<decltype(Epi::kWinTab)>>
+    : std::integral_constant<bool, (Epi::kWinTab >= 0)> {};
+template <class Epi>
+__host__ __device__ constexpr bool has_window() { return HasWindow<Epi>::value; }
+
+// An epilogue's conversion of one block (or pair of blocks), through the LDS
+// window or not.
+template <bool WIN, class Epi>
+__device__ __forceinline__ uint2 convert_one(const Epi& e, const v4i& v, float x,
+                                             const typename Epi::Col& c) {
+    if constexpr (WIN) return e.convert_w(v, x, c);
+    else return e.convert(v, x, c);
+}
+template <bool WIN, class Epi>
+__device__ __forceinline__ uint2 convert_pair(const Epi& e, const v4i& a, const v4i& b, float x,
+                                              const typename Epi::Col& ca,
+                                              const typename Epi::Col& cb) {
+    if constexpr (WIN) return e.convert2_w(a, b, x, ca, cb);
+    else return e.convert2(a, b, x, ca, cb);
+}
 
 // Row offset of a paired epilogue's second half (0 for the others).
 template <class Epi>
@@ -477,17 +547,26 @@ __device__ __forceinline__ void staged_store(const Epi& epi, v4i (&acc)[TN][TM],
             const int b = RB * pass + bb;
             const int r = 16 * bb + (lane & 15);
             const float x = rowv(b);
+            auto row_of_blocks = [&](auto Wc) {
+                constexpr bool WIN = decltype(Wc)::value;
 #pragma unroll
-            for (int a = 0; a < OUT_TN; ++a) {
-                const int c = 16 * a + 4 * (lane >> 4);
-                uint2 v;
-                if constexpr (PAIRED)
-                    v = epi.convert2(acc[2 * a][b], acc[2 * a + 1][b], x, ccol[2 * a],
-                                     ccol[2 * a + 1]);
-                else
-                    v = epi.convert(acc[a][b], x, ccol[a]);
-                *reinterpret_cast<uint2*>(stg + r * 256 + (((c >> 3) ^ (r & 15)) << 4) +
-                                          (c & 7) * 2) = v;
+                for (int a = 0; a < OUT_TN; ++a) {
+                    const int c = 16 * a + 4 * (lane >> 4);
+                    uint2 v;
+                    if constexpr (PAIRED)
+                        v = convert_pair<WIN>(epi, acc[2 * a][b], acc[2 * a + 1][b], x, ccol[2 * a],
+                                              ccol[2 * a + 1]);
+                    else
+                        v = convert_one<WIN>(epi, acc[a][b], x, ccol[a]);
+                    *reinterpret_cast<uint2*>(stg + r * 256 + (((c >> 3) ^ (r & 15)) << 4) +
+                                              (c & 7) * 2) = v;
+                }
+            };
+            if constexpr (has_window<Epi>()) {
+                if (epi.win) row_of_blocks(std::true_type{});
+                else row_of_blocks(std::false_type{});
+            } else {
+                row_of_blocks(std::false_type{});
             }
         }
         __builtin_amdgcn_s_waitcnt(0xC07F);                       // lgkmcnt(0)
@@ -758,7 +837,11 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_pp_kernel(
     constexpr int NSCALE = STAGED ? BM + NCV * BN_OUT : 0;
     constexpr int SCALE_BYTES = NSCALE * 4;
     constexpr int SPT = (NSCALE + 511) / 512;                   // operand values per thread
-    __shared__ __attribute__((aligned(1024))) int8_t smem[RING + 2 * SCALE_BYTES + 16];
+    // the activation table's LDS window, for an epilogue that has one
+    constexpr int WIN_BYTES = has_window<Epi>() ? 2 * kWinSize : 0;
+    __shared__ __attribute__((aligned(1024))) int8_t smem[RING + 2 * SCALE_BYTES + WIN_BYTES + 16];
+    static_assert(RING + 2 * SCALE_BYTES + WIN_BYTES + 16 <= 160 * 1024, "LDS");
+    Epi epi_w = epi;                    // the epilogue, with the window's address once filled
 
     const int tiles = tiles_m * tiles_n;
     const int lane = threadIdx.x & 63;
@@ -919,7 +1002,7 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_pp_kernel(
             }
             // staged through the slot of the tile's last step (the other
             // three hold the next tile's first steps)
-            staged_store<TM, TN, WN_OUT, Epi, 1>(epi, acc, [&](int b) { return xr[16 * b]; }, ccol,
+            staged_store<TM, TN, WN_OUT, Epi, 1>(epi_w, acc, [&](int b) { return xr[16 * b]; }, ccol,
                                                  smem + slot(KT - 1) + wave * (16 * 256),
                                                  m0 + wm * WM, n0 + wn * WN_OUT, M, N, lane);
         } else {
@@ -940,6 +1023,13 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_pp_kernel(
 
     int ti = blockIdx.x;
     if (ti >= tiles) return;
+    if constexpr (WIN_BYTES > 0) {
+        // the window, read once per block (visible after the first barrier)
+        uint16_t* w = reinterpret_cast<uint16_t*>(smem + RING + 2 * SCALE_BYTES);
+        const uint16_t* t = epi.tab + size_t(Epi::kWinTab) * kTabSize;
+        for (int i = threadIdx.x; i < kWinSize; i += 512) w[i] = t[win_bits(i)];
+        epi_w.win = lds_addr(w);
+    }
     int m0, n0;
     tile_origin(ti, m0, n0);
     setup(m0, n0);

@@ -466,13 +466,26 @@ def test_ffn_up_persistent_tiles_exact(dev, act):
     check_ffn_up(dev, act, 4100, 5200, 1040)
 
 
-def check_ffn_up(dev, act, m, inner, k):
+@pytest.mark.parametrize("act", [4, 5])
+def test_ffn_up_wide_range_exact(dev, act):
+    """The persistent kernel reads the GELU (erf) table through a window in LDS
+    that holds the inputs with |g| in [2^-12, 16), and the table in global
+    memory for the others: column scales spread over twelve decades put the
+    activation's inputs on both sides of the window, both signs, in every
+    wave."""
+    check_ffn_up(dev, act, 4100, 5200, 1040, wide=True)
+
+
+def check_ffn_up(dev, act, m, inner, k, wide=False):
     rng = np.random.default_rng(act * 100 + m)
     rows = 2 * inner if act in O.PAIRED else inner
     xq = rng.integers(-127, 128, (m, k), dtype=np.int8)
     w8 = rng.integers(-127, 128, (rows, k), dtype=np.int8)
     xs = rng.uniform(0.01, 0.05, m).astype(np.float32)
-    ws = rng.uniform(1e-5, 1e-4, rows).astype(np.float32)
+    if wide:
+        ws = (10.0 ** rng.uniform(-11, 1, rows)).astype(np.float32)
+    else:
+        ws = rng.uniform(1e-5, 1e-4, rows).astype(np.float32)
     out = torch.empty((m, inner), device=dev, dtype=torch.bfloat16)
     lib = L._lib()
     t = [torch.from_numpy(a).to(dev) for a in (xq, xs, w8, ws)]
