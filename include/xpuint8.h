@@ -131,6 +131,26 @@ int xpuint8_linear_gemm_stream(const void *stream, const int8_t *xq, const float
                                const int8_t *w8, const float *w_scale, const void *bias,
                                int32_t bias_bf16, void *out, int64_t M, int64_t N, int64_t K);
 
+/* The whole INT8 linear in one call: out = xpuint8_linear_gemm_stream of
+ * xpuint8_convrot_quantize_stream(x), bit for bit, with x bf16 [M,K], the
+ * quantized activation and its row scales kept in `work` (a device buffer of
+ * at least xpuint8_linear_workspace_size(M, N, K) bytes, 16-byte aligned; it
+ * needs no clearing).  Inside it q is laid out for the GEMM that reads it (the
+ * MFMA block layout when the split-K kernel takes the shape: narrow outputs
+ * with a long K, as the FFN's down-projection), which is why the
+ * intermediate is not exposed.  K % 256 == 0, N % 16 == 0; bias as in
+ * xpuint8_linear_gemm_stream.  Replaces quantize + torch._int_mm + dequant at
+ * python/xpu_kernels/int8/ops.py:622-638 and the down-projection of ffn
+ * (ops.py:716-719). */
+int xpuint8_linear_stream(const void *stream, const void *x, const int8_t *w8,
+                          const float *w_scale, const void *bias, int32_t bias_bf16, void *out,
+                          int64_t M, int64_t N, int64_t K, void *work, int64_t work_bytes);
+
+/* The workspace xpuint8_linear_stream needs, in bytes, or -1 when the shape is
+ * not supported.  No device needed.  A helper of the entry point above, with
+ * no counterpart in the reference. */
+int64_t xpuint8_linear_workspace_size(int64_t M, int64_t N, int64_t K);
+
 /* xpuint8_linear_gemm_stream followed by the residual update of
  * linear(residual=, residual_scale=), fused into the same store:
  *   d[m,n]   = the linear_gemm result (bf16),

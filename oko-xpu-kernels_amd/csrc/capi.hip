@@ -6,6 +6,7 @@
 // (the reference keeps one process-global string, src/xpuint8.cpp:36-50).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <atomic>
 #include <cstdio>
 #include <cstring>
@@ -140,9 +141,11 @@ int check_gemm(int64_t M, int64_t N, int64_t K) {
     } while (0)
 
 // The workspace of linear_dx_int8: the row-quantized column-scaled gradient
-// q [M,N] int8 and its row scales a [M] fp32, the transposed weight w8^T
-// [K,N] int8 (the GEMM's K-contiguous operand), and the product before the
-// inverse rotation, bf16 [M,K].  Each piece starts on a 256-byte boundary.
+// q [M,N] int8 (row-major, or in the MFMA block layout when the split-K
+// kernel reads it) and its row scales a [M] fp32, the transposed weight w8^T
+// [K,N] int8 (the GEMM's K-contiguous operand, for shapes the split-K kernel
+// does not take), and the product before the inverse rotation, bf16 [M,K].
+// Each piece starts on a 256-byte boundary.
 struct DxWork {
     size_t q, a, wt, pre, total;
 };
@@ -150,7 +153,7 @@ DxWork dx_work_layout(int64_t M, int64_t N, int64_t K) {
     auto up = [](int64_t b) { return (size_t(b) + 255) & ~size_t(255); };
     DxWork w;
     w.q = 0;
-    w.a = w.q + up(M * N);
+    w.a = w.q + up(std::max(M * N, tiled_bytes(M, N)));
     w.wt = w.a + up(4 * M);
     w.pre = w.wt + up(N * K);
     w.total = w.pre + up(2 * M * K);
@@ -172,9 +175,17 @@ int dx_chain(hipStream_t st, const void* dy, const float* w_scale, const int8_t*
     float* a = reinterpret_cast<float*>(work + L.a);
     int8_t* wt = reinterpret_cast<int8_t*>(work + L.wt);
     void* pre = work + L.pre;
-    XPU_TRY(launched(quantize_row(st, dy, w_scale, q, a, M, int(N)), "linear_dx_int8 (quantize_row)"));
     // the split-K kernel reads w8 [N, K] as it is stored (transposing LDS
-    // reads); other shapes take the transposed copy and the NT kernels
+    // reads) and q in the MFMA block layout, written so by the quantizer;
+    // other shapes take a row-major q, the transposed copy and the NT kernels
+    if (splitk_nn_applies(int(M), int(K), int(N), K) && rowquant_can_tile(int(N))) {
+        XPU_TRY(launched(quantize_row(st, dy, w_scale, q, a, M, int(N), true),
+                         "linear_dx_int8 (quantize_row)"));
+        XPU_TRY(launched(gemm_dequant_nn_xt(st, q, w8, K, pre, K, a, int(M), int(K), int(N)),
+                         "linear_dx_int8 (gemm)"));
+        return launched(rotate_bf16(st, pre, dx, M, int(K)), "linear_dx_int8 (rotate)");
+    }
+    XPU_TRY(launched(quantize_row(st, dy, w_scale, q, a, M, int(N)), "linear_dx_int8 (quantize_row)"));
     bool nn = false;
     XPU_TRY(launched(gemm_dequant_nn(st, q, N, w8, K, pre, K, a, int(M), int(K), int(N), &nn),
                      "linear_dx_int8 (gemm)"));
@@ -186,6 +197,14 @@ int dx_chain(hipStream_t st, const void* dy, const float* w_scale, const int8_t*
     }
     return launched(rotate_bf16(st, pre, dx, M, int(K)), "linear_dx_int8 (rotate)");
 }
+
+// The workspace of xpuint8_linear_stream: x quantized, q int8 (row-major, or
+// in the MFMA block layout when the split-K kernel reads it), then its row
+// scales fp32 [M], on a 256-byte boundary.
+size_t linear_work_q_bytes(int64_t M, int64_t K) {
+    return (size_t(std::max(M * K, tiled_bytes(M, K))) + 255) & ~size_t(255);
+}
+size_t linear_work_bytes(int64_t M, int64_t K) { return linear_work_q_bytes(M, K) + 4 * size_t(M); }
 
 int act_ok(int32_t act) {
     if (act < 1 || act > 5)
@@ -389,6 +408,42 @@ int xpuint8_linear_gemm_stream(const void* stream, const int8_t* xq, const float
     return launched(gemm_dequant(as_stream(stream), xq, K, w8, K, out, N, x_scale, w_scale, b32,
                                  b16, int(M), int(N), int(K)),
                     "linear_gemm");
+}
+
+int64_t xpuint8_linear_workspace_size(int64_t M, int64_t N, int64_t K) {
+    if (check_rows(M, K) != 0 || check_epilogue(M, N) != 0 || check_gemm(M, N, K) != 0) return -1;
+    return int64_t(linear_work_bytes(M, K));
+}
+
+int xpuint8_linear_stream(const void* stream, const void* x, const int8_t* w8,
+                          const float* w_scale, const void* bias, int32_t bias_bf16, void* out,
+                          int64_t M, int64_t N, int64_t K, void* work, int64_t work_bytes) {
+    XPU_TRY(check_rows(M, K));
+    XPU_TRY(check_epilogue(M, N));
+    XPU_TRY(check_gemm(M, N, K));
+    XPU_NONNULL(x); XPU_NONNULL(w8); XPU_NONNULL(w_scale); XPU_NONNULL(out); XPU_NONNULL(work);
+    XPU_ALIGNED_OPT(bias);
+    if (bias_bf16 != 0 && bias_bf16 != 1) return fail(2, "bias_bf16 must be 0 or 1");
+    if (work_bytes < int64_t(linear_work_bytes(M, K)))
+        return fail(2, "work must hold xpuint8_linear_workspace_size(M, N, K) bytes");
+    XPU_TRY(ensure_device());
+    hipStream_t st = as_stream(stream);
+    int8_t* q = static_cast<int8_t*>(work);
+    float* xs = reinterpret_cast<float*>(static_cast<char*>(work) + linear_work_q_bytes(M, K));
+    const float* b32 = bias_bf16 ? nullptr : static_cast<const float*>(bias);
+    const uint16_t* b16 = bias_bf16 ? static_cast<const uint16_t*>(bias) : nullptr;
+    // narrow outputs with a long K take the split-K kernel, which reads q in
+    // the MFMA block layout; the other shapes a row-major q
+    if (splitk_applies(int(M), int(N), int(K)) && rowquant_can_tile(int(K))) {
+        XPU_TRY(launched(convrot_quantize_tiled(st, x, q, xs, M, int(K)), "linear (quantize)"));
+        return launched(gemm_dequant_xt(st, q, w8, K, out, N, xs, w_scale, b32, b16, int(M),
+                                        int(N), int(K)),
+                        "linear (gemm)");
+    }
+    XPU_TRY(launched(convrot_quantize(st, x, q, xs, M, int(K), 0), "linear (quantize)"));
+    return launched(gemm_dequant(st, q, K, w8, K, out, N, xs, w_scale, b32, b16, int(M), int(N),
+                                 int(K)),
+                    "linear (gemm)");
 }
 
 int xpuint8_linear_gemm_residual_stream(const void* stream, const int8_t* xq,

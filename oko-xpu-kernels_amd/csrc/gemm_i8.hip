@@ -1150,7 +1150,7 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_pp_kernel(
 // its stage is refilled only after the phase that consumed it.  Team 1 then
 // hands its accumulators to team 0 through LDS in two halves (exact int32
 // sums), and team 0 runs the epilogue.
-template <int S, bool KTAIL, bool WNN, class Epi>
+template <int S, bool KTAIL, bool WNN, class Epi, bool XT = false>
 __global__ __launch_bounds__(512, 1) void gemm_i8_splitk_kernel(
     const int8_t* __restrict__ X, int64_t ldx, const int8_t* __restrict__ W, int64_t ldw, int M,
     int N, int K, int tiles_m, int tiles_n, Epi epi) {
@@ -1215,7 +1215,13 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_splitk_kernel(
     for (int i = 0; i < PER; ++i) {
         const int j = min(wt + 4 * i, NB - 1);
         krow[i] = 0;
-        if (j < XB) {
+        if (j < XB && XT) {
+            // X in the MFMA block layout: row block m0/16 + j (the last one
+            // for blocks past M), one contiguous 1 KB per step
+            const int mb = min(m0 / 16 + j, (M + 15) / 16 - 1);
+            base[i] = X + int64_t(mb) * ((K + BK - 1) / BK) * 1024;
+            off[i] = 16 * lane;
+        } else if (j < XB) {
             base[i] = xbase;
             off[i] = (min(m0 + 16 * j + lr, M - 1) - m0) * int(ldx) + lc;
         } else if constexpr (WNN) {
@@ -1242,6 +1248,9 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_splitk_kernel(
             if (WNN && j >= XB) {
                 p = base[i] + uint64_t(uint32_t(off[i]) + uint32_t(k0) * uint32_t(ldw));
                 if (KTAIL && k0 + krow[i] >= K) p = g_zero16;
+            } else if (XT && j < XB) {
+                // bytes past K in the last step are multiplied by W's zeros
+                p = base[i] + uint64_t(off[i]) + uint64_t(kt0 + s) * 1024;
             } else {
                 p = base[i] + uint64_t(uint32_t(off[i] + k0));
                 if (KTAIL && k0 + lc >= K) p = g_zero16;
@@ -1379,27 +1388,20 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_splitk_kernel(
                                          n0 + wn * WN, M, N, lane);
 }
 
-template <bool WNN = false, class Epi>
+template <bool WNN = false, class Epi, bool XT = false>
 hipError_t launch_splitk(hipStream_t st, const int8_t* X, int64_t ldx, const int8_t* W,
                          int64_t ldw, int M, int N, int K, const Epi& epi) {
     constexpr int S = 4;                        // 2 x 4 x 18 KB of LDS
     const int tm = (M + 127) / 128, tn = (N + 159) / 160;
     if (K % 64 == 0)
-        hipLaunchKernelGGL((gemm_i8_splitk_kernel<S, false, WNN, Epi>), dim3(unsigned(tm * tn)),
+        hipLaunchKernelGGL((gemm_i8_splitk_kernel<S, false, WNN, Epi, XT>), dim3(unsigned(tm * tn)),
                            dim3(512), 0, st, X, ldx, W, ldw, M, N, K, tm, tn, epi);
     else
-        hipLaunchKernelGGL((gemm_i8_splitk_kernel<S, true, WNN, Epi>), dim3(unsigned(tm * tn)),
+        hipLaunchKernelGGL((gemm_i8_splitk_kernel<S, true, WNN, Epi, XT>), dim3(unsigned(tm * tn)),
                            dim3(512), 0, st, X, ldx, W, ldw, M, N, K, tm, tn, epi);
     return hipGetLastError();
 }
 
-// Whether launch_gemm takes the split-K kernel for a staged epilogue.
-bool splitk_applies(int M, int N, int K) {
-    if (M <= 64) return false;
-    const int64_t tm = (M + 255) / 256, tn = (N + 159) / 160;
-    const int64_t tiles_split = int64_t((M + 127) / 128) * ((N + 159) / 160);
-    return tm * tn < 192 && K >= 2048 && tiles_split >= 128;
-}
 
 // ------------------------------------------------------------ skinny M
 // M <= 64: the product streams the weight once, so it is bound by HBM
@@ -1669,6 +1671,20 @@ __global__ __launch_bounds__(256) void transpose_i8_kernel(const int8_t* __restr
 
 }  // namespace
 
+// Whether launch_gemm takes the split-K kernel for a staged epilogue.
+bool splitk_applies(int M, int N, int K) {
+    if (M <= 64) return false;
+    const int64_t tm = (M + 255) / 256, tn = (N + 159) / 160;
+    const int64_t tiles_split = int64_t((M + 127) / 128) * ((N + 159) / 160);
+    return tm * tn < 192 && K >= 2048 && tiles_split >= 128;
+}
+
+// B[k, n] as stored (the NN product); the 32-bit DMA offsets of the weight
+// need K * ldb below 2^32
+bool splitk_nn_applies(int M, int N, int K, int64_t ldb) {
+    return splitk_applies(M, N, K) && N % 16 == 0 && int64_t(K + 64) * ldb < (int64_t(1) << 32);
+}
+
 hipError_t gemm_i32(hipStream_t st, const int8_t* A, int64_t lda, const int8_t* B, int64_t ldb,
                     int32_t* C, int64_t ldc, int M, int N, int K) {
     return launch_gemm(st, A, lda, B, ldb, M, N, K, EpiI32{C, ldc});
@@ -1684,13 +1700,26 @@ hipError_t gemm_dequant(hipStream_t st, const int8_t* A, int64_t lda, const int8
 hipError_t gemm_dequant_nn(hipStream_t st, const int8_t* A, int64_t lda, const int8_t* Bkn,
                            int64_t ldb, void* out, int64_t ldo, const float* xs, int M, int N,
                            int K, bool* done) {
-    // B[k, n] as stored (the NN product); the 32-bit DMA offsets of the
-    // weight need K * ldb below 2^32
-    *done = splitk_applies(M, N, K) && N % 16 == 0 && int64_t(K + 64) * ldb < (int64_t(1) << 32);
+    *done = splitk_nn_applies(M, N, K, ldb);
     if (!*done) return hipSuccess;
     return launch_splitk<true>(st, A, lda, Bkn, ldb, M, N, K,
                                EpiDequant{static_cast<uint16_t*>(out), ldo, xs, nullptr, nullptr,
                                           nullptr});
+}
+
+hipError_t gemm_dequant_xt(hipStream_t st, const int8_t* At, const int8_t* B, int64_t ldb,
+                           void* out, int64_t ldo, const float* xs, const float* ws,
+                           const float* bias, const uint16_t* bias16, int M, int N, int K) {
+    return launch_splitk<false, EpiDequant, true>(
+        st, At, 0, B, ldb, M, N, K,
+        EpiDequant{static_cast<uint16_t*>(out), ldo, xs, ws, bias, bias16});
+}
+
+hipError_t gemm_dequant_nn_xt(hipStream_t st, const int8_t* At, const int8_t* Bkn, int64_t ldb,
+                              void* out, int64_t ldo, const float* xs, int M, int N, int K) {
+    return launch_splitk<true, EpiDequant, true>(
+        st, At, 0, Bkn, ldb, M, N, K,
+        EpiDequant{static_cast<uint16_t*>(out), ldo, xs, nullptr, nullptr, nullptr});
 }
 
 hipError_t gemm_dequant_residual(hipStream_t st, const int8_t* A, int64_t lda, const int8_t* B,

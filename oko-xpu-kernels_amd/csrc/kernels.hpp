@@ -8,6 +8,21 @@
 
 namespace xpuint8 {
 
+// The MFMA block layout of an int8 GEMM operand [M, K]: the GEMM kernels' LDS
+// stage layout, laid out in memory, so that one 16-row block of a 64-byte K
+// step is one contiguous 1 KB direct-to-LDS load.  Block (m/16, k/64) sits at
+// ((m/16) * KB + k/64) * 1024 (KB = ceil(K/64)); in it, row r = m%16 at 64r and
+// its 16-byte chunk c = (k%64)/16 at position c ^ ((r >> 1) & 3).  Rows past
+// M in the last block and bytes past K in the last column of blocks are
+// unspecified (the GEMM multiplies them by zeros or never stores them).
+__host__ __device__ inline int64_t tiled_bytes(int64_t M, int64_t K) {
+    return ((M + 15) / 16) * ((K + 63) / 64) * 1024;
+}
+__host__ __device__ inline int64_t tiled_offset(int64_t m, int k, int KB) {
+    const int r = int(m & 15), c = (k >> 4) & 3;
+    return (((m >> 4) * KB + (k >> 6)) << 10) + (r << 6) + ((c ^ ((r >> 1) & 3)) << 4);
+}
+
 // rowquant.hip
 hipError_t convrot_quantize(hipStream_t st, const void* x, int8_t* q, float* scale, int64_t M,
                             int K, int act);
@@ -20,7 +35,12 @@ hipError_t dequant_weight(hipStream_t st, const int8_t* w8, const float* scale, 
 hipError_t prepare_weight(hipStream_t st, const void* w, int8_t* q, float* scale, int64_t N,
                           int K);
 hipError_t quantize_row(hipStream_t st, const void* x, const float* colscale, int8_t* q,
-                        float* scale, int64_t M, int N);
+                        float* scale, int64_t M, int N, bool tiled = false);
+// the quantizers above (rotating with act 0, and quantize_row) can write q in
+// the MFMA block layout (tiled = true) for rows of this length
+bool rowquant_can_tile(int K);
+hipError_t convrot_quantize_tiled(hipStream_t st, const void* x, int8_t* q, float* scale,
+                                  int64_t M, int K);
 
 // gemm_i8.hip
 hipError_t gemm_i32(hipStream_t st, const int8_t* A, int64_t lda, const int8_t* B, int64_t ldb,
@@ -33,6 +53,17 @@ hipError_t gemm_dequant(hipStream_t st, const int8_t* A, int64_t lda, const int8
 hipError_t gemm_dequant_nn(hipStream_t st, const int8_t* A, int64_t lda, const int8_t* Bkn,
                            int64_t ldb, void* out, int64_t ldo, const float* xs, int M, int N,
                            int K, bool* done);
+// whether the split-K kernel takes the dequant GEMM of this shape, and its NN
+// form (gemm_dequant_nn) with B stored [K, N] at row stride ldb
+bool splitk_applies(int M, int N, int K);
+bool splitk_nn_applies(int M, int N, int K, int64_t ldb);
+// the split-K dequant GEMMs with A in the MFMA block layout (tiled_offset);
+// callers check splitk_applies first
+hipError_t gemm_dequant_xt(hipStream_t st, const int8_t* At, const int8_t* B, int64_t ldb,
+                           void* out, int64_t ldo, const float* xs, const float* ws,
+                           const float* bias, const uint16_t* bias16, int M, int N, int K);
+hipError_t gemm_dequant_nn_xt(hipStream_t st, const int8_t* At, const int8_t* Bkn, int64_t ldb,
+                              void* out, int64_t ldo, const float* xs, int M, int N, int K);
 // the same with the residual update out = bf16(res + d * rscale[n]) (bf16 res, rscale)
 hipError_t gemm_dequant_residual(hipStream_t st, const int8_t* A, int64_t lda, const int8_t* B,
                                  int64_t ldb, void* out, int64_t ldo, const float* xs,

@@ -354,7 +354,7 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-template <int P, bool ROT, int MODE, bool FULL, class Loader>
+template <int P, bool ROT, int MODE, bool FULL, class Loader, bool TILED = false>
 __global__ __launch_bounds__(1024) void rowquant_seg_kernel(Loader load, int8_t* __restrict__ q,
                                                            float* __restrict__ scale, int64_t M,
                                                            int K, int S, int R, int s_mul) {
@@ -408,7 +408,12 @@ __global__ __launch_bounds__(1024) void rowquant_seg_kernel(Loader load, int8_t*
 #pragma unroll
     for (int p = 0; p < P; ++p) {
         const uint4 w = quant16<ROT, MODE>(v[p], sc, inv, dom);
-        if (FULL || col[p] < K) *reinterpret_cast<uint4*>(at32(qrow, r, K, col[p] + dcol)) = w;
+        if (FULL || col[p] < K) {
+            if constexpr (TILED)
+                *reinterpret_cast<uint4*>(q + tiled_offset(row0 + r, col[p] + dcol, (K + 63) / 64)) = w;
+            else
+                *reinterpret_cast<uint4*>(at32(qrow, r, K, col[p] + dcol)) = w;
+        }
     }
 }
 
@@ -484,34 +489,38 @@ inline bool seg_shape(int G, int& P, int& S, int& R, int& nseg) {
     return true;
 }
 
-template <int P, bool ROT, int MODE, bool FULL, class Loader>
+template <int P, bool ROT, int MODE, bool FULL, class Loader, bool TILED = false>
 void launch_seg(hipStream_t st, const Loader& ld, int8_t* q, float* scale, int64_t M, int K,
                 int S, int R, int nseg) {
     const dim3 grid(unsigned((M + R - 1) / R)), block(unsigned(nseg * 16));
     const int s_mul = (4096 + S - 1) / S;
-    hipLaunchKernelGGL((rowquant_seg_kernel<P, ROT, MODE, FULL, Loader>), grid, block, 0, st, ld,
-                       q, scale, M, K, S, R, s_mul);
+    hipLaunchKernelGGL((rowquant_seg_kernel<P, ROT, MODE, FULL, Loader, TILED>), grid, block, 0,
+                       st, ld, q, scale, M, K, S, R, s_mul);
 }
 
-template <bool ROT, int MODE, class Loader>
+// TILED: q in the MFMA block layout (tiled_offset); only for rows that the
+// segmented kernel takes (rowquant_can_tile)
+template <bool ROT, int MODE, class Loader, bool TILED = false>
 hipError_t launch_rowquant(hipStream_t st, const Loader& ld, int8_t* q, float* scale, int64_t M,
                            int K) {
     const int G = (K + kGroup - 1) / kGroup;
     int P, S, R, nseg;
     if (seg_shape(G, P, S, R, nseg)) {
         if constexpr (ROT) {     // rotating entry points guarantee K % 256 == 0
-            if (P == 2) launch_seg<2, ROT, MODE, true>(st, ld, q, scale, M, K, S, R, nseg);
-            else        launch_seg<1, ROT, MODE, true>(st, ld, q, scale, M, K, S, R, nseg);
+            if (P == 2) launch_seg<2, ROT, MODE, true, Loader, TILED>(st, ld, q, scale, M, K, S, R, nseg);
+            else        launch_seg<1, ROT, MODE, true, Loader, TILED>(st, ld, q, scale, M, K, S, R, nseg);
         } else {
             const bool full = K % kGroup == 0;
             if (P == 2) {
-                if (full) launch_seg<2, ROT, MODE, true>(st, ld, q, scale, M, K, S, R, nseg);
-                else      launch_seg<2, ROT, MODE, false>(st, ld, q, scale, M, K, S, R, nseg);
+                if (full) launch_seg<2, ROT, MODE, true, Loader, TILED>(st, ld, q, scale, M, K, S, R, nseg);
+                else      launch_seg<2, ROT, MODE, false, Loader, TILED>(st, ld, q, scale, M, K, S, R, nseg);
             } else {
-                if (full) launch_seg<1, ROT, MODE, true>(st, ld, q, scale, M, K, S, R, nseg);
-                else      launch_seg<1, ROT, MODE, false>(st, ld, q, scale, M, K, S, R, nseg);
+                if (full) launch_seg<1, ROT, MODE, true, Loader, TILED>(st, ld, q, scale, M, K, S, R, nseg);
+                else      launch_seg<1, ROT, MODE, false, Loader, TILED>(st, ld, q, scale, M, K, S, R, nseg);
             }
         }
+    } else if constexpr (TILED) {
+        return hipErrorInvalidValue;    // callers check rowquant_can_tile
     } else {
         const dim3 grid(unsigned((M + kRowsPerBlock - 1) / kRowsPerBlock)), block(256);
         hipLaunchKernelGGL((rowquant_2pass_kernel<ROT, MODE, Loader>), grid, block, 0, st, ld, q,
@@ -618,9 +627,21 @@ hipError_t prepare_weight(hipStream_t st, const void* w, int8_t* q, float* scale
 }
 
 hipError_t quantize_row(hipStream_t st, const void* x, const float* colscale, int8_t* q,
-                        float* scale, int64_t M, int N) {
-    return launch_rowquant<false, kDivide>(
-        st, LoadColScaled{static_cast<const uint16_t*>(x), N, colscale}, q, scale, M, N);
+                        float* scale, int64_t M, int N, bool tiled) {
+    const LoadColScaled ld{static_cast<const uint16_t*>(x), N, colscale};
+    if (tiled) return launch_rowquant<false, kDivide, LoadColScaled, true>(st, ld, q, scale, M, N);
+    return launch_rowquant<false, kDivide>(st, ld, q, scale, M, N);
+}
+
+bool rowquant_can_tile(int K) {
+    int P, S, R, nseg;
+    return seg_shape((K + kGroup - 1) / kGroup, P, S, R, nseg);
+}
+
+hipError_t convrot_quantize_tiled(hipStream_t st, const void* x, int8_t* q, float* scale,
+                                  int64_t M, int K) {
+    return launch_rowquant<true, kRecip, LoadBF16, true>(
+        st, LoadBF16{static_cast<const uint16_t*>(x), K}, q, scale, M, K);
 }
 
 }  // namespace xpuint8

@@ -525,20 +525,28 @@ def linear(x, w8, w_scale, bias=None, act: Optional[str] = None, residual=None,
     if not x2.is_contiguous():
         x2 = x2.contiguous()
 
+    lib = _lib()
+    w8c = _c(w8)
+    rs = None if return_acc else _fused_residual_scale(residual, residual_scale, input_dtype, n,
+                                                      x.device)
+    if act is None and not return_acc and rs is None:
+        # quantize and GEMM in one call, the quantized activation in a
+        # workspace laid out for the GEMM that reads it
+        ws = expand_scale(w_scale, n, x.device)
+        b, b16 = _bias_arg(bias, n, x.device)
+        out = _linear_bf16(lib, x2, w8c, ws, b, b16, m, n, k)
+        return _residual_tail(out, residual, residual_scale, input_dtype, x.shape, m, n)
     if act is None:
         xq, xs = quantize(x2)
     else:
         xq, xs = quantize_act(x2, act)
-    w8c = _c(w8)
     if return_acc:
         acc = int_mm(xq, w8c.t())
         return acc, xs.reshape(-1), expand_scale(w_scale, n, acc.device)
 
-    lib = _lib()
     ws = expand_scale(w_scale, n, x.device)
     b, b16 = _bias_arg(bias, n, x.device)
     out = torch.empty((m, n), device=x.device, dtype=torch.bfloat16)
-    rs = _fused_residual_scale(residual, residual_scale, input_dtype, n, x.device)
     if rs is not None:
         # the residual update in the GEMM's store: bf16 activation, residual
         # and per-column scale, the case whose addcmul result is bf16
@@ -553,16 +561,36 @@ def linear(x, w8, w_scale, bias=None, act: Optional[str] = None, residual=None,
                                         _ptr(ws), _opt(b), b16, _ptr(out), m, n, k)
     if rc != 0:
         _err(lib, "linear")
+    return _residual_tail(out, residual, residual_scale, input_dtype, x.shape, m, n)
+
+
+def _linear_bf16(lib, x2, w8c, ws, b, b16, m, n, k):
+    """quantize + GEMM + dequant of a bf16 [m, k] through one library call
+    (xpuint8_linear_stream) with its workspace."""
+    need = lib.xpuint8_linear_workspace_size(m, n, k)
+    if need < 0:
+        _err(lib, "linear")
+    work = torch.empty(int(need), device=x2.device, dtype=torch.uint8)
+    out = torch.empty((m, n), device=x2.device, dtype=torch.bfloat16)
+    rc = lib.xpuint8_linear_stream(_stream(x2.device), _ptr(x2), _ptr(w8c), _ptr(ws), _opt(b),
+                                   b16, _ptr(out), m, n, k, _ptr(work), int(need))
+    if rc != 0:
+        _err(lib, "linear")
+    return out
+
+
+def _residual_tail(out, residual, residual_scale, input_dtype, shape, m, n):
+    """ops.py:639-646 after the GEMM: a residual the store did not fuse (an
+    fp32 model, a per-row or full-size scale, an fp32 scale whose addcmul
+    promotes to fp32) through the reference's own torch chain, then the
+    reshape and the cast back to the input dtype."""
     if residual is not None:
-        # any other residual form (an fp32 model, a per-row or full-size
-        # scale, an fp32 scale whose addcmul promotes to fp32): the
-        # reference's own torch chain
         residual = residual.reshape(m, n).to(
             out.dtype if input_dtype == torch.bfloat16 else input_dtype)
         if input_dtype != torch.bfloat16:
             out = out.to(dtype=input_dtype)
         out = torch.addcmul(residual, out, residual_scale)
-    out = out.reshape(*x.shape[:-1], n)
+    out = out.reshape(*shape[:-1], n)
     return out if input_dtype == torch.bfloat16 else out.to(dtype=input_dtype)
 
 
@@ -652,15 +680,11 @@ def ffn(x, up_w8, up_scale, down_w8, down_scale, down_bias=None, act="situ"):
                                    _ptr(v), m, inner, k, ACTIVATIONS[act])
     if rc != 0:
         _err(lib, "ffn (up projection)")
-    q2, xs2 = quantize(v)
     dw8 = _c(down_w8)
     ds = expand_scale(down_scale, k, device)
     b, b16 = _bias_arg(down_bias, k, device)
-    out = torch.empty((m, k), device=device, dtype=torch.bfloat16)
-    rc = lib.xpuint8_linear_gemm_stream(_stream(device), _ptr(q2), _ptr(xs2), _ptr(dw8),
-                                        _ptr(ds), _opt(b), b16, _ptr(out), m, k, inner)
-    if rc != 0:
-        _err(lib, "ffn")
+    # rotate+quantize of the activation and the down-projection in one call
+    out = _linear_bf16(lib, v, dw8, ds, b, b16, m, k, inner)
     out = out.reshape(*x.shape[:-1], k)
     return out if input_dtype == torch.bfloat16 else out.to(dtype=input_dtype)
 

@@ -427,6 +427,35 @@ def test_linear_full_size_c3(dev):
     assert torch.equal(same.view(torch.int16), y.view(torch.int16))
 
 
+@pytest.mark.parametrize("m,n,k", [(2100, 1280, 5120), (4096, 1296, 2304), (300, 1040, 1280)])
+def test_linear_one_call_exact(dev, m, n, k):
+    """xpuint8_linear_stream (quantize and GEMM in one call, the quantized
+    activation in its workspace): bit-exact against the oracle's linear with
+    an fp32 and a bf16 bias and with none.  The first two shapes take the
+    split-K kernel, which reads the activation in the MFMA block layout
+    written by the quantizer (ragged last row block, a 16-column last column
+    tile, K = 2304); the third a row-major activation."""
+    x = activation(m, k, seed=m, n_out=8, mult=20.0)
+    w = weight(n, k, seed=n)
+    bias = weight(1, n, seed=k, std=0.01)[0]
+    w8, ws = int8.prepare_weight(w.to(dev))
+    lib = L._lib()
+    need = lib.xpuint8_linear_workspace_size(m, n, k)
+    assert need > 0
+    work = torch.empty(need, device=dev, dtype=torch.uint8)
+    xd = x.to(dev)
+    for bvec, kind, bref in ((None, 0, None), (bias.float(), 0, O.bf16_to_f32(bits(bias))),
+                             (bias, 1, O.bf16_to_f32(bits(bias)))):
+        out = torch.empty((m, n), device=dev, dtype=torch.bfloat16)
+        bd = bvec.to(dev) if bvec is not None else None
+        rc = lib.xpuint8_linear_stream(L._stream(dev), L._ptr(xd), L._ptr(w8), L._ptr(ws),
+                                       L._ptr(bd) if bd is not None else None, kind, L._ptr(out),
+                                       m, n, k, L._ptr(work), need)
+        assert rc == 0, lib.xpuint8_last_error()
+        want = O.linear(bits(x), npy(w8), npy(ws), bref)
+        assert np.array_equal(bits(out), want), (kind, mismatch(bits(out), want))
+
+
 def test_linear_shapes_and_dtypes(dev):
     x = activation(2 * 3 * 5, 512, seed=3).reshape(2, 3, 5, 512)
     w = weight(48, 512)

@@ -74,6 +74,11 @@ def _rc(lib, fn, *args):
     ("xpuint8_linear_dx_int8_stream", (Z, P, P, P, P, 4, 24, 512, P, 1 << 20), 2, "16"),
     ("xpuint8_linear_dx_int8_stream", (Z, P, P, P, P, 4, 32, 512, Z, 1 << 20), 6, "null"),
     ("xpuint8_linear_dx_int8_stream", (Z, P, P, P, P, 4, 32, 512, P, 1024), 2, "workspace_size"),
+    ("xpuint8_linear_stream", (Z, P, P, P, Z, 0, P, 4, 32, 300, P, 1 << 20), 3, "256"),
+    ("xpuint8_linear_stream", (Z, P, P, P, Z, 0, P, 4, 24, 512, P, 1 << 20), 2, "16"),
+    ("xpuint8_linear_stream", (Z, P, P, P, Z, 2, P, 4, 32, 512, P, 1 << 20), 2, "bias_bf16"),
+    ("xpuint8_linear_stream", (Z, P, P, P, Z, 0, P, 4, 32, 512, Z, 1 << 20), 6, "null"),
+    ("xpuint8_linear_stream", (Z, P, P, P, Z, 0, P, 4, 32, 512, P, 64), 2, "workspace_size"),
     ("xpuint8_prepare_weight_stream", (Z, P, P, P, 16, 300), 3, "256"),
     ("xpuint8_quantize_row_stream", (Z, P, Z, P, P, 4, 20), 2, "16"),
     ("xpuint8_activation_table", (7, P), 6, "0..5"),
@@ -107,14 +112,37 @@ def test_init_without_a_device_fails_cleanly(lib):
     assert rc == 1 and "device" in lib.xpuint8_last_error().decode().lower()
 
 
+def up256(b):
+    return (b + 255) // 256 * 256
+
+
+def tiled(m, k):
+    """Bytes of an int8 [m, k] operand in the MFMA block layout: 16-row x
+    64-byte blocks of 1 KB."""
+    return -(-m // 16) * -(-k // 64) * 1024
+
+
 def test_dx_workspace_size(lib):
-    """The linear_dx_int8 workspace: q [M,N] int8, a [M] fp32, w8^T [K,N] int8
-    and the bf16 [M,K] product, each rounded up to 256 bytes; -1 for a shape
-    the entry point rejects."""
-    up = lambda b: (b + 255) // 256 * 256
+    """The linear_dx_int8 workspace: q [M,N] int8 (row-major or in the block
+    layout, whichever is larger), a [M] fp32, w8^T [K,N] int8 and the bf16
+    [M,K] product, each rounded up to 256 bytes; -1 for a shape the entry
+    point rejects."""
     m, n, k = 4096, 5120, 1280
-    want = up(m * n) + up(4 * m) + up(n * k) + up(2 * m * k)
+    want = up256(m * n) + up256(4 * m) + up256(n * k) + up256(2 * m * k)
     assert lib.xpuint8_linear_dx_int8_workspace_size(m, n, k) == want
-    assert lib.xpuint8_linear_dx_int8_workspace_size(3, 16, 256) == 256 + 256 + 16 * 256 + up(2 * 3 * 256)
+    assert lib.xpuint8_linear_dx_int8_workspace_size(3, 16, 256) == (
+        up256(tiled(3, 16)) + 256 + 16 * 256 + up256(2 * 3 * 256))
     assert lib.xpuint8_linear_dx_int8_workspace_size(4, 24, 512) == -1
     assert lib.xpuint8_linear_dx_int8_workspace_size(4, 32, 300) == -1
+
+
+def test_linear_workspace_size(lib):
+    """The linear's workspace: the quantized activation (row-major or in the
+    block layout, whichever is larger) rounded up to 256 bytes, then its fp32
+    row scales; -1 for a shape the entry point rejects."""
+    for m, n, k in [(4096, 1280, 5120), (4096, 10240, 1280), (3, 16, 256), (2100, 1296, 2304)]:
+        want = up256(max(m * k, tiled(m, k))) + 4 * m
+        assert lib.xpuint8_linear_workspace_size(m, n, k) == want, (m, n, k)
+    assert lib.xpuint8_linear_workspace_size(4, 32, 300) == -1
+    assert lib.xpuint8_linear_workspace_size(4, 24, 512) == -1
+    assert lib.xpuint8_linear_workspace_size(0, 32, 512) == -1
