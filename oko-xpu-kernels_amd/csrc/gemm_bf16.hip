@@ -368,10 +368,289 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_nn_kernel(
     }
 }
 
+// ---------------------------------------------------------------- split K
+// The dense dx at narrow outputs with a long contraction (C5: M = 4096 rows,
+// K = 1280 outputs, R = 5120 contraction rows).  There the 128 x 128 tiles
+// above make 320 blocks for 256 CUs, and the CUs that run two of them set the
+// time.  Here one block of 8 waves owns a 128 (m) x 160 (k) tile -- 256 tiles
+// at C5 -- in two teams of 4 (2 x 2 waves of 64 m x 80 k): team t owns half of
+// the 32-row contraction steps through its own ring of S LDS stages, and the
+// teams alternate between MFMAs and data movement every half step, so that on
+// each SIMD one wave feeds the matrix core while the other reads fragments
+// and issues loads:
+//   A(s): team 0 runs its step s;  team 1 reads its step s's fragments and
+//         issues its loads for step s + S - 1
+//   B(s): team 1 runs its step s;  team 0 reads its step s + 1's fragments
+//         and issues its loads for step s + S - 1
+// with one s_barrier between phases.  A stage holds
+//   8 dy blocks of 16 rows (m) x 64 bytes (one step of 32 bf16): chunk c of
+//     row r at position c ^ ((r >> 1) & 3), lane l's B fragment (row l%16,
+//     elements 8(l/16)..+7) one 16-byte read;
+//   10 weight blocks of 32 rows (contraction) x 16 columns (32 bytes): row r
+//     in slot r ^ ((r >> 1) & 4), where the two transposing reads of an A
+//     fragment (rows 8g + 4h + q, g, q = 0..3) cover the 64 banks twice, the
+//     two-cycle minimum for their 512 bytes.
+// The fp32 sums of the two halves meet in LDS (each team adds the other's
+// partial for half of the rows: IEEE addition is commutative, so the sum does
+// not depend on which team forms it), and each team rounds and stores its
+// half.
+__device__ __forceinline__ int swz_y(int r, int c) { return c ^ ((r >> 1) & 3); }
+__device__ __forceinline__ int slot_w(int r) { return r ^ ((r >> 1) & 4); }
+
+template <int OFF>
+__device__ __forceinline__ v4s tr_read_at(uint32_t addr) {
+    static_assert(OFF >= 0 && OFF < 65536, "ds offset field");
+    v4s r;
+    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "n"(OFF));
+    return r;
+}
+template <int OFF>
+__device__ __forceinline__ v8s plain_read_at(uint32_t addr) {
+    static_assert(OFF >= 0 && OFF < 65536, "ds offset field");
+    v8s r;
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "n"(OFF));
+    return r;
+}
+
+template <int S>
+__global__ __launch_bounds__(512, 1) void gemm_bf16_nn_splitk_kernel(
+    const uint16_t* __restrict__ W, int64_t ldw, const uint16_t* __restrict__ Y, int64_t ldy,
+    uint16_t* __restrict__ out, int64_t ldo, int R, int K, int M, int tiles_m, int tiles_k) {
+    constexpr int BM = 128, BK = 160;                   // tile: m rows, k output columns
+    constexpr int TM = 4, TK = 5;                       // 16x16 blocks per wave (m, k)
+    constexpr int YB = BM / 16, WB = BK / 16, NB = YB + WB;   // 18 blocks of 1 KB
+    constexpr int PER = (NB + 3) / 4, REM = NB % 4;
+    constexpr int STAGE = NB * 1024, RING = S * STAGE;
+    static_assert(2 * RING >= 2 * 4 * TK * (TM / 2) * 1024, "the exchanged halves fit");
+    __shared__ __attribute__((aligned(1024))) int8_t smem[2 * RING];
+
+    // tile grid over the 8 XCDs (block b on XCD b % 8): each XCD a gx x
+    // (8 / gx) block of tiles, gx chosen so that it reads the fewest operand
+    // rows and columns
+    int tmi = blockIdx.x % tiles_m, tki = blockIdx.x / tiles_m;
+    {
+        int best = 0, cost = 0;
+        for (int gx = 1; gx <= 8; gx *= 2) {
+            const int gy = 8 / gx;
+            if (tiles_m % gx || tiles_k % gy) continue;
+            const int c = (tiles_m / gx) * BM + (tiles_k / gy) * BK;
+            if (!best || c < cost) best = gx, cost = c;
+        }
+        if (best) {
+            const int x = blockIdx.x % 8, j = blockIdx.x / 8;
+            const int lm = tiles_m / best, lk = tiles_k / (8 / best);
+            tmi = (x % best) * lm + j % lm;
+            tki = (x / best) * lk + j / lm;
+        }
+    }
+    const int m0 = tmi * BM, k0 = tki * BK;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int team = wave >> 2, wt = wave & 3;
+    const int wm = wt >> 1, wk = wt & 1;
+    int8_t* const ring = smem + team * RING;
+
+    const int RT = R / kStepRows, RH = (RT + 1) / 2;   // team 0 takes the first RH steps
+    const int st0 = team * RH, nst = min(RT, st0 + RH) - st0;
+
+    // DMA: wave wt brings blocks wt, wt + 4, ... of its team's stages.  Byte
+    // offsets from a wave-uniform base; a step adds 64 bytes (dy) or 32 rows
+    // (weight).  Rows past M repeat the last row, columns past K a valid
+    // chunk (neither is stored).
+    const int8_t* const ybase = reinterpret_cast<const int8_t*>(Y + int64_t(m0) * ldy);
+    const int8_t* const wbase = reinterpret_cast<const int8_t*>(W + k0);
+    int off[PER];
+    bool isw[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const int j = min(wt + 4 * i, NB - 1);
+        isw[i] = j >= YB;
+        if (j < YB) {
+            const int r = lane >> 2;
+            const int c = swz_y(r, lane & 3);
+            off[i] = (min(m0 + 16 * j + r, M - 1) - m0) * int(ldy) * 2 + 16 * c;
+        } else {
+            const int cg = j - YB, p = lane >> 1, half = lane & 1;
+            const int r = slot_w(p);                    // slot_w is an involution
+            off[i] = r * int(ldw) * 2 + (min(k0 + 16 * cg + 8 * half, K - 8) - k0) * 2;
+        }
+    }
+    const bool full_share = REM == 0 || wt < REM;
+    auto issue = [&](int s) {
+        const int step = st0 + s;
+        int8_t* const st = ring + (s % S) * STAGE;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            if (i == PER - 1 && !full_share) break;
+            const int j = wt + 4 * i;
+            const int8_t* p =
+                isw[i] ? wbase + uint64_t(uint32_t(off[i]) +
+                                          uint32_t(step * kStepRows) * uint32_t(ldw) * 2u)
+                       : ybase + uint64_t(uint32_t(off[i] + step * 64));
+            dma16(p, st + j * 1024);
+        }
+    };
+    auto wait_batches = [&](int later) {
+        const int per = full_share ? PER : PER - 1;
+        if (later >= 2) {
+            if (per == PER) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * PER));
+            else __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * (PER - 1)));
+        } else if (later == 1) {
+            if (per == PER) __builtin_amdgcn_s_waitcnt(vmcnt_imm(PER));
+            else __builtin_amdgcn_s_waitcnt(vmcnt_imm(PER - 1));
+        } else {
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        }
+    };
+
+    // fragment addresses within a stage
+    const int g = lane >> 4, j = lane & 15;
+    const uint32_t yoff = (wm * TM) * 1024 + j * 64 + swz_y(j, g) * 16;
+    uint32_t woff[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+        woff[h] = (YB + wk * TK) * 1024 + 32 * slot_w(8 * g + 4 * h + (j >> 2)) + 8 * (j & 3);
+    const uint32_t rbase = lds_addr(ring);
+
+    v4f acc[TK][TM];
+#pragma unroll
+    for (int a = 0; a < TK; ++a)
+#pragma unroll
+        for (int b = 0; b < TM; ++b) acc[a][b] = v4f{0.f, 0.f, 0.f, 0.f};
+    v4s wl[TK], wh[TK];
+    v8s yf[TM];
+    auto read_frags = [&](int s) {
+        const uint32_t sb = rbase + (s % S) * STAGE;
+        auto rd = [&](auto A) {
+            constexpr int a = decltype(A)::value;
+            wl[a] = tr_read_at<a * 1024>(sb + woff[0]);
+            wh[a] = tr_read_at<a * 1024>(sb + woff[1]);
+        };
+        rd(std::integral_constant<int, 0>{});
+        rd(std::integral_constant<int, 1>{});
+        rd(std::integral_constant<int, 2>{});
+        rd(std::integral_constant<int, 3>{});
+        rd(std::integral_constant<int, 4>{});
+        yf[0] = plain_read_at<0>(sb + yoff);
+        yf[1] = plain_read_at<1024>(sb + yoff);
+        yf[2] = plain_read_at<2048>(sb + yoff);
+        yf[3] = plain_read_at<3072>(sb + yoff);
+    };
+    auto compute = [&]() {
+        // every read has landed before any fragment is used (the operands tie
+        // the fragments to this wait)
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(wl[0]), "+v"(wl[1]), "+v"(wl[2]), "+v"(wl[3]), "+v"(wl[4]),
+                       "+v"(wh[0]), "+v"(wh[1]), "+v"(wh[2]), "+v"(wh[3]), "+v"(wh[4]),
+                       "+v"(yf[0]), "+v"(yf[1]), "+v"(yf[2]), "+v"(yf[3]));
+#pragma unroll
+        for (int a = 0; a < TK; ++a) {
+            const v8s wv = {wl[a][0], wl[a][1], wl[a][2], wl[a][3],
+                            wh[a][0], wh[a][1], wh[a][2], wh[a][3]};
+            const v8bf wa = __builtin_bit_cast(v8bf, wv);
+#pragma unroll
+            for (int b = 0; b < TM; ++b)
+                acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    wa, __builtin_bit_cast(v8bf, yf[b]), acc[a][b], 0, 0, 0);
+        }
+    };
+    auto barrier = [&]() {
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    for (int s = 0; s < S - 1; ++s)
+        if (s < nst) issue(s);
+    if (nst > 0) wait_batches(min(S - 2, nst - 1));
+    barrier();
+    if (team == 0) {
+        if (nst > 0) read_frags(0);
+        barrier();
+#pragma clang loop unroll(disable)
+        for (int s = 0; s < RH; ++s) {
+            if (s < nst) compute();                             // A(s)
+            if (s + 1 < nst) wait_batches(min(S - 3, nst - 2 - s));
+            barrier();
+            if (s + 1 < nst) read_frags(s + 1);                 // B(s)
+            if (s + S - 1 < nst) issue(s + S - 1);
+            barrier();
+        }
+    } else {
+        barrier();
+#pragma clang loop unroll(disable)
+        for (int s = 0; s < RH; ++s) {
+            if (s < nst) read_frags(s);                         // A(s)
+            if (s + S - 1 < nst) issue(s + S - 1);
+            barrier();
+            if (s < nst) compute();                             // B(s)
+            if (s + 1 < nst) wait_batches(min(S - 2, nst - 2 - s));
+            barrier();
+        }
+    }
+
+    // exchange: team t gives the other team its partial sums of the row
+    // blocks that team owns (team 0: m blocks 0, 1 of each wave; team 1: 2, 3);
+    // constant block indices in each branch keep the accumulators in registers
+    __syncthreads();
+    v4f* const xchg = reinterpret_cast<v4f*>(smem);
+    auto slot = [&](int tm, int a, int bb) { return (((tm * 4 + wt) * TK + a) * (TM / 2) + bb) * 64 + lane; };
+    auto finish = [&](auto Own) {
+        constexpr int own = decltype(Own)::value, give = TM / 2 - own;
+        const int other = 1 - team;
+#pragma unroll
+        for (int a = 0; a < TK; ++a)
+#pragma unroll
+            for (int bb = 0; bb < TM / 2; ++bb) xchg[slot(team, a, bb)] = acc[a][give + bb];
+        __syncthreads();
+#pragma unroll
+        for (int a = 0; a < TK; ++a)
+#pragma unroll
+            for (int bb = 0; bb < TM / 2; ++bb) acc[a][own + bb] += xchg[slot(other, a, bb)];
+        // lane l of block (a, b): output row m = m0 + 64 wm + 16b + l%16,
+        // columns k = k0 + 80 wk + 16a + 4(l/16) .. +3
+#pragma unroll
+        for (int bb = 0; bb < TM / 2; ++bb) {
+            const int m = m0 + wm * 64 + 16 * (own + bb) + (lane & 15);
+            if (m >= M) continue;
+#pragma unroll
+            for (int a = 0; a < TK; ++a) {
+                const int k = k0 + wk * 80 + 16 * a + 4 * (lane >> 4);
+                if (k < K) {
+                    const v4f v = acc[a][own + bb];
+                    *reinterpret_cast<uint2*>(out + int64_t(m) * ldo + k) =
+                        make_uint2(cvt_pk_bf16(v[0], v[1]), cvt_pk_bf16(v[2], v[3]));
+                }
+            }
+        }
+    };
+    if (team == 0) finish(std::integral_constant<int, 0>{});
+    else finish(std::integral_constant<int, TM / 2>{});
+}
+
 }  // namespace
+
+// Whether the dense dx takes the split-K kernel: a contraction of whole
+// 32-row steps long enough for two teams, and enough 128 x 160 tiles to fill
+// the chip where 128 x 128 tiles would leave a ragged second round.
+// (The weight's byte offsets, up to R rows of ldw, stay below 2^32.)
+static bool bf16_nn_splitk_applies(int M, int R, int K, int64_t ldw) {
+    if (M <= 64 || R % kStepRows || R < 2048 || K % 8) return false;
+    if (int64_t(R) * ldw * 2 >= (int64_t(1) << 32)) return false;
+    const int64_t tiles = int64_t((M + 127) / 128) * ((K + 159) / 160);
+    return tiles >= 128 && tiles <= 256;
+}
 
 hipError_t gemm_bf16_nn(hipStream_t st, const void* dy, int64_t ldy, const void* w, int64_t ldw,
                         void* out, int64_t ldo, int M, int N, int K) {
+    if (bf16_nn_splitk_applies(M, N, K, ldw)) {
+        const int tm = (M + 127) / 128, tk = (K + 159) / 160;
+        hipLaunchKernelGGL((gemm_bf16_nn_splitk_kernel<4>), dim3(unsigned(tm * tk)), dim3(512), 0,
+                           st, static_cast<const uint16_t*>(w), ldw,
+                           static_cast<const uint16_t*>(dy), ldy, static_cast<uint16_t*>(out), ldo,
+                           N, K, M, tm, tk);
+        return hipGetLastError();
+    }
     const int tiles_k = (K + 127) / 128, tiles_m = (M + 127) / 128;
     hipLaunchKernelGGL((gemm_bf16_nn_kernel<2>), dim3(unsigned(tiles_k * tiles_m)), dim3(256), 0,
                        st, static_cast<const uint16_t*>(w), ldw, static_cast<const uint16_t*>(dy),

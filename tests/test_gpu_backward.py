@@ -34,8 +34,11 @@ def _bf16_bound(got_bf16_bits, ref, mag):
     return _within(O.bf16_to_f32(got_bf16_bits), ref, mag, 2.0 ** -8, 2.0 ** -14)
 
 
+# (2100, 2048, 1200) and (4000, 2080, 1280) take the split-K kernel with
+# ragged rows and columns and, for the second, an odd number of 32-row
+# contraction steps (the teams' halves differ by one)
 @pytest.mark.parametrize("m,n,k", [(4096, 5120, 1280), (77, 48, 144), (1, 16, 16), (300, 1040, 272),
-                                   (129, 4096, 640)])
+                                   (129, 4096, 640), (2100, 2048, 1200), (4000, 2080, 1280)])
 def test_linear_dx_dense(dev, m, n, k):
     g = torch.Generator().manual_seed(m + n + k)
     dy = (torch.randn(m, n, generator=g) * 1e-3).to(torch.bfloat16)
