@@ -369,31 +369,36 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_nn_kernel(
 }
 
 // ---------------------------------------------------------------- split K
-// The dense dx at narrow outputs with a long contraction (C5: M = 4096 rows,
-// K = 1280 outputs, R = 5120 contraction rows).  There the 128 x 128 tiles
-// above make 320 blocks for 256 CUs, and the CUs that run two of them set the
-// time.  Here one block of 8 waves owns a 128 (m) x 160 (k) tile -- 256 tiles
-// at C5 -- in two teams of 4 (2 x 2 waves of 64 m x 80 k): team t owns half of
-// the 32-row contraction steps through its own ring of S LDS stages, and the
-// teams alternate between MFMAs and data movement every half step, so that on
-// each SIMD one wave feeds the matrix core while the other reads fragments
-// and issues loads:
+// Narrow outputs with a long contraction: the dense dx (C5: M = 4096 rows,
+// K = 1280 outputs, R = 5120 contraction rows) and dW (N = 5120 rows, K = 1280,
+// R = 4096).  There the 128 x 128 tiles above make 320 (400) blocks for 256
+// CUs, and the CUs that run two of them set the time.  Here one block of 8
+// waves owns a BB x 160 tile of out[b, k] (256 tiles at C5 for both), in two
+// teams of 4 (2 x 2 waves of BB/2 x 80): team t owns half of the 32-row
+// contraction steps through its own ring of S LDS stages, and the teams
+// alternate between MFMAs and data movement every half step, so that on each
+// SIMD one wave feeds the matrix core while the other reads fragments and
+// issues loads:
 //   A(s): team 0 runs its step s;  team 1 reads its step s's fragments and
 //         issues its loads for step s + S - 1
 //   B(s): team 1 runs its step s;  team 0 reads its step s + 1's fragments
 //         and issues its loads for step s + S - 1
-// with one s_barrier between phases.  A stage holds
-//   8 dy blocks of 16 rows (m) x 64 bytes (one step of 32 bf16): chunk c of
-//     row r at position c ^ ((r >> 1) & 3), lane l's B fragment (row l%16,
-//     elements 8(l/16)..+7) one 16-byte read;
-//   10 weight blocks of 32 rows (contraction) x 16 columns (32 bytes): row r
-//     in slot r ^ ((r >> 1) & 4), where the two transposing reads of an A
+// with one s_barrier between phases.  D = A * B with A from the operand
+// contracted along its rows, a[r, k] (dx: the weight; dW: x), and B from
+// b (dx: dy[m, r], contracted along its contiguous dimension, BB = 128; dW,
+// YT: dy[r, n], contracted along its rows, BB = 160).  A stage holds
+//   for A, 10 blocks of 32 rows (contraction) x 16 columns (32 bytes): row r
+//     in slot r ^ ((r >> 1) & 4), where the two transposing reads of a
 //     fragment (rows 8g + 4h + q, g, q = 0..3) cover the 64 banks twice, the
-//     two-cycle minimum for their 512 bytes.
+//     two-cycle minimum for their 512 bytes;
+//   for B, the same (YT), or 8 blocks of 16 rows (m) x 64 bytes (one step of
+//     32 bf16): chunk c of row r at position c ^ ((r >> 1) & 3), lane l's
+//     fragment (row l%16, elements 8(l/16)..+7) one 16-byte read.
 // The fp32 sums of the two halves meet in LDS (each team adds the other's
-// partial for half of the rows: IEEE addition is commutative, so the sum does
-// not depend on which team forms it), and each team rounds and stores its
-// half.
+// partial for its share of the B blocks: IEEE addition is commutative, so the
+// sum does not depend on which team forms it), and each team rounds and
+// stores its share.  Lane l of block (a, b) holds D[4(l/16)+i][l%16]: four
+// consecutive k of one output row, one 8-byte store.
 __device__ __forceinline__ int swz_y(int r, int c) { return c ^ ((r >> 1) & 3); }
 __device__ __forceinline__ int slot_w(int r) { return r ^ ((r >> 1) & 4); }
 
@@ -412,146 +417,180 @@ __device__ __forceinline__ v8s plain_read_at(uint32_t addr) {
     return r;
 }
 
-template <int S>
-__global__ __launch_bounds__(512, 1) void gemm_bf16_nn_splitk_kernel(
-    const uint16_t* __restrict__ W, int64_t ldw, const uint16_t* __restrict__ Y, int64_t ldy,
-    uint16_t* __restrict__ out, int64_t ldo, int R, int K, int M, int tiles_m, int tiles_k) {
-    constexpr int BM = 128, BK = 160;                   // tile: m rows, k output columns
-    constexpr int TM = 4, TK = 5;                       // 16x16 blocks per wave (m, k)
-    constexpr int YB = BM / 16, WB = BK / 16, NB = YB + WB;   // 18 blocks of 1 KB
+template <int S, bool YT>
+__global__ __launch_bounds__(512, 1) void gemm_bf16_splitk_kernel(
+    const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ Y, int64_t ldy,
+    uint16_t* __restrict__ out, int64_t ldo, int R, int K, int NBR, int tiles_b, int tiles_k) {
+    constexpr int BK = 160, TK = 5;                     // A side: k columns, blocks per wave
+    constexpr int TB = YT ? 5 : 4, BB = 32 * TB;        // B side: blocks per wave, tile rows
+    constexpr int AB = BK / 16, YB = BB / 16, NB = AB + YB;
+    // block order in a stage: the dx's dy blocks first (measured 3 us faster
+    // at C5 than after the weight's), dW's x blocks first
+    constexpr int A0 = YT ? 0 : YB, Y0 = YT ? AB : 0;
     constexpr int PER = (NB + 3) / 4, REM = NB % 4;
     constexpr int STAGE = NB * 1024, RING = S * STAGE;
-    static_assert(2 * RING >= 2 * 4 * TK * (TM / 2) * 1024, "the exchanged halves fit");
+    constexpr int OWN0 = (TB + 1) / 2;                  // team 0 owns B blocks 0..OWN0-1
+    static_assert(2 * RING >= 4 * TK * TB * 1024, "the exchanged partial sums fit");
+    static_assert(2 * RING <= 160 * 1024, "LDS");
     __shared__ __attribute__((aligned(1024))) int8_t smem[2 * RING];
 
     // tile grid over the 8 XCDs (block b on XCD b % 8): each XCD a gx x
     // (8 / gx) block of tiles, gx chosen so that it reads the fewest operand
     // rows and columns
-    int tmi = blockIdx.x % tiles_m, tki = blockIdx.x / tiles_m;
+    int tbi = blockIdx.x % tiles_b, tki = blockIdx.x / tiles_b;
     {
         int best = 0, cost = 0;
         for (int gx = 1; gx <= 8; gx *= 2) {
             const int gy = 8 / gx;
-            if (tiles_m % gx || tiles_k % gy) continue;
-            const int c = (tiles_m / gx) * BM + (tiles_k / gy) * BK;
+            if (tiles_b % gx || tiles_k % gy) continue;
+            const int c = (tiles_b / gx) * BB + (tiles_k / gy) * BK;
             if (!best || c < cost) best = gx, cost = c;
         }
         if (best) {
             const int x = blockIdx.x % 8, j = blockIdx.x / 8;
-            const int lm = tiles_m / best, lk = tiles_k / (8 / best);
-            tmi = (x % best) * lm + j % lm;
-            tki = (x / best) * lk + j / lm;
+            const int lb = tiles_b / best, lk = tiles_k / (8 / best);
+            tbi = (x % best) * lb + j % lb;
+            tki = (x / best) * lk + j / lb;
         }
     }
-    const int m0 = tmi * BM, k0 = tki * BK;
+    const int b0 = tbi * BB, k0 = tki * BK;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int team = wave >> 2, wt = wave & 3;
-    const int wm = wt >> 1, wk = wt & 1;
+    const int wb = wt >> 1, wk = wt & 1;
     int8_t* const ring = smem + team * RING;
 
     const int RT = R / kStepRows, RH = (RT + 1) / 2;   // team 0 takes the first RH steps
     const int st0 = team * RH, nst = min(RT, st0 + RH) - st0;
 
-    // DMA: wave wt brings blocks wt, wt + 4, ... of its team's stages.  Byte
-    // offsets from a wave-uniform base; a step adds 64 bytes (dy) or 32 rows
-    // (weight).  Rows past M repeat the last row, columns past K a valid
-    // chunk (neither is stored).
-    const int8_t* const ybase = reinterpret_cast<const int8_t*>(Y + int64_t(m0) * ldy);
-    const int8_t* const wbase = reinterpret_cast<const int8_t*>(W + k0);
+    // DMA: wave wt brings blocks wt, wt + 4, ... of its team's stages.  Byte offsets from a wave-uniform base; a step adds 32
+    // rows (row-contracted operands) or 64 bytes (dy of the dx).  Rows past
+    // the output edge repeat the last row, columns past it a valid chunk
+    // (neither is stored).
+    const int8_t* const abase = reinterpret_cast<const int8_t*>(A + k0);
+    const int8_t* const ybase =
+        reinterpret_cast<const int8_t*>(YT ? Y + b0 : Y + int64_t(b0) * ldy);
     int off[PER];
-    bool isw[PER];
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
         const int j = min(wt + 4 * i, NB - 1);
-        isw[i] = j >= YB;
-        if (j < YB) {
-            const int r = lane >> 2;
-            const int c = swz_y(r, lane & 3);
-            off[i] = (min(m0 + 16 * j + r, M - 1) - m0) * int(ldy) * 2 + 16 * c;
+        const int p = lane >> 1, half = lane & 1, r = slot_w(p);   // slot_w is an involution
+        const bool isa = j >= A0 && j < A0 + AB;
+        if (isa) {
+            off[i] = r * int(lda) * 2 + (min(k0 + 16 * (j - A0) + 8 * half, K - 8) - k0) * 2;
+        } else if constexpr (YT) {
+            off[i] = r * int(ldy) * 2 + (min(b0 + 16 * (j - Y0) + 8 * half, NBR - 8) - b0) * 2;
         } else {
-            const int cg = j - YB, p = lane >> 1, half = lane & 1;
-            const int r = slot_w(p);                    // slot_w is an involution
-            off[i] = r * int(ldw) * 2 + (min(k0 + 16 * cg + 8 * half, K - 8) - k0) * 2;
+            const int rr = lane >> 2, c = swz_y(rr, lane & 3);
+            off[i] = (min(b0 + 16 * (j - Y0) + rr, NBR - 1) - b0) * int(ldy) * 2 + 16 * c;
         }
     }
     const bool full_share = REM == 0 || wt < REM;
     auto issue = [&](int s) {
         const int step = st0 + s;
         int8_t* const st = ring + (s % S) * STAGE;
+        const uint32_t arow = uint32_t(step * kStepRows) * uint32_t(lda) * 2u;
+        const uint32_t yrow = YT ? uint32_t(step * kStepRows) * uint32_t(ldy) * 2u
+                                 : uint32_t(step * 64);
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
             if (i == PER - 1 && !full_share) break;
             const int j = wt + 4 * i;
-            const int8_t* p =
-                isw[i] ? wbase + uint64_t(uint32_t(off[i]) +
-                                          uint32_t(step * kStepRows) * uint32_t(ldw) * 2u)
-                       : ybase + uint64_t(uint32_t(off[i] + step * 64));
+            const int8_t* p = (j >= A0 && j < A0 + AB) ? abase + uint64_t(uint32_t(off[i]) + arow)
+                                                       : ybase + uint64_t(uint32_t(off[i]) + yrow);
             dma16(p, st + j * 1024);
         }
     };
     auto wait_batches = [&](int later) {
-        const int per = full_share ? PER : PER - 1;
-        if (later >= 2) {
-            if (per == PER) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * PER));
-            else __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * (PER - 1)));
-        } else if (later == 1) {
-            if (per == PER) __builtin_amdgcn_s_waitcnt(vmcnt_imm(PER));
-            else __builtin_amdgcn_s_waitcnt(vmcnt_imm(PER - 1));
+        if (full_share) {
+            if (later >= 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * PER));
+            else if (later == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(PER));
+            else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
         } else {
-            __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+            if (later >= 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * (PER - 1)));
+            else if (later == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(PER - 1));
+            else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
         }
     };
 
-    // fragment addresses within a stage
+    // fragment addresses within a stage: transposing reads for row-contracted
+    // blocks (lane j of group g: row 8g + 4h + j/4, 8 bytes at column 4(j%4)),
+    // plain 16-byte reads for dy of the dx
     const int g = lane >> 4, j = lane & 15;
-    const uint32_t yoff = (wm * TM) * 1024 + j * 64 + swz_y(j, g) * 16;
-    uint32_t woff[2];
+    uint32_t troff[2];
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
-        woff[h] = (YB + wk * TK) * 1024 + 32 * slot_w(8 * g + 4 * h + (j >> 2)) + 8 * (j & 3);
+    for (int h = 0; h < 2; ++h) troff[h] = 32 * slot_w(8 * g + 4 * h + (j >> 2)) + 8 * (j & 3);
+    const uint32_t aoff = (A0 + wk * TK) * 1024;
+    const uint32_t yoff = YT ? (Y0 + wb * TB) * 1024 : (Y0 + wb * TB) * 1024 + j * 64 + swz_y(j, g) * 16;
     const uint32_t rbase = lds_addr(ring);
 
-    v4f acc[TK][TM];
+    v4f acc[TK][TB];
 #pragma unroll
     for (int a = 0; a < TK; ++a)
 #pragma unroll
-        for (int b = 0; b < TM; ++b) acc[a][b] = v4f{0.f, 0.f, 0.f, 0.f};
-    v4s wl[TK], wh[TK];
-    v8s yf[TM];
+        for (int b = 0; b < TB; ++b) acc[a][b] = v4f{0.f, 0.f, 0.f, 0.f};
+    v4s al[TK], ah[TK];
+    v4s yl[YT ? TB : 1], yh[YT ? TB : 1];
+    v8s yf[YT ? 1 : TB];
     auto read_frags = [&](int s) {
         const uint32_t sb = rbase + (s % S) * STAGE;
-        auto rd = [&](auto A) {
-            constexpr int a = decltype(A)::value;
-            wl[a] = tr_read_at<a * 1024>(sb + woff[0]);
-            wh[a] = tr_read_at<a * 1024>(sb + woff[1]);
+        auto rda = [&](auto I) {
+            constexpr int a = decltype(I)::value;
+            if constexpr (a < TK) {
+                al[a] = tr_read_at<a * 1024>(sb + aoff + troff[0]);
+                ah[a] = tr_read_at<a * 1024>(sb + aoff + troff[1]);
+            }
         };
-        rd(std::integral_constant<int, 0>{});
-        rd(std::integral_constant<int, 1>{});
-        rd(std::integral_constant<int, 2>{});
-        rd(std::integral_constant<int, 3>{});
-        rd(std::integral_constant<int, 4>{});
-        yf[0] = plain_read_at<0>(sb + yoff);
-        yf[1] = plain_read_at<1024>(sb + yoff);
-        yf[2] = plain_read_at<2048>(sb + yoff);
-        yf[3] = plain_read_at<3072>(sb + yoff);
+        auto rdb = [&](auto I) {
+            constexpr int b = decltype(I)::value;
+            if constexpr (b < TB) {
+                if constexpr (YT) {
+                    yl[b] = tr_read_at<b * 1024>(sb + yoff + troff[0]);
+                    yh[b] = tr_read_at<b * 1024>(sb + yoff + troff[1]);
+                } else {
+                    yf[b] = plain_read_at<b * 1024>(sb + yoff);
+                }
+            }
+        };
+        rda(std::integral_constant<int, 0>{});
+        rda(std::integral_constant<int, 1>{});
+        rda(std::integral_constant<int, 2>{});
+        rda(std::integral_constant<int, 3>{});
+        rda(std::integral_constant<int, 4>{});
+        rdb(std::integral_constant<int, 0>{});
+        rdb(std::integral_constant<int, 1>{});
+        rdb(std::integral_constant<int, 2>{});
+        rdb(std::integral_constant<int, 3>{});
+        rdb(std::integral_constant<int, 4>{});
+    };
+    auto join = [](const v4s& lo, const v4s& hi) {
+        const v8s v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        return __builtin_bit_cast(v8bf, v);
     };
     auto compute = [&]() {
         // every read has landed before any fragment is used (the operands tie
         // the fragments to this wait)
         asm volatile("s_waitcnt lgkmcnt(0)"
-                     : "+v"(wl[0]), "+v"(wl[1]), "+v"(wl[2]), "+v"(wl[3]), "+v"(wl[4]),
-                       "+v"(wh[0]), "+v"(wh[1]), "+v"(wh[2]), "+v"(wh[3]), "+v"(wh[4]),
-                       "+v"(yf[0]), "+v"(yf[1]), "+v"(yf[2]), "+v"(yf[3]));
+                     : "+v"(al[0]), "+v"(al[1]), "+v"(al[2]), "+v"(al[3]), "+v"(al[4]),
+                       "+v"(ah[0]), "+v"(ah[1]), "+v"(ah[2]), "+v"(ah[3]), "+v"(ah[4]));
+        if constexpr (YT) {
+            asm volatile("" : "+v"(yl[0]), "+v"(yl[1]), "+v"(yl[2]), "+v"(yl[3]), "+v"(yl[4]),
+                              "+v"(yh[0]), "+v"(yh[1]), "+v"(yh[2]), "+v"(yh[3]), "+v"(yh[4]));
+        } else {
+            asm volatile("" : "+v"(yf[0]), "+v"(yf[1]), "+v"(yf[2]), "+v"(yf[3]));
+        }
+        v8bf bfr[TB];
+#pragma unroll
+        for (int b = 0; b < TB; ++b) {
+            if constexpr (YT) bfr[b] = join(yl[b], yh[b]);
+            else bfr[b] = __builtin_bit_cast(v8bf, yf[b]);
+        }
 #pragma unroll
         for (int a = 0; a < TK; ++a) {
-            const v8s wv = {wl[a][0], wl[a][1], wl[a][2], wl[a][3],
-                            wh[a][0], wh[a][1], wh[a][2], wh[a][3]};
-            const v8bf wa = __builtin_bit_cast(v8bf, wv);
+            const v8bf af = join(al[a], ah[a]);
 #pragma unroll
-            for (int b = 0; b < TM; ++b)
-                acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                    wa, __builtin_bit_cast(v8bf, yf[b]), acc[a][b], 0, 0, 0);
+            for (int b = 0; b < TB; ++b)
+                acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bfr[b], acc[a][b], 0, 0, 0);
         }
     };
     auto barrier = [&]() {
@@ -589,64 +628,76 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_nn_splitk_kernel(
         }
     }
 
-    // exchange: team t gives the other team its partial sums of the row
-    // blocks that team owns (team 0: m blocks 0, 1 of each wave; team 1: 2, 3);
-    // constant block indices in each branch keep the accumulators in registers
+    // exchange: each team gives the other its partial sums of the B blocks
+    // the other owns (team 0 owns blocks 0 .. OWN0-1 of each wave, team 1 the
+    // rest).  Team t's given blocks fill its own region of LDS, [wave][a][b]
+    // x 64 lanes; constant block indices in each branch keep the
+    // accumulators in registers.
     __syncthreads();
     v4f* const xchg = reinterpret_cast<v4f*>(smem);
-    auto slot = [&](int tm, int a, int bb) { return (((tm * 4 + wt) * TK + a) * (TM / 2) + bb) * 64 + lane; };
-    auto finish = [&](auto Own) {
-        constexpr int own = decltype(Own)::value, give = TM / 2 - own;
-        const int other = 1 - team;
+    constexpr int CNT0 = TB - OWN0, CNT1 = OWN0;        // blocks given by team 0, 1
+    auto slot = [&](auto T, int a, int b) {
+        constexpr int t = decltype(T)::value;
+        constexpr int first = t == 0 ? OWN0 : 0, cnt = t == 0 ? CNT0 : CNT1;
+        constexpr int region = t == 0 ? 0 : 4 * TK * CNT0;
+        return ((region + (wt * TK + a) * cnt + (b - first)) * 64) + lane;
+    };
+    auto finish = [&](auto T) {
+        constexpr int t = decltype(T)::value;
+        constexpr int lo = t == 0 ? 0 : OWN0, hi = t == 0 ? OWN0 : TB;   // owned blocks
+        constexpr std::integral_constant<int, t> self{};
+        constexpr std::integral_constant<int, 1 - t> other{};
 #pragma unroll
         for (int a = 0; a < TK; ++a)
 #pragma unroll
-            for (int bb = 0; bb < TM / 2; ++bb) xchg[slot(team, a, bb)] = acc[a][give + bb];
+            for (int b = 0; b < TB; ++b)
+                if (b < lo || b >= hi) xchg[slot(self, a, b)] = acc[a][b];
         __syncthreads();
 #pragma unroll
         for (int a = 0; a < TK; ++a)
 #pragma unroll
-            for (int bb = 0; bb < TM / 2; ++bb) acc[a][own + bb] += xchg[slot(other, a, bb)];
-        // lane l of block (a, b): output row m = m0 + 64 wm + 16b + l%16,
-        // columns k = k0 + 80 wk + 16a + 4(l/16) .. +3
+            for (int b = lo; b < hi; ++b) acc[a][b] += xchg[slot(other, a, b)];
+        // lane l of block (a, b): output row b0 + (BB/2) wb + 16b + l%16,
+        // columns k0 + 80 wk + 16a + 4(l/16) .. +3
 #pragma unroll
-        for (int bb = 0; bb < TM / 2; ++bb) {
-            const int m = m0 + wm * 64 + 16 * (own + bb) + (lane & 15);
-            if (m >= M) continue;
+        for (int b = lo; b < hi; ++b) {
+            const int row = b0 + wb * (BB / 2) + 16 * b + (lane & 15);
+            if (row >= NBR) continue;
 #pragma unroll
             for (int a = 0; a < TK; ++a) {
                 const int k = k0 + wk * 80 + 16 * a + 4 * (lane >> 4);
                 if (k < K) {
-                    const v4f v = acc[a][own + bb];
-                    *reinterpret_cast<uint2*>(out + int64_t(m) * ldo + k) =
+                    const v4f v = acc[a][b];
+                    *reinterpret_cast<uint2*>(out + int64_t(row) * ldo + k) =
                         make_uint2(cvt_pk_bf16(v[0], v[1]), cvt_pk_bf16(v[2], v[3]));
                 }
             }
         }
     };
     if (team == 0) finish(std::integral_constant<int, 0>{});
-    else finish(std::integral_constant<int, TM / 2>{});
+    else finish(std::integral_constant<int, 1>{});
 }
 
 }  // namespace
 
-// Whether the dense dx takes the split-K kernel: a contraction of whole
-// 32-row steps long enough for two teams, and enough 128 x 160 tiles to fill
-// the chip where 128 x 128 tiles would leave a ragged second round.
-// (The weight's byte offsets, up to R rows of ldw, stay below 2^32.)
-static bool bf16_nn_splitk_applies(int M, int R, int K, int64_t ldw) {
-    if (M <= 64 || R % kStepRows || R < 2048 || K % 8) return false;
-    if (int64_t(R) * ldw * 2 >= (int64_t(1) << 32)) return false;
-    const int64_t tiles = int64_t((M + 127) / 128) * ((K + 159) / 160);
+// Whether a product takes the split-K kernel: a contraction of whole 32-row
+// steps long enough for two teams, and enough bb x 160 tiles to fill the chip
+// where 128 x 128 tiles would leave a ragged second round.  (The byte offsets
+// of the row-contracted operands, up to R rows, stay below 2^32.)
+static bool bf16_splitk_applies(int nb, int bb, int R, int K, int64_t lda, int64_t ldy, bool yt) {
+    if (nb <= 64 || R % kStepRows || R < 2048 || K % 8 || (yt && nb % 8)) return false;
+    if (int64_t(R) * lda * 2 >= (int64_t(1) << 32)) return false;
+    if (yt && int64_t(R) * ldy * 2 >= (int64_t(1) << 32)) return false;
+    const int64_t tiles = int64_t((nb + bb - 1) / bb) * ((K + 159) / 160);
     return tiles >= 128 && tiles <= 256;
 }
 
 hipError_t gemm_bf16_nn(hipStream_t st, const void* dy, int64_t ldy, const void* w, int64_t ldw,
                         void* out, int64_t ldo, int M, int N, int K) {
-    if (bf16_nn_splitk_applies(M, N, K, ldw)) {
+    if (bf16_splitk_applies(M, 128, N, K, ldw, ldy, false)) {
         const int tm = (M + 127) / 128, tk = (K + 159) / 160;
-        hipLaunchKernelGGL((gemm_bf16_nn_splitk_kernel<4>), dim3(unsigned(tm * tk)), dim3(512), 0,
-                           st, static_cast<const uint16_t*>(w), ldw,
+        hipLaunchKernelGGL((gemm_bf16_splitk_kernel<4, false>), dim3(unsigned(tm * tk)), dim3(512),
+                           0, st, static_cast<const uint16_t*>(w), ldw,
                            static_cast<const uint16_t*>(dy), ldy, static_cast<uint16_t*>(out), ldo,
                            N, K, M, tm, tk);
         return hipGetLastError();
@@ -660,6 +711,15 @@ hipError_t gemm_bf16_nn(hipStream_t st, const void* dy, int64_t ldy, const void*
 
 hipError_t gemm_bf16_tn(hipStream_t st, const void* dy, int64_t ldy, const void* x, int64_t ldx,
                         void* dw, int64_t ldo, int R, int N, int K) {
+    constexpr int STAGES_TN = 4;                // 2 x 4 x 20 KB of LDS
+    if (bf16_splitk_applies(N, 160, R, K, ldx, ldy, true)) {
+        const int tn = (N + 159) / 160, tk = (K + 159) / 160;
+        hipLaunchKernelGGL((gemm_bf16_splitk_kernel<STAGES_TN, true>), dim3(unsigned(tn * tk)),
+                           dim3(512), 0, st, static_cast<const uint16_t*>(x), ldx,
+                           static_cast<const uint16_t*>(dy), ldy, static_cast<uint16_t*>(dw), ldo,
+                           R, K, N, tn, tk);
+        return hipGetLastError();
+    }
     const int tiles_k = (K + 127) / 128, tiles_n = (N + 127) / 128;
     // two stages (one in flight): measured fastest at the C5 shape (75 us vs
     // 83-86 us for three to five), the smaller LDS footprint leaving room for

@@ -549,8 +549,12 @@ def test_ffn_full_size_c4(dev):
     assert np.array_equal(bits(y), want), mismatch(bits(y), want)
 
 
+# (2080, 3000, 1200) and (2048, 4000, 1280) take the split-K kernel with
+# ragged output rows and columns, the first with an odd number of 32-row
+# contraction steps
 @pytest.mark.parametrize("m,n,k", [(4096, 5120, 1280), (1000, 272, 208), (1, 16, 16),
-                                   (77, 1280, 4096), (300, 2000, 2000), (33, 2400, 1600)])
+                                   (77, 1280, 4096), (300, 2000, 2000), (33, 2400, 1600),
+                                   (2080, 3000, 1200), (2048, 4000, 1280)])
 def test_linear_dw(dev, m, n, k):
     """dL/dW = dy^T x through the bf16 MFMA kernel, against float64: each
     element within one bf16 rounding of the exact value plus the fp32
