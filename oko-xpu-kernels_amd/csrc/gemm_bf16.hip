@@ -424,9 +424,10 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_splitk_kernel(
     constexpr int BK = 160, TK = 5;                     // A side: k columns, blocks per wave
     constexpr int TB = YT ? 5 : 4, BB = 32 * TB;        // B side: blocks per wave, tile rows
     constexpr int AB = BK / 16, YB = BB / 16, NB = AB + YB;
-    // block order in a stage: the dx's dy blocks first (measured 3 us faster
-    // at C5 than after the weight's), dW's x blocks first
-    constexpr int A0 = YT ? 0 : YB, Y0 = YT ? AB : 0;
+    // block order in a stage: dy's blocks first (measured faster at C5 than
+    // after the A operand's: 61.0 against 63.9 us for the dx, 59.8 against
+    // 61.0 for dW)
+    constexpr int A0 = YB, Y0 = 0;
     constexpr int PER = (NB + 3) / 4, REM = NB % 4;
     constexpr int STAGE = NB * 1024, RING = S * STAGE;
     constexpr int OWN0 = (TB + 1) / 2;                  // team 0 owns B blocks 0..OWN0-1
