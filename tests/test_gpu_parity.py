@@ -456,6 +456,25 @@ def test_linear_one_call_exact(dev, m, n, k):
         assert np.array_equal(bits(out), want), (kind, mismatch(bits(out), want))
 
 
+# one shape per kernel the plain linear dispatches to (M <= 64: the skinny
+# kernel; few tiles: the 128 x 128 kernel; more: the two-block 256 x 160
+# kernel; a 256 x 320 tile per CU: the persistent kernel; narrow output with
+# a long K: split K over the block-layout activation), with ragged rows and
+# columns
+@pytest.mark.parametrize("m,n,k", [(16, 528, 768), (64, 2048, 1024), (65, 1040, 512),
+                                   (2000, 4000, 512), (4100, 5120, 256), (1500, 1920, 2048),
+                                   (2050, 1296, 3072)])
+def test_linear_dispatch_sweep(dev, m, n, k):
+    """int8.linear through each GEMM kernel, bit-exact against the oracle."""
+    x = activation(m, k, seed=m + k, n_out=4, mult=25.0)
+    w = weight(n, k, seed=n + 1)
+    bias = weight(1, n, seed=n + k, std=0.01)[0]
+    w8, ws = int8.prepare_weight(w.to(dev))
+    y = int8.linear(x.to(dev), w8, ws, bias.to(dev))
+    want = O.linear(bits(x), npy(w8), npy(ws), O.bf16_to_f32(bits(bias)))
+    assert np.array_equal(bits(y), want), mismatch(bits(y), want)
+
+
 def test_linear_shapes_and_dtypes(dev):
     x = activation(2 * 3 * 5, 512, seed=3).reshape(2, 3, 5, 512)
     w = weight(48, 512)
