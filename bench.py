@@ -193,6 +193,149 @@ def cpu_baseline(seconds):
     }
 
 
+def measure_side_rows(torch, int8, lib, L, st, dev, K, W, SET, extra, hbm_line, dev_gen,
+                      dev_act, dev_weight, x, w8, ws, bias):
+    """The entry points beside the config-3 step, each at the shape its caller
+    uses: the int32 GEMM of ``linear_acc``, ``linear``'s fused residual, the
+    standalone epilogues, the activation quantizers, ``dequant_weight`` and an
+    ``int8_linear`` training step (forward + backward) at config 5.  The
+    HBM-bound ones are timed cold (rotating buffer sets) and warm; the GEMMs
+    warm, on the config-3 operands."""
+    M, Kd, N = 4096, 1280, 10240
+    ops3 = 2.0 * M * N * Kd
+    xq, xs = int8.quantize(x)
+
+    def C(fn, *a):
+        if fn(st, *a) != 0:
+            L._err(lib, fn.__name__)
+
+    # linear_acc's GEMM (int32 out, 4 bytes per element stored) and
+    # linear(residual=, residual_scale=) with the addcmul in the store
+    acc = torch.empty((M, N), device=dev, dtype=torch.int32)
+    out = torch.empty((M, N), device=dev, dtype=torch.bfloat16)
+    res = (torch.randn(M, N, device=dev, generator=dev_gen(900)) * 0.1).to(torch.bfloat16)
+    rsc = (torch.rand(N, device=dev, generator=dev_gen(901)) + 0.5).to(torch.bfloat16)
+    ms_i32 = timed(torch, lambda i: C(lib.xpuint8_int8_gemm_stream, L._ptr(xq), L._ptr(w8),
+                                      L._ptr(acc), M, N, Kd), K, W, SET)
+    ms_res = timed(torch, lambda i: C(lib.xpuint8_linear_gemm_residual_stream, L._ptr(xq),
+                                      L._ptr(xs), L._ptr(w8), L._ptr(ws), L._ptr(bias), 1,
+                                      L._ptr(res), L._ptr(rsc), L._ptr(out), M, N, Kd),
+                   K, W, SET)
+    ms_acc_api = timed(torch, lambda i: int8.linear_acc(x, w8, ws), K, W, SET)
+    extra["config3_linear_acc"] = {
+        "gemm_int32_ms_warm": round(ms_i32, 5),
+        "gemm_int32_TOP/s_warm": round(ops3 / (ms_i32 * 1e-3) / 1e12, 1),
+        "api_ms_warm": round(ms_acc_api, 5)}
+    extra["config3_linear_residual"] = {
+        "gemm_residual_ms_warm": round(ms_res, 5),
+        "TOP/s_warm": round(ops3 / (ms_res * 1e-3) / 1e12, 1)}
+    log(f"[bench] linear_acc int32 GEMM {ms_i32:.4f} ms (API {ms_acc_api:.4f}); "
+        f"GEMM + residual {ms_res:.4f} ms")
+    del out, res
+
+    # the standalone epilogues on an int32 accumulator: dequant of [M, N], and
+    # dequant_slice of the q columns [M, 3072] of a [M, 9216] qkv accumulator
+    xs32 = torch.rand(M, device=dev, generator=dev_gen(902)) * 0.01
+    ws32 = torch.rand(N, device=dev, generator=dev_gen(903)) * 0.01
+    b32 = torch.randn(N, device=dev, generator=dev_gen(904)) * 0.01
+    bytes_dq = 6 * M * N + 4 * M + 8 * N
+    ndq = n_sets(bytes_dq)
+    dq = [(acc if i == 0 else torch.randint(-2 ** 20, 2 ** 20, (M, N), device=dev,
+                                            generator=dev_gen(910 + i), dtype=torch.int32),
+           torch.empty((M, N), device=dev, dtype=torch.bfloat16)) for i in range(ndq)]
+
+    def deq(i):
+        a, o = dq[i % ndq]
+        C(lib.xpuint8_dequant_epilogue_stream, L._ptr(a), L._ptr(o), L._ptr(xs32), L._ptr(ws32),
+                                            L._ptr(b32), M, N)
+    extra["config3_dequant"] = hbm_line(bytes_dq, timed(torch, deq, K, W, SET),
+                                        timed(torch, lambda i: deq(0), K, W, SET), sets=ndq)
+    del dq, acc
+    Nq, Nqkv = 3072, 9216
+    bytes_sl = 6 * M * Nq + 4 * M + 8 * Nq
+    nsl = n_sets(bytes_sl)
+    sl = [(torch.randint(-2 ** 20, 2 ** 20, (M, Nqkv), device=dev, generator=dev_gen(960 + i),
+                         dtype=torch.int32),
+           torch.empty((M, Nq), device=dev, dtype=torch.bfloat16)) for i in range(nsl)]
+
+    def deq_slice(i):
+        a, o = sl[i % nsl]
+        C(lib.xpuint8_dequant_epilogue_slice_stream, L._ptr(a), L._ptr(o), L._ptr(xs32),
+                                                  L._ptr(ws32), L._ptr(b32), M, Nq, Nqkv)
+    extra["qkv_dequant_slice_m4096_n3072"] = hbm_line(
+        bytes_sl, timed(torch, deq_slice, K, W, SET), timed(torch, lambda i: deq_slice(0), K, W, SET),
+        sets=nsl)
+    del sl
+
+    # quantize_act: GELU-erf on [4096, 5120], GEGLU-erf on [4096, 2*5120]
+    Mr, Kr = 4096, 5120
+    for name, aid, width in (("gelu_erf", 5, Kr), ("geglu_erf", 4, 2 * Kr)):
+        bytes_a = 2 * Mr * width + Mr * Kr + 4 * Mr
+        na = n_sets(bytes_a)
+        sa = [(dev_act(Mr, width, 1000 + 50 * aid + i),
+               torch.empty((Mr, Kr), device=dev, dtype=torch.int8),
+               torch.empty(Mr, device=dev, dtype=torch.float32)) for i in range(na)]
+
+        def qa(i, sa=sa, na=na, aid=aid):
+            xi, qi, si = sa[i % na]
+            C(lib.xpuint8_convrot_quantize_act_stream, L._ptr(xi), L._ptr(qi), L._ptr(si),
+                                                    Mr, Kr, aid)
+        extra[f"quantize_act_{name}_m4096_k5120"] = hbm_line(
+            bytes_a, timed(torch, qa, K, W, SET), timed(torch, lambda i: qa(0), K, W, SET), sets=na)
+        del sa
+
+    # dequant_act_quantize (the reference's FFN middle step): GEGLU on an int32
+    # [4096, 2*5120] accumulator
+    bytes_daq = 4 * Mr * 2 * Kr + Mr * Kr + 4 * Mr + 8 * Kr + 4 * Mr
+    ndaq = n_sets(bytes_daq)
+    xsd = torch.rand(Mr, device=dev, generator=dev_gen(1300)) * 1e-3
+    wsd = torch.rand(2 * Kr, device=dev, generator=dev_gen(1301)) * 1e-3
+    sd = [(torch.randint(-2 ** 20, 2 ** 20, (Mr, 2 * Kr), device=dev, generator=dev_gen(1310 + i),
+                         dtype=torch.int32),
+           torch.empty((Mr, Kr), device=dev, dtype=torch.int8),
+           torch.empty(Mr, device=dev, dtype=torch.float32)) for i in range(ndaq)]
+
+    def daq(i):
+        a, qi, si = sd[i % ndaq]
+        C(lib.xpuint8_dequant_act_quantize_stream, L._ptr(a), L._ptr(qi), L._ptr(si), L._ptr(xsd),
+                                                L._ptr(wsd), Mr, Kr, 4)
+    extra["dequant_act_quantize_geglu_m4096_k5120"] = hbm_line(
+        bytes_daq, timed(torch, daq, K, W, SET), timed(torch, lambda i: daq(0), K, W, SET),
+        sets=ndaq)
+    del sd
+
+    # dequant_weight of a config-2 weight [10240, 1280]
+    bytes_dw = 3 * 10240 * 1280 + 4 * 10240
+    ndw = n_sets(bytes_dw)
+    sw = [int8.prepare_weight(dev_weight(10240, 1280, 1400 + i)) for i in range(ndw)]
+    ow = [torch.empty((10240, 1280), device=dev, dtype=torch.bfloat16) for _ in range(ndw)]
+
+    def dqw(i):
+        w_i, s_i = sw[i % ndw]
+        C(lib.xpuint8_dequant_weight_stream, L._ptr(w_i), L._ptr(s_i), L._ptr(ow[i % ndw]),
+                                          10240, 1280)
+    extra["dequant_weight_n10240_k1280"] = hbm_line(
+        bytes_dw, timed(torch, dqw, K, W, SET), timed(torch, lambda i: dqw(0), K, W, SET), sets=ndw)
+    del sw, ow
+
+    # int8_linear training step at config 5 shapes: forward, then backward
+    # (dx, dbias; the weight is frozen int8), for both backward modes
+    x5 = dev_act(4096, 1280, 1500).requires_grad_(True)
+    w5_8, w5_s = int8.prepare_weight(dev_weight(5120, 1280, 1501))
+    b5 = dev_weight(1, 5120, 1502, 0.01)[0].requires_grad_(True)
+    dy5 = (torch.randn(4096, 5120, device=dev, generator=dev_gen(1503)) * 1e-3).to(torch.bfloat16)
+    ops_step = 2 * (2.0 * 4096 * 5120 * 1280)
+    for mode in ("int8", "dense"):
+        def step(i, mode=mode):
+            x5.grad = None
+            b5.grad = None
+            int8.int8_linear(x5, w5_8, w5_s, b5, mode=mode).backward(dy5)
+        ms_st = timed(torch, step, K, W, SET)
+        extra[f"config5_int8_linear_step_{mode}"] = {
+            "ms": round(ms_st, 5), "TOP/s": round(ops_step / (ms_st * 1e-3) / 1e12, 1)}
+        log(f"[bench] int8_linear step ({mode} backward): {ms_st:.4f} ms")
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -479,6 +622,8 @@ def main():
                                                             sets=nro)
         del accs, qsl
         log(f"[bench] rms+rope dequant: {ms_rope:.4f} / {ms_rope_warm:.4f} ms")
+        measure_side_rows(torch, int8, lib, L, st, dev, K, W, SET, extra, hbm_line, dev_gen,
+                          dev_act, dev_weight, x, w8, ws, bias)
 
     line = {
         "metric": "int8_linear TOPS (M=4096,K=1280,N=10240); rotate+quant HBM GB/s",

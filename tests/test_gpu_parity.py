@@ -364,18 +364,21 @@ def test_dequant_rounding_edge_cases(dev):
 
 
 @pytest.mark.parametrize("bias", [False, True])
-def test_dequant_and_slice_exact(dev, bias):
-    rng = np.random.default_rng(2)
-    acc = rng.integers(-2**22, 2**22, (37, 96)).astype(np.int32)
-    xs = rng.uniform(1e-3, 1e-1, 37).astype(np.float32)
-    ws = rng.uniform(1e-4, 1e-2, 96).astype(np.float32)
-    b = rng.standard_normal(96).astype(np.float32) if bias else None
+@pytest.mark.parametrize("m,n", [(37, 96), (5, 1040), (3, 2064), (9, 4112), (2, 10240)])
+def test_dequant_and_slice_exact(dev, bias, m, n):
+    """Row widths on both sides of the kernel's 1024-column slot and
+    2048-column block boundaries; the slice is read from a wider row."""
+    rng = np.random.default_rng(2 + n)
+    acc = rng.integers(-2**22, 2**22, (m, n)).astype(np.int32)
+    xs = rng.uniform(1e-3, 1e-1, m).astype(np.float32)
+    ws = rng.uniform(1e-4, 1e-2, n).astype(np.float32)
+    b = rng.standard_normal(n).astype(np.float32) if bias else None
     t = lambda a: torch.from_numpy(a).to(dev)
     got = bits(int8.dequant(t(acc), t(xs), t(ws), None if b is None else t(b)))
     want = O.dequant(acc, xs, ws, b)
     assert np.array_equal(got, want), mismatch(got, want)
     wide = t(np.concatenate([acc, acc[:, :32]], axis=1))
-    sl = bits(int8.dequant_slice(wide[:, :96], t(xs), t(ws), None if b is None else t(b)))
+    sl = bits(int8.dequant_slice(wide[:, :n], t(xs), t(ws), None if b is None else t(b)))
     assert np.array_equal(sl, want)
 
 
