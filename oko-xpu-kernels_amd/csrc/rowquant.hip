@@ -34,6 +34,59 @@ __device__ __forceinline__ T* at32(T* base, int r, int64_t ld, int col) {
     return reinterpret_cast<T*>(reinterpret_cast<B*>(base) + uint64_t(off));
 }
 
+// ------------------------------------------------------- table window in LDS
+// The activations with one table lookup per output (gelu_tanh, swiglu's
+// SiLU, GEGLU's and GELU's erf form) read their table through an LDS copy of
+// its window (activations.hpp: inputs with |x| in [2^-12, 2^4), 4096 entries,
+// 8 KB), filled once per block; inputs outside it read the table in global
+// memory behind a wave-uniform branch.  The same table words either way.
+template <int ACT>
+__host__ __device__ constexpr int lookup_table() {
+    return ACT == 1 ? kTabGeluTanh : ACT == 2 ? kTabSilu : (ACT == 4 || ACT == 5) ? kTabGeluErf : -1;
+}
+
+// Loaders that read through a window declare kWinTab >= 0 and expand_w().
+template <class L, class = void>
+struct LoaderWindow : std::integral_constant<int, -1> {};
+template <class L>
+struct LoaderWindow<L, std::void_t<decltype(L::kWinTab)>> : std::integral_constant<int, L::kWinTab> {};
+
+// 16-byte unit i < 512 of table T's window: units [0, 256) are table words
+// kWinLo + 8i (positive inputs), units [256, 512) the same for the negative
+// ones; LDS position p holds the word of win_bits(p).
+__device__ __forceinline__ const uint4* win_unit(const uint16_t* tab, int T, int i) {
+    const uint32_t word = (uint32_t(i >> 8) << 15) + uint32_t(kWinLo) + 8u * uint32_t(i & 255);
+    return reinterpret_cast<const uint4*>(tab + size_t(T) * kTabSize + word);
+}
+
+// Table words for 16 inputs given by their bf16 bits k: LDS reads at
+// clamped positions, then the global table for inputs outside the window, if
+// the wave has any.
+template <int T>
+__device__ __forceinline__ void win_lookup16(const uint16_t* win, const uint16_t* tab,
+                                             const uint32_t (&k)[16], uint32_t (&t)[16]) {
+    bool miss = false;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const uint32_t rel = (k[i] & 0x7FFFu) - uint32_t(kWinLo);
+        miss = miss || rel >= uint32_t(kWinHalf);
+        t[i] = win[((k[i] >> 15) << 11) + min(rel, uint32_t(kWinHalf - 1))];
+    }
+    if (__builtin_amdgcn_ballot_w64(miss)) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            if ((k[i] & 0x7FFFu) - uint32_t(kWinLo) >= uint32_t(kWinHalf))
+                t[i] = tab[T * kTabSize + k[i]];
+    }
+}
+
+// activate<ACT>(a, b) of a one-lookup activation from its table word t
+template <int ACT>
+__device__ __forceinline__ float act_from_word(float a, float b, uint32_t t) {
+    if constexpr (ACT == 1 || ACT == 5) return tab_float(t);
+    else return bf16_round(act_combine<ACT>(a, b, &t));
+}
+
 // ------------------------------------------------------------------ loaders
 // A loader produces the pre-rotation values of elements [col, col+16) of a
 // row, as bf16-valued floats, in two steps: fetch() issues the memory reads
@@ -103,6 +156,26 @@ struct LoadAct {
             for (int t = 0; t < 16; ++t) v[t] = activate<ACT>(tab, a[t], 0.f);
         }
     }
+    static constexpr int kWinTab = lookup_table<ACT>();
+    __device__ __forceinline__ void expand_w(const Raw& r, float (&v)[16],
+                                             const uint16_t* win) const {
+        // the looked-up operand's bf16 bits: the gate half for GEGLU, else the first
+        const LoadBF16::Raw& kr = ACT == 4 ? r.b : r.a;
+        const uint32_t kw[8] = {kr.a.x, kr.a.y, kr.a.z, kr.a.w, kr.b.x, kr.b.y, kr.b.z, kr.b.w};
+        uint32_t k[16], w[16];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) { k[2 * j] = kw[j] & 0xFFFFu; k[2 * j + 1] = kw[j] >> 16; }
+        win_lookup16<kWinTab>(win, tab, k, w);
+        float a[16], b[16];
+        LoadBF16{x, ld}.expand(r.a, a);
+        if constexpr (act_paired(ACT)) LoadBF16{x, ld}.expand(r.b, b);
+        else {
+#pragma unroll
+            for (int t = 0; t < 16; ++t) b[t] = 0.f;
+        }
+#pragma unroll
+        for (int t = 0; t < 16; ++t) v[t] = act_from_word<ACT>(a[t], b[t], w[t]);
+    }
     __device__ __forceinline__ void operator()(int64_t row, int col, float (&v)[16]) const {
         expand(fetch(row, col), v);
     }
@@ -131,38 +204,53 @@ struct LoadDequantAct {
             o[4 * j + 3] = bf16_round(float(a.w) * (w.w * xsr));
         }
     }
-    __device__ __forceinline__ void operator()(int64_t row, int col, float (&v)[16]) const {
-        const float xsr = xs[row];
-        float h[16];
-        deq(row, col, xsr, h);
-        if constexpr (act_paired(ACT)) {
-            float g[16];
-            deq(row, col + half, xsr, g);
-#pragma unroll
-            for (int t = 0; t < 16; ++t) v[t] = activate<ACT>(tab, h[t], g[t]);
-        } else {
-#pragma unroll
-            for (int t = 0; t < 16; ++t) v[t] = activate<ACT>(tab, h[t], 0.f);
-        }
-    }
-    // (not pipelined: the raw form would be 32 registers of accumulators)
-    struct Raw { float v[16]; };
+    // Raw: the dequantized bf16 values, two to a word: the first half in the
+    // low 16 bits, the gate half (paired) in the high ones.  Without a table
+    // window (situ) the activation is applied here and its bf16 result is
+    // held in the low bits.
+    static constexpr int kWinTab = lookup_table<ACT>();
+    struct Raw { uint32_t w[16]; };
     __device__ __forceinline__ Raw fetch(int64_t row, int col) const {
         Raw r;
-        (*this)(row, col, r.v);
+        const float xsr = xs[row];
+        float h[16], g[16];
+        deq(row, col, xsr, h);
+        if constexpr (act_paired(ACT)) deq(row, col + half, xsr, g);
+#pragma unroll
+        for (int t = 0; t < 16; ++t) {
+            if constexpr (kWinTab < 0)
+                r.w[t] = __float_as_uint(activate<ACT>(tab, h[t], act_paired(ACT) ? g[t] : 0.f)) >> 16;
+            else if constexpr (act_paired(ACT))
+                r.w[t] = (__float_as_uint(h[t]) >> 16) | (__float_as_uint(g[t]) & 0xFFFF0000u);
+            else
+                r.w[t] = __float_as_uint(h[t]) >> 16;
+        }
         return r;
     }
     __device__ __forceinline__ LoadDequantAct rebase(int64_t row0) const {
         return {acc + row0 * ld, ld, half, xs + row0, ws, tab};
     }
-    __device__ __forceinline__ Raw fetch_r(int r, int col) const {
-        Raw o;
-        (*this)(r, col, o.v);
-        return o;
-    }
+    __device__ __forceinline__ Raw fetch_r(int r, int col) const { return fetch(r, col); }
     __device__ __forceinline__ void expand(const Raw& r, float (&v)[16]) const {
 #pragma unroll
-        for (int t = 0; t < 16; ++t) v[t] = r.v[t];
+        for (int t = 0; t < 16; ++t) {
+            const float h = __uint_as_float(r.w[t] << 16), g = __uint_as_float(r.w[t] & 0xFFFF0000u);
+            v[t] = kWinTab < 0 ? h : activate<ACT>(tab, h, g);
+        }
+    }
+    __device__ __forceinline__ void expand_w(const Raw& r, float (&v)[16],
+                                             const uint16_t* win) const {
+        uint32_t k[16], w[16];
+#pragma unroll
+        for (int t = 0; t < 16; ++t) k[t] = ACT == 4 ? r.w[t] >> 16 : r.w[t] & 0xFFFFu;
+        win_lookup16<kWinTab>(win, tab, k, w);
+#pragma unroll
+        for (int t = 0; t < 16; ++t)
+            v[t] = act_from_word<ACT>(__uint_as_float(r.w[t] << 16),
+                                      __uint_as_float(r.w[t] & 0xFFFF0000u), w[t]);
+    }
+    __device__ __forceinline__ void operator()(int64_t row, int col, float (&v)[16]) const {
+        expand(fetch(row, col), v);
     }
 };
 
@@ -359,6 +447,21 @@ __global__ __launch_bounds__(1024) void rowquant_seg_kernel(Loader load, int8_t*
                                                            float* __restrict__ scale, int64_t M,
                                                            int K, int S, int R, int s_mul) {
     __shared__ uint32_t row_max[kMaxSegments];
+    // (one group per lane only: with two, the window's staging registers
+    // would push the paired dequant loaders past the register budget)
+    constexpr int WT = P == 1 ? LoaderWindow<Loader>::value : -1;
+    __shared__ __align__(16) uint16_t win[WT >= 0 ? kWinSize : 8];
+    // the window's 512 16-byte units, read before the row and without
+    // branches (a branch per read made the compiler wait for each one before
+    // the next): blocks have at least 192 threads, so three reads per thread
+    // at clamped unit indices cover it, and lanes that clamp to the same unit
+    // write the same value
+    uint4 wv[3];
+    if constexpr (WT >= 0) {
+#pragma unroll
+        for (int j = 0; j < 3; ++j)
+            wv[j] = *win_unit(load.tab, WT, min(int(threadIdx.x + j * blockDim.x), 511));
+    }
     const int seg = threadIdx.x >> 4;
     const int sl = threadIdx.x & 15;
     const int r = int(__umul24(seg, s_mul)) >> 12;   // seg / S (exact for seg, S <= 64)
@@ -371,6 +474,11 @@ __global__ __launch_bounds__(1024) void rowquant_seg_kernel(Loader load, int8_t*
     const Loader lb = load.rebase(row0);
     int col[P];
     typename Loader::Raw raw[P];
+    float v[P][16];
+    // a window-capable loader without its window (two groups per lane)
+    // expands each group as soon as it is fetched, which keeps one group's
+    // table reads in flight at a time
+    constexpr bool EARLY = LoaderWindow<Loader>::value >= 0 && WT < 0;
     const XlaneSigns sgn = xlane_signs(sl);
 #pragma unroll
     for (int p = 0; p < P; ++p) {
@@ -381,12 +489,20 @@ __global__ __launch_bounds__(1024) void rowquant_seg_kernel(Loader load, int8_t*
             raw[p] = typename Loader::Raw{};
             if (col[p] < K) raw[p] = lb.fetch_r(r_ld, col[p]);
         }
+        if constexpr (EARLY) lb.expand(raw[p], v[p]);
     }
     if (threadIdx.x < R) row_max[threadIdx.x] = 0u;
-    lds_barrier();                               // the zeros land before any max
-    float v[P][16];
+    if constexpr (WT >= 0) {
 #pragma unroll
-    for (int p = 0; p < P; ++p) lb.expand(raw[p], v[p]);
+        for (int j = 0; j < 3; ++j)
+            *reinterpret_cast<uint4*>(win + 8 * min(int(threadIdx.x + j * blockDim.x), 511)) = wv[j];
+    }
+    lds_barrier();                               // the zeros (and window) land before any use
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        if constexpr (WT >= 0) lb.expand_w(raw[p], v[p], win);
+        else if constexpr (!EARLY) lb.expand(raw[p], v[p]);
+    }
     float dom = 1.0f;
     if constexpr (ROT) dom = rotate_groups<P>(v, sgn);
     float m = 0.f;

@@ -273,6 +273,58 @@ def test_quantize_act_exact(dev, act, m, k):
     assert np.array_equal(npy(q), wq), mismatch(npy(q), wq)
 
 
+# bf16 bit patterns on both sides of the table window the activation
+# quantizers read from LDS (|x| in [2^-12, 16)): zeros, denormals, the largest
+# value below 2^-12, 2^-12, the largest below 16, 16, and values far outside
+WINDOW_EDGES = np.array([0x0000, 0x8000, 0x0001, 0x8001, 0x397F, 0xB97F, 0x3980, 0xB980,
+                         0x417F, 0xC17F, 0x4180, 0xC180, 0x447A, 0xC47A, 0x3F80, 0xBF80],
+                        np.uint16)
+
+
+@pytest.mark.parametrize("act", [1, 2, 4, 5])
+@pytest.mark.parametrize("m,k", [(7, 1280), (2, 20480)])
+def test_quantize_act_window_edges(dev, act, m, k):
+    """Every lookup operand on a window edge or outside it, mixed into ordinary
+    rows: the LDS lookups, the global-table fallback of a partly missing wave,
+    and (k = 20480, two groups per lane) the kernel without the window."""
+    name = {v: kk for kk, v in int8.ACTIVATIONS.items()}[act]
+    width = 2 * k if act in O.PAIRED else k
+    x = bits(activation(m, width, seed=act + k, scale=1.5))
+    rng = np.random.default_rng(act * 7 + m)
+    pick = rng.random((m, width)) < 0.3
+    x[pick] = rng.choice(WINDOW_EDGES, int(pick.sum()))
+    x[0, :16] = WINDOW_EDGES                                 # one segment entirely on edges
+    q, s = int8.quantize_act(from_bits(x, dev), name)
+    wq, ws = O.quantize_act(x, act)
+    assert np.array_equal(npy(s), ws), mismatch(npy(s), ws)
+    assert np.array_equal(npy(q), wq), mismatch(npy(q), wq)
+
+
+@pytest.mark.parametrize("act", [4, 5])
+@pytest.mark.parametrize("k", [1280, 20480])
+def test_dequant_act_quantize_window_edges(dev, act, k):
+    """Dequantized values on the window edges: with both scales 2^-10 the
+    value is bf16(acc * 2^-20), so acc = 256 gives 2^-12, 255 the largest
+    value below it, 2^24 gives 16 and 2^24 - 2^16 a value just below."""
+    m = 6
+    n = 2 * k if act in O.PAIRED else k
+    rng = np.random.default_rng(act + k)
+    edges = np.array([0, 1, -1, 255, -255, 256, -256, 2 ** 24 - 2 ** 16, -(2 ** 24 - 2 ** 16),
+                      2 ** 24, -(2 ** 24), 2 ** 28, -(2 ** 28), 2 ** 20, -(2 ** 20)], np.int64)
+    acc = rng.integers(-2 ** 22, 2 ** 22, (m, n))
+    pick = rng.random((m, n)) < 0.4
+    acc[pick] = rng.choice(edges, int(pick.sum()))
+    acc = acc.astype(np.int32)
+    xs = np.full(m, 2.0 ** -10, np.float32)
+    ws = np.full(n, 2.0 ** -10, np.float32)
+    name = {v: kk for kk, v in int8.ACTIVATIONS.items()}[act]
+    t = lambda a: torch.from_numpy(a).to(dev)
+    q, s = int8.dequant_act_quantize(t(acc), t(xs), t(ws), name)
+    wq, wsc = O.dequant_act_quantize(acc, xs, ws, act)
+    assert np.array_equal(npy(s), wsc), mismatch(npy(s), wsc)
+    assert np.array_equal(npy(q), wq), mismatch(npy(q), wq)
+
+
 @pytest.mark.parametrize("m,k", [(1, 256), (13, 1280), (64, 5120), (3, 20480)])
 def test_rotate_exact(dev, m, k):
     x = activation(m, k, seed=k)
