@@ -34,22 +34,38 @@ __device__ __forceinline__ T* at32(T* base, int r, int64_t ld, int col) {
     return reinterpret_cast<T*>(reinterpret_cast<B*>(base) + uint64_t(off));
 }
 
-// ------------------------------------------------------- table window in LDS
-// The activations with one table lookup per output (gelu_tanh, swiglu's
-// SiLU, GEGLU's and GELU's erf form) read their table through an LDS copy of
-// its window (activations.hpp: inputs with |x| in [2^-12, 2^4), 4096 entries,
-// 8 KB), filled once per block; inputs outside it read the table in global
-// memory behind a wave-uniform branch.  The same table words either way.
+// ------------------------------------------------------- table windows in LDS
+// The activations read their tables through LDS copies of the tables'
+// windows (activations.hpp: inputs with |x| in [2^-12, 2^4), 4096 entries,
+// 8 KB per table), filled once per block; inputs outside a window read the
+// table in global memory behind a wave-uniform branch.  The same table words
+// either way.  One window for the one-lookup activations (gelu_tanh,
+// swiglu's SiLU, the erf GELU of GEGLU and GELU), three for situ (tanh(g/4)
+// and sigmoid(g) of the gate, tanh(h/25) of the hidden value).
 template <int ACT>
-__host__ __device__ constexpr int lookup_table() {
-    return ACT == 1 ? kTabGeluTanh : ACT == 2 ? kTabSilu : (ACT == 4 || ACT == 5) ? kTabGeluErf : -1;
+__host__ __device__ constexpr int win_count() {
+    return ACT == 3 ? 3 : (ACT == 1 || ACT == 2 || ACT == 4 || ACT == 5) ? 1 : 0;
+}
+template <int ACT>
+__host__ __device__ constexpr int win_table(int j) {
+    return ACT == 1 ? kTabGeluTanh
+         : ACT == 2 ? kTabSilu
+         : (ACT == 4 || ACT == 5) ? kTabGeluErf
+         : j == 0 ? kTabSituTanhG : j == 1 ? kTabSigmoid : kTabSituTanhH;
 }
 
-// Loaders that read through a window declare kWinTab >= 0 and expand_w().
+// Loaders that read through windows declare kWins > 0, win_tab(j) and expand_w().
 template <class L, class = void>
-struct LoaderWindow : std::integral_constant<int, -1> {};
+struct LoaderWins : std::integral_constant<int, 0> {};
 template <class L>
-struct LoaderWindow<L, std::void_t<decltype(L::kWinTab)>> : std::integral_constant<int, L::kWinTab> {};
+struct LoaderWins<L, std::void_t<decltype(L::kWins)>> : std::integral_constant<int, L::kWins> {};
+// Loaders whose expand() (the global-table form) should run right after each
+// fetch when several groups are fetched: they declare kExpandAtFetch.
+template <class L, class = void>
+struct LoaderEarly : std::false_type {};
+template <class L>
+struct LoaderEarly<L, std::void_t<decltype(L::kExpandAtFetch)>>
+    : std::integral_constant<bool, L::kExpandAtFetch> {};
 
 // 16-byte unit i < 512 of table T's window: units [0, 256) are table words
 // kWinLo + 8i (positive inputs), units [256, 512) the same for the negative
@@ -59,32 +75,73 @@ __device__ __forceinline__ const uint4* win_unit(const uint16_t* tab, int T, int
     return reinterpret_cast<const uint4*>(tab + size_t(T) * kTabSize + word);
 }
 
-// Table words for 16 inputs given by their bf16 bits k: LDS reads at
-// clamped positions, then the global table for inputs outside the window, if
-// the wave has any.
-template <int T>
-__device__ __forceinline__ void win_lookup16(const uint16_t* win, const uint16_t* tab,
-                                             const uint32_t (&k)[16], uint32_t (&t)[16]) {
-    bool miss = false;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const uint32_t rel = (k[i] & 0x7FFFu) - uint32_t(kWinLo);
-        miss = miss || rel >= uint32_t(kWinHalf);
-        t[i] = win[((k[i] >> 15) << 11) + min(rel, uint32_t(kWinHalf - 1))];
-    }
-    if (__builtin_amdgcn_ballot_w64(miss)) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i)
-            if ((k[i] & 0x7FFFu) - uint32_t(kWinLo) >= uint32_t(kWinHalf))
-                t[i] = tab[T * kTabSize + k[i]];
-    }
+// Whether bf16 bits k lie outside the windows
+__device__ __forceinline__ bool win_outside(uint32_t k) {
+    return (k & 0x7FFFu) - uint32_t(kWinLo) >= uint32_t(kWinHalf);
+}
+// The window word of bf16 bits k (clamped into the window when outside)
+__device__ __forceinline__ uint32_t win_word(const uint16_t* win, uint32_t k) {
+    const uint32_t rel = (k & 0x7FFFu) - uint32_t(kWinLo);
+    return win[((k >> 15) << 11) + min(rel, uint32_t(kWinHalf - 1))];
 }
 
-// activate<ACT>(a, b) of a one-lookup activation from its table word t
+// activate<ACT>(a, b) for 16 inputs given by their bf16 bits (ka: the first
+// input, kb: the second; unused for the one-input activations), the tables
+// read through the windows at win (win_count<ACT>() of them, back to back),
+// with a wave-uniform branch, rarely taken, for lookup operands outside the
+// windows.  One-lookup activations read all 16 words, then patch the missing
+// ones from the table in global memory.  Situ (three lookups) instead
+// recomputes a missing output from the global tables, so that only inputs and
+// outputs are live across the branch: patching its 48 words kept every word
+// and key live and cost the kernel half its occupancy (47 against 106-124
+// VGPRs; 32.5 against 51 us for quantize_act at 4096 x 5120), while for the
+// one-lookup activations patching measured faster (dequant_act_quantize
+// GELU at 4096 x 5120: 26.9 against 30.4 us).
 template <int ACT>
-__device__ __forceinline__ float act_from_word(float a, float b, uint32_t t) {
-    if constexpr (ACT == 1 || ACT == 5) return tab_float(t);
-    else return bf16_round(act_combine<ACT>(a, b, &t));
+__device__ __forceinline__ void act_windowed(const uint16_t* win, const uint16_t* tab,
+                                             const uint32_t (&ka)[16], const uint32_t (&kb)[16],
+                                             float (&v)[16]) {
+    if constexpr (ACT == 3) {
+        bool miss = false;
+#pragma unroll
+        for (int t = 0; t < 16; ++t) {
+            const uint32_t w[3] = {win_word(win, kb[t]), win_word(win + kWinSize, kb[t]),
+                                   win_word(win + 2 * kWinSize, ka[t])};
+            miss = miss || win_outside(ka[t]) || win_outside(kb[t]);
+            v[t] = bf16_round(act_combine<3>(0.f, 0.f, w));
+        }
+        if (__builtin_amdgcn_ballot_w64(miss)) {
+#pragma unroll
+            for (int t = 0; t < 16; ++t)
+                if (win_outside(ka[t]) || win_outside(kb[t]))
+                    v[t] = activate<3>(tab, __uint_as_float(ka[t] << 16),
+                                       __uint_as_float(kb[t] << 16));
+        }
+    } else {
+        constexpr int T = win_table<ACT>(0);
+        const uint32_t* k = ACT == 4 ? kb : ka;
+        uint32_t w[16];
+        bool miss = false;
+#pragma unroll
+        for (int t = 0; t < 16; ++t) {
+            miss = miss || win_outside(k[t]);
+            w[t] = win_word(win, k[t]);
+        }
+        if (__builtin_amdgcn_ballot_w64(miss)) {
+#pragma unroll
+            for (int t = 0; t < 16; ++t)
+                if (win_outside(k[t])) w[t] = tab[T * kTabSize + k[t]];
+        }
+#pragma unroll
+        for (int t = 0; t < 16; ++t) {
+            if constexpr (ACT == 1 || ACT == 5) {
+                v[t] = tab_float(w[t]);
+            } else {
+                const float a = __uint_as_float(ka[t] << 16), b = __uint_as_float(kb[t] << 16);
+                v[t] = bf16_round(act_combine<ACT>(a, b, &w[t]));
+            }
+        }
+    }
 }
 
 // ------------------------------------------------------------------ loaders
@@ -156,25 +213,21 @@ struct LoadAct {
             for (int t = 0; t < 16; ++t) v[t] = activate<ACT>(tab, a[t], 0.f);
         }
     }
-    static constexpr int kWinTab = lookup_table<ACT>();
+    static constexpr int kWins = win_count<ACT>();
+    __host__ __device__ static constexpr int win_tab(int j) { return win_table<ACT>(j); }
     __device__ __forceinline__ void expand_w(const Raw& r, float (&v)[16],
                                              const uint16_t* win) const {
-        // the looked-up operand's bf16 bits: the gate half for GEGLU, else the first
-        const LoadBF16::Raw& kr = ACT == 4 ? r.b : r.a;
-        const uint32_t kw[8] = {kr.a.x, kr.a.y, kr.a.z, kr.a.w, kr.b.x, kr.b.y, kr.b.z, kr.b.w};
-        uint32_t k[16], w[16];
+        uint32_t ka[16], kb[16];
+        const uint32_t wa[8] = {r.a.a.x, r.a.a.y, r.a.a.z, r.a.a.w, r.a.b.x, r.a.b.y, r.a.b.z, r.a.b.w};
+        const uint32_t wb[8] = {r.b.a.x, r.b.a.y, r.b.a.z, r.b.a.w, r.b.b.x, r.b.b.y, r.b.b.z, r.b.b.w};
 #pragma unroll
-        for (int j = 0; j < 8; ++j) { k[2 * j] = kw[j] & 0xFFFFu; k[2 * j + 1] = kw[j] >> 16; }
-        win_lookup16<kWinTab>(win, tab, k, w);
-        float a[16], b[16];
-        LoadBF16{x, ld}.expand(r.a, a);
-        if constexpr (act_paired(ACT)) LoadBF16{x, ld}.expand(r.b, b);
-        else {
-#pragma unroll
-            for (int t = 0; t < 16; ++t) b[t] = 0.f;
+        for (int j = 0; j < 8; ++j) {
+            ka[2 * j] = wa[j] & 0xFFFFu;
+            ka[2 * j + 1] = wa[j] >> 16;
+            kb[2 * j] = act_paired(ACT) ? wb[j] & 0xFFFFu : 0u;
+            kb[2 * j + 1] = act_paired(ACT) ? wb[j] >> 16 : 0u;
         }
-#pragma unroll
-        for (int t = 0; t < 16; ++t) v[t] = act_from_word<ACT>(a[t], b[t], w[t]);
+        act_windowed<ACT>(win, tab, ka, kb, v);
     }
     __device__ __forceinline__ void operator()(int64_t row, int col, float (&v)[16]) const {
         expand(fetch(row, col), v);
@@ -205,10 +258,7 @@ struct LoadDequantAct {
         }
     }
     // Raw: the dequantized bf16 values, two to a word: the first half in the
-    // low 16 bits, the gate half (paired) in the high ones.  Without a table
-    // window (situ) the activation is applied here and its bf16 result is
-    // held in the low bits.
-    static constexpr int kWinTab = lookup_table<ACT>();
+    // low 16 bits, the gate half (paired) in the high ones
     struct Raw { uint32_t w[16]; };
     __device__ __forceinline__ Raw fetch(int64_t row, int col) const {
         Raw r;
@@ -218,12 +268,8 @@ struct LoadDequantAct {
         if constexpr (act_paired(ACT)) deq(row, col + half, xsr, g);
 #pragma unroll
         for (int t = 0; t < 16; ++t) {
-            if constexpr (kWinTab < 0)
-                r.w[t] = __float_as_uint(activate<ACT>(tab, h[t], act_paired(ACT) ? g[t] : 0.f)) >> 16;
-            else if constexpr (act_paired(ACT))
-                r.w[t] = (__float_as_uint(h[t]) >> 16) | (__float_as_uint(g[t]) & 0xFFFF0000u);
-            else
-                r.w[t] = __float_as_uint(h[t]) >> 16;
+            r.w[t] = __float_as_uint(h[t]) >> 16;
+            if constexpr (act_paired(ACT)) r.w[t] |= __float_as_uint(g[t]) & 0xFFFF0000u;
         }
         return r;
     }
@@ -233,21 +279,25 @@ struct LoadDequantAct {
     __device__ __forceinline__ Raw fetch_r(int r, int col) const { return fetch(r, col); }
     __device__ __forceinline__ void expand(const Raw& r, float (&v)[16]) const {
 #pragma unroll
-        for (int t = 0; t < 16; ++t) {
-            const float h = __uint_as_float(r.w[t] << 16), g = __uint_as_float(r.w[t] & 0xFFFF0000u);
-            v[t] = kWinTab < 0 ? h : activate<ACT>(tab, h, g);
-        }
+        for (int t = 0; t < 16; ++t)
+            v[t] = activate<ACT>(tab, __uint_as_float(r.w[t] << 16),
+                                 __uint_as_float(r.w[t] & 0xFFFF0000u));
     }
+    static constexpr int kWins = win_count<ACT>();
+    // without windows (two groups per lane), expand each group as soon as it
+    // is fetched: one group's table reads in flight at a time keeps the
+    // kernel within its registers
+    static constexpr bool kExpandAtFetch = true;
+    __host__ __device__ static constexpr int win_tab(int j) { return win_table<ACT>(j); }
     __device__ __forceinline__ void expand_w(const Raw& r, float (&v)[16],
                                              const uint16_t* win) const {
-        uint32_t k[16], w[16];
+        uint32_t ka[16], kb[16];
 #pragma unroll
-        for (int t = 0; t < 16; ++t) k[t] = ACT == 4 ? r.w[t] >> 16 : r.w[t] & 0xFFFFu;
-        win_lookup16<kWinTab>(win, tab, k, w);
-#pragma unroll
-        for (int t = 0; t < 16; ++t)
-            v[t] = act_from_word<ACT>(__uint_as_float(r.w[t] << 16),
-                                      __uint_as_float(r.w[t] & 0xFFFF0000u), w[t]);
+        for (int t = 0; t < 16; ++t) {
+            ka[t] = r.w[t] & 0xFFFFu;
+            kb[t] = r.w[t] >> 16;
+        }
+        act_windowed<ACT>(win, tab, ka, kb, v);
     }
     __device__ __forceinline__ void operator()(int64_t row, int col, float (&v)[16]) const {
         expand(fetch(row, col), v);
@@ -447,20 +497,23 @@ __global__ __launch_bounds__(1024) void rowquant_seg_kernel(Loader load, int8_t*
                                                            float* __restrict__ scale, int64_t M,
                                                            int K, int S, int R, int s_mul) {
     __shared__ uint32_t row_max[kMaxSegments];
-    // (one group per lane only: with two, the window's staging registers
-    // would push the paired dequant loaders past the register budget)
-    constexpr int WT = P == 1 ? LoaderWindow<Loader>::value : -1;
-    __shared__ __align__(16) uint16_t win[WT >= 0 ? kWinSize : 8];
-    // the window's 512 16-byte units, read before the row and without
-    // branches (a branch per read made the compiler wait for each one before
-    // the next): blocks have at least 192 threads, so three reads per thread
-    // at clamped unit indices cover it, and lanes that clamp to the same unit
-    // write the same value
-    uint4 wv[3];
-    if constexpr (WT >= 0) {
-#pragma unroll
-        for (int j = 0; j < 3; ++j)
-            wv[j] = *win_unit(load.tab, WT, min(int(threadIdx.x + j * blockDim.x), 511));
+    // (one group per lane only: with two, the paired dequant loaders would
+    // exceed the register budget)
+    constexpr int NW = P == 1 ? LoaderWins<Loader>::value : 0;
+    __shared__ __align__(16) uint16_t win[NW > 0 ? NW * kWinSize : 8];
+    // each window is 8 chunks of 64 16-byte units; a wave copies a chunk with
+    // one global -> LDS DMA (no registers staged), the block's waves taking
+    // the NW * 8 chunks in turn, before the row is read
+    if constexpr (NW > 0) {
+        const int lane = threadIdx.x & 63;
+        for (int c = threadIdx.x >> 6; c < NW * 8; c += blockDim.x >> 6) {
+            const int w = c >> 3, u = 64 * (c & 7);
+#if defined(__HIP_DEVICE_COMPILE__)
+            __builtin_amdgcn_global_load_lds(
+                win_unit(load.tab, Loader::win_tab(w), u + lane),
+                (__attribute__((address_space(3))) void*)(win + w * kWinSize + 8 * u), 16, 0, 0);
+#endif
+        }
     }
     const int seg = threadIdx.x >> 4;
     const int sl = threadIdx.x & 15;
@@ -475,10 +528,7 @@ __global__ __launch_bounds__(1024) void rowquant_seg_kernel(Loader load, int8_t*
     int col[P];
     typename Loader::Raw raw[P];
     float v[P][16];
-    // a window-capable loader without its window (two groups per lane)
-    // expands each group as soon as it is fetched, which keeps one group's
-    // table reads in flight at a time
-    constexpr bool EARLY = LoaderWindow<Loader>::value >= 0 && WT < 0;
+    constexpr bool EARLY = NW == 0 && LoaderEarly<Loader>::value;
     const XlaneSigns sgn = xlane_signs(sl);
 #pragma unroll
     for (int p = 0; p < P; ++p) {
@@ -492,15 +542,13 @@ __global__ __launch_bounds__(1024) void rowquant_seg_kernel(Loader load, int8_t*
         if constexpr (EARLY) lb.expand(raw[p], v[p]);
     }
     if (threadIdx.x < R) row_max[threadIdx.x] = 0u;
-    if constexpr (WT >= 0) {
-#pragma unroll
-        for (int j = 0; j < 3; ++j)
-            *reinterpret_cast<uint4*>(win + 8 * min(int(threadIdx.x + j * blockDim.x), 511)) = wv[j];
-    }
-    lds_barrier();                               // the zeros (and window) land before any use
+    // every wave's window DMAs have landed before the barrier (this waits for
+    // the row's reads too, which the next step needs anyway)
+    if constexpr (NW > 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    lds_barrier();                               // the zeros (and windows) land before any use
 #pragma unroll
     for (int p = 0; p < P; ++p) {
-        if constexpr (WT >= 0) lb.expand_w(raw[p], v[p], win);
+        if constexpr (NW > 0) lb.expand_w(raw[p], v[p], win);
         else if constexpr (!EARLY) lb.expand(raw[p], v[p]);
     }
     float dom = 1.0f;

@@ -281,7 +281,7 @@ WINDOW_EDGES = np.array([0x0000, 0x8000, 0x0001, 0x8001, 0x397F, 0xB97F, 0x3980,
                         np.uint16)
 
 
-@pytest.mark.parametrize("act", [1, 2, 4, 5])
+@pytest.mark.parametrize("act", [1, 2, 3, 4, 5])
 @pytest.mark.parametrize("m,k", [(7, 1280), (2, 20480)])
 def test_quantize_act_window_edges(dev, act, m, k):
     """Every lookup operand on a window edge or outside it, mixed into ordinary
@@ -300,7 +300,7 @@ def test_quantize_act_window_edges(dev, act, m, k):
     assert np.array_equal(npy(q), wq), mismatch(npy(q), wq)
 
 
-@pytest.mark.parametrize("act", [4, 5])
+@pytest.mark.parametrize("act", [3, 4, 5])
 @pytest.mark.parametrize("k", [1280, 20480])
 def test_dequant_act_quantize_window_edges(dev, act, k):
     """Dequantized values on the window edges: with both scales 2^-10 the
