@@ -280,7 +280,8 @@ int xpuint8_rms_rope_dequant_stream(const void *stream, const int32_t *acc, int6
 
 /* Host copy of an activation table (65536 bf16 entries indexed by the bf16
  * bit pattern of the input): 0 gelu_erf, 1 gelu_tanh, 2 silu, 3 situ's
- * tanh(bf16(x/4)), 4 sigmoid, 5 situ's tanh(bf16(x/25)).  No device needed.
+ * tanh(bf16(x/4)), 4 sigmoid, 5 situ's tanh(bf16(x/25)), 6 situ's gate
+ * factor bf16(table 3 * table 4).  No device needed.
  * No counterpart in the reference: it exposes the exact functions the fused
  * activations apply, for verification. */
 int xpuint8_activation_table(int32_t id, uint16_t *out);

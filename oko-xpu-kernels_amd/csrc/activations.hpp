@@ -23,7 +23,10 @@ enum ActTable : int {
     kTabSituTanhG = 3,  // bf16(tanh_fast(bf16(x / 4)))                     (151-152)
     kTabSigmoid = 4,    // bf16(1 / (1 + exp(-x)))                          (153-154)
     kTabSituTanhH = 5,  // bf16(tanh_fast(bf16(x / 25)))                    (155-156)
-    kNumTables = 6,
+    kTabSituGate = 6,   // bf16(table 3 * table 4): situ's gate factor, a
+                        // function of the gate alone (the product of two bf16
+                        // values is exact in fp32, then rounded once)
+    kNumTables = 7,
 };
 constexpr int kTabSize = 65536;
 

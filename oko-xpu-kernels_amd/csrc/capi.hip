@@ -600,7 +600,7 @@ int xpuint8_quantize_row_stream(const void* stream, const void* x, const float* 
 }
 
 int xpuint8_activation_table(int32_t id, uint16_t* out) {
-    if (id < 0 || id >= kNumTables) return fail(6, "table id must be 0..5");
+    if (id < 0 || id >= kNumTables) return fail(6, "table id must be 0..6");
     XPU_NONNULL(out);
     std::memcpy(out, host_activation_tables() + size_t(id) * kTabSize, sizeof(uint16_t) * kTabSize);
     return 0;

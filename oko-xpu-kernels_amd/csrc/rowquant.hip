@@ -35,23 +35,31 @@ __device__ __forceinline__ T* at32(T* base, int r, int64_t ld, int col) {
 }
 
 // ------------------------------------------------------- table windows in LDS
-// The activations read their tables through LDS copies of the tables'
-// windows (activations.hpp: inputs with |x| in [2^-12, 2^4), 4096 entries,
-// 8 KB per table), filled once per block; inputs outside a window read the
-// table in global memory behind a wave-uniform branch.  The same table words
-// either way.  One window for the one-lookup activations (gelu_tanh,
-// swiglu's SiLU, the erf GELU of GEGLU and GELU), three for situ (tanh(g/4)
-// and sigmoid(g) of the gate, tanh(h/25) of the hidden value).
+// The activations read their tables through LDS copies of a window of each
+// table: the entries of the bf16 inputs with |x| in [2^-20, 2^4) (exponent
+// field in [107, 131)), 3072 positive then 3072 negative, 12 KB per table,
+// filled once per block.  Inputs outside a window (zeros, |x| < 2^-20,
+// |x| >= 16, infinities, NaNs) take the tables in global memory behind a
+// wave-uniform branch; the same table words either way.  (The window reaches
+// below the GEMM epilogue's, whose LDS is scarcer: with [2^-12, 16) roughly
+// one wave in five of normal-distributed inputs had an input below it.)
+// One window for the one-lookup activations (gelu_tanh, swiglu's SiLU, the erf
+// GELU of GEGLU and GELU), two for situ: its gate factor bf16(tanh(g/4) *
+// sigmoid(g)), a function of the gate alone, and tanh(h/25) of the hidden value.
+constexpr int kRowWinLo = 107 << 7, kRowWinHalf = 24 * 128, kRowWinSize = 2 * kRowWinHalf;
+constexpr int kRowWinUnits = kRowWinSize / 8;       // 16-byte units per window
+static_assert(kRowWinHalf % (8 * 64) == 0, "a DMA chunk (64 units) stays in one sign half");
+
 template <int ACT>
 __host__ __device__ constexpr int win_count() {
-    return ACT == 3 ? 3 : (ACT == 1 || ACT == 2 || ACT == 4 || ACT == 5) ? 1 : 0;
+    return ACT == 3 ? 2 : (ACT == 1 || ACT == 2 || ACT == 4 || ACT == 5) ? 1 : 0;
 }
 template <int ACT>
 __host__ __device__ constexpr int win_table(int j) {
     return ACT == 1 ? kTabGeluTanh
          : ACT == 2 ? kTabSilu
          : (ACT == 4 || ACT == 5) ? kTabGeluErf
-         : j == 0 ? kTabSituTanhG : j == 1 ? kTabSigmoid : kTabSituTanhH;
+         : j == 0 ? kTabSituGate : kTabSituTanhH;
 }
 
 // Loaders that read through windows declare kWins > 0, win_tab(j) and expand_w().
@@ -67,22 +75,23 @@ template <class L>
 struct LoaderEarly<L, std::void_t<decltype(L::kExpandAtFetch)>>
     : std::integral_constant<bool, L::kExpandAtFetch> {};
 
-// 16-byte unit i < 512 of table T's window: units [0, 256) are table words
-// kWinLo + 8i (positive inputs), units [256, 512) the same for the negative
-// ones; LDS position p holds the word of win_bits(p).
+// 16-byte unit i < kRowWinUnits of table T's window: the first half of the
+// units are table words kRowWinLo + 8i (positive inputs), the second half the
+// same for the negative ones
 __device__ __forceinline__ const uint4* win_unit(const uint16_t* tab, int T, int i) {
-    const uint32_t word = (uint32_t(i >> 8) << 15) + uint32_t(kWinLo) + 8u * uint32_t(i & 255);
+    constexpr int H = kRowWinUnits / 2;
+    const uint32_t word = (i >= H ? 0x8000u : 0u) + uint32_t(kRowWinLo) + 8u * uint32_t(i >= H ? i - H : i);
     return reinterpret_cast<const uint4*>(tab + size_t(T) * kTabSize + word);
 }
 
 // Whether bf16 bits k lie outside the windows
 __device__ __forceinline__ bool win_outside(uint32_t k) {
-    return (k & 0x7FFFu) - uint32_t(kWinLo) >= uint32_t(kWinHalf);
+    return (k & 0x7FFFu) - uint32_t(kRowWinLo) >= uint32_t(kRowWinHalf);
 }
 // The window word of bf16 bits k (clamped into the window when outside)
 __device__ __forceinline__ uint32_t win_word(const uint16_t* win, uint32_t k) {
-    const uint32_t rel = (k & 0x7FFFu) - uint32_t(kWinLo);
-    return win[((k >> 15) << 11) + min(rel, uint32_t(kWinHalf - 1))];
+    const uint32_t rel = (k & 0x7FFFu) - uint32_t(kRowWinLo);
+    return win[((k & 0x8000u) ? uint32_t(kRowWinHalf) : 0u) + min(rel, uint32_t(kRowWinHalf - 1))];
 }
 
 // activate<ACT>(a, b) for 16 inputs given by their bf16 bits (ka: the first
@@ -90,13 +99,13 @@ __device__ __forceinline__ uint32_t win_word(const uint16_t* win, uint32_t k) {
 // read through the windows at win (win_count<ACT>() of them, back to back),
 // with a wave-uniform branch, rarely taken, for lookup operands outside the
 // windows.  One-lookup activations read all 16 words, then patch the missing
-// ones from the table in global memory.  Situ (three lookups) instead
+// ones from the table in global memory.  Situ (two lookups) instead
 // recomputes a missing output from the global tables, so that only inputs and
-// outputs are live across the branch: patching its 48 words kept every word
-// and key live and cost the kernel half its occupancy (47 against 106-124
-// VGPRs; 32.5 against 51 us for quantize_act at 4096 x 5120), while for the
-// one-lookup activations patching measured faster (dequant_act_quantize
-// GELU at 4096 x 5120: 26.9 against 30.4 us).
+// outputs are live across the branch: patching its words kept every word and
+// key live and cost the kernel half its occupancy (47 against 106-124 VGPRs;
+// 32.5 against 51 us for quantize_act at 4096 x 5120, then with three
+// tables), while for the one-lookup activations patching measured faster
+// (dequant_act_quantize GELU at 4096 x 5120: 26.9 against 30.4 us).
 template <int ACT>
 __device__ __forceinline__ void act_windowed(const uint16_t* win, const uint16_t* tab,
                                              const uint32_t (&ka)[16], const uint32_t (&kb)[16],
@@ -105,10 +114,11 @@ __device__ __forceinline__ void act_windowed(const uint16_t* win, const uint16_t
         bool miss = false;
 #pragma unroll
         for (int t = 0; t < 16; ++t) {
-            const uint32_t w[3] = {win_word(win, kb[t]), win_word(win + kWinSize, kb[t]),
-                                   win_word(win + 2 * kWinSize, ka[t])};
+            // bf16(bf16(tg * sg) * th) with the gate factor read whole
+            const float p = tab_float(win_word(win, kb[t]));
+            const float th = tab_float(win_word(win + kRowWinSize, ka[t]));
             miss = miss || win_outside(ka[t]) || win_outside(kb[t]);
-            v[t] = bf16_round(act_combine<3>(0.f, 0.f, w));
+            v[t] = bf16_round(p * th);
         }
         if (__builtin_amdgcn_ballot_w64(miss)) {
 #pragma unroll
@@ -500,18 +510,19 @@ __global__ __launch_bounds__(1024) void rowquant_seg_kernel(Loader load, int8_t*
     // (one group per lane only: with two, the paired dequant loaders would
     // exceed the register budget)
     constexpr int NW = P == 1 ? LoaderWins<Loader>::value : 0;
-    __shared__ __align__(16) uint16_t win[NW > 0 ? NW * kWinSize : 8];
-    // each window is 8 chunks of 64 16-byte units; a wave copies a chunk with
+    __shared__ __align__(16) uint16_t win[NW > 0 ? NW * kRowWinSize : 8];
+    // each window is CH chunks of 64 16-byte units; a wave copies a chunk with
     // one global -> LDS DMA (no registers staged), the block's waves taking
-    // the NW * 8 chunks in turn, before the row is read
+    // the NW * CH chunks in turn, before the row is read
     if constexpr (NW > 0) {
+        constexpr int CH = kRowWinUnits / 64;
         const int lane = threadIdx.x & 63;
-        for (int c = threadIdx.x >> 6; c < NW * 8; c += blockDim.x >> 6) {
-            const int w = c >> 3, u = 64 * (c & 7);
+        for (int c = threadIdx.x >> 6; c < NW * CH; c += blockDim.x >> 6) {
+            const int w = c / CH, u = 64 * (c - w * CH);
 #if defined(__HIP_DEVICE_COMPILE__)
             __builtin_amdgcn_global_load_lds(
                 win_unit(load.tab, Loader::win_tab(w), u + lane),
-                (__attribute__((address_space(3))) void*)(win + w * kWinSize + 8 * u), 16, 0, 0);
+                (__attribute__((address_space(3))) void*)(win + w * kRowWinSize + 8 * u), 16, 0, 0);
 #endif
         }
     }

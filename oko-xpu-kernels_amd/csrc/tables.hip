@@ -64,6 +64,9 @@ void build() {
         t[kTabSituTanhG * kTabSize + b] = to_bf16(tanh_fast(bf16r(x / 4.0f)));  // 151-152
         t[kTabSigmoid * kTabSize + b] = to_bf16(1.0f / (1.0f + exp_cr(-x)));    // 153-154
         t[kTabSituTanhH * kTabSize + b] = to_bf16(tanh_fast(bf16r(x / 25.0f))); // 155-156
+        t[kTabSituGate * kTabSize + b] =                                         // 151-154
+            to_bf16(f32(uint32_t(t[kTabSituTanhG * kTabSize + b]) << 16) *
+                    f32(uint32_t(t[kTabSigmoid * kTabSize + b]) << 16));
     }
 }
 

@@ -273,12 +273,13 @@ def test_quantize_act_exact(dev, act, m, k):
     assert np.array_equal(npy(q), wq), mismatch(npy(q), wq)
 
 
-# bf16 bit patterns on both sides of the table window the activation
-# quantizers read from LDS (|x| in [2^-12, 16)): zeros, denormals, the largest
-# value below 2^-12, 2^-12, the largest below 16, 16, and values far outside
-WINDOW_EDGES = np.array([0x0000, 0x8000, 0x0001, 0x8001, 0x397F, 0xB97F, 0x3980, 0xB980,
-                         0x417F, 0xC17F, 0x4180, 0xC180, 0x447A, 0xC47A, 0x3F80, 0xBF80],
-                        np.uint16)
+# bf16 bit patterns on both sides of the table windows the activation
+# quantizers read from LDS (|x| in [2^-20, 16)): zeros, denormals, the largest
+# value below 2^-20, 2^-20, values around 2^-12 (the GEMM epilogue's window
+# edge), the largest below 16, 16, and values far outside
+WINDOW_EDGES = np.array([0x0000, 0x8000, 0x0001, 0x8001, 0x357F, 0xB57F, 0x3580, 0xB580,
+                         0x397F, 0xB97F, 0x3980, 0xB980, 0x417F, 0xC17F, 0x4180, 0xC180,
+                         0x447A, 0xC47A, 0x3F80, 0xBF80], np.uint16)
 
 
 @pytest.mark.parametrize("act", [1, 2, 3, 4, 5])
@@ -293,7 +294,7 @@ def test_quantize_act_window_edges(dev, act, m, k):
     rng = np.random.default_rng(act * 7 + m)
     pick = rng.random((m, width)) < 0.3
     x[pick] = rng.choice(WINDOW_EDGES, int(pick.sum()))
-    x[0, :16] = WINDOW_EDGES                                 # one segment entirely on edges
+    x[0, :len(WINDOW_EDGES)] = WINDOW_EDGES                  # one lane's values all on edges
     q, s = int8.quantize_act(from_bits(x, dev), name)
     wq, ws = O.quantize_act(x, act)
     assert np.array_equal(npy(s), ws), mismatch(npy(s), ws)
@@ -304,18 +305,21 @@ def test_quantize_act_window_edges(dev, act, m, k):
 @pytest.mark.parametrize("k", [1280, 20480])
 def test_dequant_act_quantize_window_edges(dev, act, k):
     """Dequantized values on the window edges: with both scales 2^-10 the
-    value is bf16(acc * 2^-20), so acc = 256 gives 2^-12, 255 the largest
-    value below it, 2^24 gives 16 and 2^24 - 2^16 a value just below."""
+    value is bf16(acc * 2^-20), so acc = 1 gives 2^-20, 256 gives 2^-12, 255
+    the largest value below it, 2^24 gives 16 and 2^24 - 2^16 a value just
+    below; rows with x_scale 2^-14 take acc * 2^-24, where 15 falls below
+    2^-20 and 16 is on it."""
     m = 6
     n = 2 * k if act in O.PAIRED else k
     rng = np.random.default_rng(act + k)
-    edges = np.array([0, 1, -1, 255, -255, 256, -256, 2 ** 24 - 2 ** 16, -(2 ** 24 - 2 ** 16),
-                      2 ** 24, -(2 ** 24), 2 ** 28, -(2 ** 28), 2 ** 20, -(2 ** 20)], np.int64)
+    edges = np.array([0, 1, -1, 15, -15, 16, -16, 255, -255, 256, -256, 2 ** 24 - 2 ** 16,
+                      -(2 ** 24 - 2 ** 16), 2 ** 24, -(2 ** 24), 2 ** 28, -(2 ** 28), 2 ** 20,
+                      -(2 ** 20)], np.int64)
     acc = rng.integers(-2 ** 22, 2 ** 22, (m, n))
     pick = rng.random((m, n)) < 0.4
     acc[pick] = rng.choice(edges, int(pick.sum()))
     acc = acc.astype(np.int32)
-    xs = np.full(m, 2.0 ** -10, np.float32)
+    xs = np.where(np.arange(m) % 2 == 0, 2.0 ** -10, 2.0 ** -14).astype(np.float32)
     ws = np.full(n, 2.0 ** -10, np.float32)
     name = {v: kk for kk, v in int8.ACTIVATIONS.items()}[act]
     t = lambda a: torch.from_numpy(a).to(dev)

@@ -81,7 +81,7 @@ def _rc(lib, fn, *args):
     ("xpuint8_linear_stream", (Z, P, P, P, Z, 0, P, 4, 32, 512, P, 64), 2, "workspace_size"),
     ("xpuint8_prepare_weight_stream", (Z, P, P, P, 16, 300), 3, "256"),
     ("xpuint8_quantize_row_stream", (Z, P, Z, P, P, 4, 20), 2, "16"),
-    ("xpuint8_activation_table", (7, P), 6, "0..5"),
+    ("xpuint8_activation_table", (7 + 1, P), 6, "0..6"),
     ("xpuint8_linear_dw_stream", (Z, P, P, P, 64, 24, 32), 2, "16"),
     ("xpuint8_linear_dw_stream", (Z, P, Z, P, 64, 32, 32), 6, "null"),
 ])

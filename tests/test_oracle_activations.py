@@ -119,6 +119,22 @@ def test_library_tables_equal_the_oracle():
         assert np.array_equal(got[~nan_g], w[~nan_w]), i
 
 
+def test_library_situ_gate_table_is_situ_at_unit_hidden_factor():
+    """Table 6 is situ's gate factor: with a hidden value whose factor
+    tanh(bf16(h/25)) rounds to exactly 1, the oracle's whole situ activation
+    of (h, g) is that table's entry for g, over every bf16 gate value."""
+    lib = _lib()
+    h = np.full_like(X, np.float32(1000.0))
+    assert np.all(O.bf16_to_f32(O.f32_to_bf16(O.tanh_fast_f32(O.bf16_round(h / np.float32(25))))) == 1)
+    with np.errstate(all="ignore"):
+        want = O.f32_to_bf16(O.activate(3, h, X))
+    got = _table(lib, 6)
+    nan_g = (got & 0x7FFF) > 0x7F80
+    nan_w = (want & 0x7FFF) > 0x7F80
+    assert np.array_equal(nan_g, nan_w)
+    assert np.array_equal(got[~nan_g], want[~nan_w])
+
+
 def test_activate_composes_the_tables():
     """The paired activations are table lookups plus exact bf16 products."""
     rng = np.random.default_rng(0)
