@@ -36,17 +36,18 @@ __device__ __forceinline__ T* at32(T* base, int r, int64_t ld, int col) {
 
 // ------------------------------------------------------- table windows in LDS
 // The activations read their tables through LDS copies of a window of each
-// table: the entries of the bf16 inputs with |x| in [2^-20, 2^4) (exponent
-// field in [107, 131)), 3072 positive then 3072 negative, 12 KB per table,
+// table: the entries of the bf16 inputs with |x| in [2^-20, 2^8) (exponent
+// field in [107, 135)), 3584 positive then 3584 negative, 14 KB per table,
 // filled once per block.  Inputs outside a window (zeros, |x| < 2^-20,
-// |x| >= 16, infinities, NaNs) take the tables in global memory behind a
-// wave-uniform branch; the same table words either way.  (The window reaches
-// below the GEMM epilogue's, whose LDS is scarcer: with [2^-12, 16) roughly
-// one wave in five of normal-distributed inputs had an input below it.)
+// |x| >= 256, infinities, NaNs) take the tables in global memory behind a
+// wave-uniform branch; the same table words either way.  (The window is wider
+// than the GEMM epilogue's, whose LDS is scarcer: with [2^-12, 16), roughly
+// one wave in five of normal-distributed inputs had an input below it, and
+// nearly every wave of rows with 1% outlier channels x30 one above it.)
 // One window for the one-lookup activations (gelu_tanh, swiglu's SiLU, the erf
 // GELU of GEGLU and GELU), two for situ: its gate factor bf16(tanh(g/4) *
 // sigmoid(g)), a function of the gate alone, and tanh(h/25) of the hidden value.
-constexpr int kRowWinLo = 107 << 7, kRowWinHalf = 24 * 128, kRowWinSize = 2 * kRowWinHalf;
+constexpr int kRowWinLo = 107 << 7, kRowWinHalf = 28 * 128, kRowWinSize = 2 * kRowWinHalf;
 constexpr int kRowWinUnits = kRowWinSize / 8;       // 16-byte units per window
 static_assert(kRowWinHalf % (8 * 64) == 0, "a DMA chunk (64 units) stays in one sign half");
 

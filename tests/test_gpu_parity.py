@@ -274,12 +274,13 @@ def test_quantize_act_exact(dev, act, m, k):
 
 
 # bf16 bit patterns on both sides of the table windows the activation
-# quantizers read from LDS (|x| in [2^-20, 16)): zeros, denormals, the largest
-# value below 2^-20, 2^-20, values around 2^-12 (the GEMM epilogue's window
-# edge), the largest below 16, 16, and values far outside
+# quantizers read from LDS (|x| in [2^-20, 256)): zeros, denormals, the largest
+# value below 2^-20, 2^-20, values around 2^-12 and 16 (the GEMM epilogue's
+# window edges), the largest value below 256, 256, and values far outside
 WINDOW_EDGES = np.array([0x0000, 0x8000, 0x0001, 0x8001, 0x357F, 0xB57F, 0x3580, 0xB580,
                          0x397F, 0xB97F, 0x3980, 0xB980, 0x417F, 0xC17F, 0x4180, 0xC180,
-                         0x447A, 0xC47A, 0x3F80, 0xBF80], np.uint16)
+                         0x437F, 0xC37F, 0x4380, 0xC380, 0x447A, 0xC47A, 0x3F80, 0xBF80],
+                        np.uint16)
 
 
 @pytest.mark.parametrize("act", [1, 2, 3, 4, 5])
@@ -306,14 +307,15 @@ def test_quantize_act_window_edges(dev, act, m, k):
 def test_dequant_act_quantize_window_edges(dev, act, k):
     """Dequantized values on the window edges: with both scales 2^-10 the
     value is bf16(acc * 2^-20), so acc = 1 gives 2^-20, 256 gives 2^-12, 255
-    the largest value below it, 2^24 gives 16 and 2^24 - 2^16 a value just
-    below; rows with x_scale 2^-14 take acc * 2^-24, where 15 falls below
-    2^-20 and 16 is on it."""
+    the largest value below it, 2^24 gives 16, 2^28 gives 256 and 2^28 - 2^20
+    the largest value below it; rows with x_scale 2^-14 take acc * 2^-24,
+    where 15 falls below 2^-20 and 16 is on it."""
     m = 6
     n = 2 * k if act in O.PAIRED else k
     rng = np.random.default_rng(act + k)
     edges = np.array([0, 1, -1, 15, -15, 16, -16, 255, -255, 256, -256, 2 ** 24 - 2 ** 16,
-                      -(2 ** 24 - 2 ** 16), 2 ** 24, -(2 ** 24), 2 ** 28, -(2 ** 28), 2 ** 20,
+                      -(2 ** 24 - 2 ** 16), 2 ** 24, -(2 ** 24), 2 ** 28 - 2 ** 20,
+                      -(2 ** 28 - 2 ** 20), 2 ** 28, -(2 ** 28), 2 ** 30, -(2 ** 30), 2 ** 20,
                       -(2 ** 20)], np.int64)
     acc = rng.integers(-2 ** 22, 2 ** 22, (m, n))
     pick = rng.random((m, n)) < 0.4
