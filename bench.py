@@ -351,6 +351,10 @@ def main():
     ap.add_argument("--only-gemm", action="store_true",
                     help="the config-3 GEMM alone, cold, and nothing else (for profiling: its "
                          "launches are then the only ones of that kernel in the run)")
+    ap.add_argument("--only-side", action="store_true",
+                    help="only the entry points beside the path (linear_acc, residual, dequant, "
+                         "dequant_slice, quantize_act, dequant_act_quantize, dequant_weight, "
+                         "int8_linear step), for profiling")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run a plain copy kernel (torch neg over 256 MiB in and out, "
                          "exactly 256 MiB) so counter runs can scale FETCH_SIZE/WRITE_SIZE")
@@ -408,6 +412,11 @@ def main():
     x = activation(torch, M, Kd).to(dev)
     w8, ws = int8.prepare_weight(weight(torch, N, Kd).to(dev))
     bias = weight(torch, 1, N, seed=2, std=0.01)[0].to(dev)
+    if args.only_side:
+        measure_side_rows(torch, int8, lib, L, st, dev, K, W, SET, extra, hbm_line, dev_gen,
+                          dev_act, dev_weight, x, w8, ws, bias)
+        print(json.dumps({"only_side": True, "steps": K, "warmup": W, "extra": extra}), flush=True)
+        return
     # cold: distinct (x, w8, ws, bias) per call, set 0 the recipe's own inputs
     n3 = n_sets(2 * M * Kd + N * Kd + 6 * N)
     sets3 = [(x, w8, ws, bias)]
