@@ -200,11 +200,20 @@ int dx_chain(hipStream_t st, const void* dy, const float* w_scale, const int8_t*
 
 // The workspace of xpuint8_linear_stream: x quantized, q int8 (row-major, or
 // in the MFMA block layout when the split-K kernel reads it), then its row
-// scales fp32 [M], on a 256-byte boundary.
+// scales fp32 [M], on a 256-byte boundary; for a product split across blocks
+// in K (gemm_slices), then the slices' int32 partial products, also on a
+// 256-byte boundary.
 size_t linear_work_q_bytes(int64_t M, int64_t K) {
     return (size_t(std::max(M * K, tiled_bytes(M, K))) + 255) & ~size_t(255);
 }
-size_t linear_work_bytes(int64_t M, int64_t K) { return linear_work_q_bytes(M, K) + 4 * size_t(M); }
+size_t linear_work_part_offset(int64_t M, int64_t K) {
+    return (linear_work_q_bytes(M, K) + 4 * size_t(M) + 255) & ~size_t(255);
+}
+size_t linear_work_bytes(int64_t M, int64_t N, int64_t K) {
+    const int nsl = gemm_slices(int(M), int(N), int(K));
+    if (nsl > 0) return linear_work_part_offset(M, K) + size_t(nsl) * size_t(M) * size_t(N) * 4;
+    return linear_work_q_bytes(M, K) + 4 * size_t(M);
+}
 
 int act_ok(int32_t act) {
     if (act < 1 || act > 5)
@@ -412,7 +421,7 @@ int xpuint8_linear_gemm_stream(const void* stream, const int8_t* xq, const float
 
 int64_t xpuint8_linear_workspace_size(int64_t M, int64_t N, int64_t K) {
     if (check_rows(M, K) != 0 || check_epilogue(M, N) != 0 || check_gemm(M, N, K) != 0) return -1;
-    return int64_t(linear_work_bytes(M, K));
+    return int64_t(linear_work_bytes(M, N, K));
 }
 
 int xpuint8_linear_stream(const void* stream, const void* x, const int8_t* w8,
@@ -424,7 +433,7 @@ int xpuint8_linear_stream(const void* stream, const void* x, const int8_t* w8,
     XPU_NONNULL(x); XPU_NONNULL(w8); XPU_NONNULL(w_scale); XPU_NONNULL(out); XPU_NONNULL(work);
     XPU_ALIGNED_OPT(bias);
     if (bias_bf16 != 0 && bias_bf16 != 1) return fail(2, "bias_bf16 must be 0 or 1");
-    if (work_bytes < int64_t(linear_work_bytes(M, K)))
+    if (work_bytes < int64_t(linear_work_bytes(M, N, K)))
         return fail(2, "work must hold xpuint8_linear_workspace_size(M, N, K) bytes");
     XPU_TRY(ensure_device());
     hipStream_t st = as_stream(stream);
@@ -432,6 +441,18 @@ int xpuint8_linear_stream(const void* stream, const void* x, const int8_t* w8,
     float* xs = reinterpret_cast<float*>(static_cast<char*>(work) + linear_work_q_bytes(M, K));
     const float* b32 = bias_bf16 ? nullptr : static_cast<const float*>(bias);
     const uint16_t* b16 = bias_bf16 ? static_cast<const uint16_t*>(bias) : nullptr;
+    // too few output tiles for the chip: the product split in K across
+    // blocks, each slice's int32 partial sums in the workspace, then one pass
+    // that adds them and applies the dequant
+    if (const int nsl = gemm_slices(int(M), int(N), int(K))) {
+        int32_t* part = reinterpret_cast<int32_t*>(static_cast<char*>(work) +
+                                                   linear_work_part_offset(M, K));
+        XPU_TRY(launched(convrot_quantize(st, x, q, xs, M, int(K), 0), "linear (quantize)"));
+        XPU_TRY(launched(gemm_i32_slices(st, q, K, w8, K, part, int(M), int(N), int(K), nsl),
+                         "linear (gemm)"));
+        return launched(dequant_slices(st, part, N, nsl, M * N, out, xs, w_scale, b32, b16, M, N),
+                        "linear (dequant)");
+    }
     // narrow outputs with a long K take the split-K kernel, which reads q in
     // the MFMA block layout; the other shapes a row-major q
     if (splitk_applies(int(M), int(N), int(K)) && rowquant_can_tile(int(K))) {

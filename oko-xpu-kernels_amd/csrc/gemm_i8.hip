@@ -67,6 +67,26 @@ struct EpiI32 {
     }
 };
 
+// The int32 partial products of one K slice of a split across blocks (the
+// split-K kernel launched with gridDim.y slices, slice blockIdx.y): slice s's
+// [M, N] sums at c + s * slice_stride.  Integer sums are exact, so adding the
+// slices in any order gives the full product bit for bit.
+struct EpiSliceI32 {
+    static constexpr bool kStaged = false;
+    static constexpr bool kPaired = false;
+    static constexpr bool kSlice = true;
+    int32_t* c;
+    int64_t ldc;
+    int64_t slice_stride;
+    __device__ __forceinline__ void operator()(int m, int n, const v4i& v) const {
+        *reinterpret_cast<v4i*>(c + int64_t(blockIdx.y) * slice_stride + int64_t(m) * ldc + n) = v;
+    }
+};
+template <class E, class = void>
+struct IsSliceEpi : std::false_type {};
+template <class E>
+struct IsSliceEpi<E, std::void_t<decltype(E::kSlice)>> : std::integral_constant<bool, E::kSlice> {};
+
 // bf16(float(acc) * (ws[n] * xs[m]) + bias[n]); ws == nullptr is a unit column
 // scale (1.0f * xs[m] == xs[m]), bias may be null.
 struct EpiDequant {
@@ -1159,8 +1179,16 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_splitk_kernel(
     constexpr int XB = BM / 16, WB = BN / 16, NB = XB + WB;     // 18 blocks of 1 KB per stage
     constexpr int PER = (NB + 3) / 4, REM = NB % 4;
     constexpr int STAGE_BYTES = NB * 1024, RING = S * STAGE_BYTES;
-    static_assert(!Epi::kPaired && Epi::kStaged, "dequant epilogues only");
+    constexpr bool SLICE = IsSliceEpi<Epi>::value;
+    static_assert(!Epi::kPaired && (Epi::kStaged || SLICE), "dequant or slice epilogues only");
+    static_assert(!SLICE || (!XT && !WNN), "K slices of row-major operands");
     static_assert(2 * RING >= 4 * TN * (TM / 2) * 1024, "half of a team's accumulators fit");
+    // K slice blockIdx.y of a split across blocks: K is the slice's length and
+    // the operands' rows keep their full strides
+    if constexpr (SLICE) {
+        X += int64_t(blockIdx.y) * K;
+        W += int64_t(blockIdx.y) * K;
+    }
     static_assert(S >= 3 && S <= 4, "three or four stages");
     __shared__ __attribute__((aligned(1024))) int8_t smem[2 * RING];
 
@@ -1383,9 +1411,24 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_splitk_kernel(
         }
     }
     __syncthreads();
-    if (team == 0)
+    if constexpr (SLICE) {
+        // lane l of block (a, b): row m0 + wm*WM + 16b + l%16, columns n .. n+3
+        // with n = n0 + wn*WN + 16a + 4*(l/16)
+        if (team == 0) {
+#pragma unroll
+            for (int b = 0; b < TM; ++b) {
+                const int m = m0 + wm * WM + 16 * b + (lane & 15);
+#pragma unroll
+                for (int a = 0; a < TN; ++a) {
+                    const int n = n0 + wn * WN + 16 * a + 4 * (lane >> 4);
+                    if (m < M && n < N) epi(m, n, acc[a][b]);
+                }
+            }
+        }
+    } else if (team == 0) {
         staged_epilogue<TM, TN, WN, Epi>(epi, acc, smem + wt * (32 * 256), m0 + wm * WM,
                                          n0 + wn * WN, M, N, lane);
+    }
 }
 
 template <bool WNN = false, class Epi, bool XT = false>
@@ -1578,14 +1621,20 @@ hipError_t launch_gemm(hipStream_t st, const int8_t* X, int64_t ldx, const int8_
 // (Measured at M = 4096, cold: 2 slots per block were fastest or within 2% at
 // N = 1280, 5120 and 10240; 1 slot was 5-18% slower there, up to 4 slots 16%
 // slower at N = 5120; 1 slot was 1 us faster at N = 3072.)
+// With nsl > 1 the accumulator is the sum of nsl int32 slices sl_stride
+// apart (the partial products of a K split across blocks): integer sums, so
+// the dequant sees the exact full product.  The bias is fp32 (bias), bf16
+// (bias16, widened exactly) or absent.
 constexpr int DQ_U = 2, DQ_COLS = 256 * 4 * DQ_U;
 
 __global__ __launch_bounds__(256) void dequant_kernel(const int32_t* __restrict__ acc,
                                                      int64_t acc_ld, uint16_t* __restrict__ out,
                                                      const float* __restrict__ xs,
                                                      const float* __restrict__ ws,
-                                                     const float* __restrict__ bias, int64_t M,
-                                                     int64_t N) {
+                                                     const float* __restrict__ bias,
+                                                     const uint16_t* __restrict__ bias16,
+                                                     int64_t M, int64_t N, int nsl,
+                                                     int64_t sl_stride) {
     const int64_t chunks = (N + DQ_COLS - 1) / DQ_COLS, tasks = M * chunks;
     for (int64_t bt = blockIdx.x; bt < tasks; bt += gridDim.x) {
         const int64_t m = bt / chunks;
@@ -1597,6 +1646,12 @@ __global__ __launch_bounds__(256) void dequant_kernel(const int32_t* __restrict_
 #pragma unroll
         for (int u = 0; u < DQ_U; ++u)
             if (c0 + 1024 * u < N) a[u] = load16_i(pa + c0 + 1024 * u);
+#pragma unroll 2
+        for (int sl = 1; sl < nsl; ++sl) {
+#pragma unroll
+            for (int u = 0; u < DQ_U; ++u)
+                if (c0 + 1024 * u < N) a[u] += load16_i(pa + sl * sl_stride + c0 + 1024 * u);
+        }
 #pragma unroll
         for (int u = 0; u < DQ_U; ++u) {
             const int64_t c = c0 + 1024 * u;
@@ -1607,6 +1662,10 @@ __global__ __launch_bounds__(256) void dequant_kernel(const int32_t* __restrict_
             if (bias) {
                 const float4 b = *reinterpret_cast<const float4*>(bias + c);
                 r0 = r0 + b.x; r1 = r1 + b.y; r2 = r2 + b.z; r3 = r3 + b.w;
+            } else if (bias16) {
+                const uint2 u2 = *reinterpret_cast<const uint2*>(bias16 + c);
+                r0 = r0 + bf16lo(u2.x); r1 = r1 + bf16hi(u2.x);
+                r2 = r2 + bf16lo(u2.y); r3 = r3 + bf16hi(u2.y);
             }
             *reinterpret_cast<uint2*>(po + c) = make_uint2(cvt_pk_bf16(r0, r1), cvt_pk_bf16(r2, r3));
         }
@@ -1684,7 +1743,34 @@ bool splitk_applies(int M, int N, int K) {
     if (M <= 64) return false;
     const int64_t tm = (M + 255) / 256, tn = (N + 159) / 160;
     const int64_t tiles_split = int64_t((M + 127) / 128) * ((N + 159) / 160);
-    return tm * tn < 192 && K >= 2048 && tiles_split >= 128;
+    return tm * tn < 192 && K >= 1024 && tiles_split >= 128;
+}
+
+// K slices for a split of the product across blocks, when the output has
+// fewer 128 x 160 tiles than the split-K kernel takes (128): the fewest
+// power-of-two slices that give at least 192 blocks, each slice at least 1024
+// long and a whole number of 64-byte steps; 0 when no split applies (M <= 64,
+// 128 tiles or more, or K too short).  (With 128-191 tiles the split-K kernel
+// alone measured faster: 28.8 against 41.2 us at M=2100, N=1296, K=2304, and
+// 1 us at M=2048 and 4096 with 128 tiles.)
+int gemm_slices(int M, int N, int K) {
+    if (M <= 64 || K % 64 != 0) return 0;
+    const int64_t tiles = int64_t((M + 127) / 128) * ((N + 159) / 160);
+    if (tiles >= 128) return 0;
+    int s = 1;
+    while (tiles * s < 192 && (K / 64) % (2 * s) == 0 && K / (2 * s) >= 1024) s *= 2;
+    return s > 1 ? s : 0;
+}
+
+// The int32 partial products of nsl K slices, slice s at part + s * M * N
+// (row stride N): the split-K kernel over a (tiles, nsl) grid.
+hipError_t gemm_i32_slices(hipStream_t st, const int8_t* X, int64_t ldx, const int8_t* W,
+                           int64_t ldw, int32_t* part, int M, int N, int K, int nsl) {
+    const int tm = (M + 127) / 128, tn = (N + 159) / 160;
+    hipLaunchKernelGGL((gemm_i8_splitk_kernel<4, false, false, EpiSliceI32, false>),
+                       dim3(unsigned(tm * tn), unsigned(nsl)), dim3(512), 0, st, X, ldx, W, ldw,
+                       M, N, K / nsl, tm, tn, EpiSliceI32{part, int64_t(N), int64_t(M) * N});
+    return hipGetLastError();
 }
 
 // B[k, n] as stored (the NN product); the 32-bit DMA offsets of the weight
@@ -1760,11 +1846,17 @@ hipError_t gemm_act(hipStream_t st, const int8_t* A, int64_t lda, const int8_t* 
 hipError_t dequant_epilogue(hipStream_t st, const int32_t* acc, int64_t acc_ld, void* out,
                             const float* xs, const float* ws, const float* bias, int64_t M,
                             int64_t N) {
+    return dequant_slices(st, acc, acc_ld, 1, 0, out, xs, ws, bias, nullptr, M, N);
+}
+
+hipError_t dequant_slices(hipStream_t st, const int32_t* acc, int64_t acc_ld, int nsl,
+                          int64_t sl_stride, void* out, const float* xs, const float* ws,
+                          const float* bias, const uint16_t* bias16, int64_t M, int64_t N) {
     int64_t blocks = M * ((N + DQ_COLS - 1) / DQ_COLS);
     if (blocks > (int64_t(1) << 20)) blocks = int64_t(1) << 20;
     if (blocks == 0) return hipSuccess;
     hipLaunchKernelGGL(dequant_kernel, dim3(unsigned(blocks)), dim3(256), 0, st, acc, acc_ld,
-                       static_cast<uint16_t*>(out), xs, ws, bias, M, N);
+                       static_cast<uint16_t*>(out), xs, ws, bias, bias16, M, N, nsl, sl_stride);
     return hipGetLastError();
 }
 

@@ -78,6 +78,16 @@ hipError_t gemm_act(hipStream_t st, const int8_t* A, int64_t lda, const int8_t* 
 hipError_t dequant_epilogue(hipStream_t st, const int32_t* acc, int64_t acc_ld, void* out,
                             const float* xs, const float* ws, const float* bias, int64_t M,
                             int64_t N);
+// the same on the sum of nsl int32 slices sl_stride apart, with an fp32 (bias)
+// or bf16 (bias16) bias or neither
+hipError_t dequant_slices(hipStream_t st, const int32_t* acc, int64_t acc_ld, int nsl,
+                          int64_t sl_stride, void* out, const float* xs, const float* ws,
+                          const float* bias, const uint16_t* bias16, int64_t M, int64_t N);
+// K slices of a split of the product across blocks (0: none applies), and the
+// slices' int32 partial products, slice s at part + s * M * N (row stride N)
+int gemm_slices(int M, int N, int K);
+hipError_t gemm_i32_slices(hipStream_t st, const int8_t* X, int64_t ldx, const int8_t* W,
+                           int64_t ldw, int32_t* part, int M, int N, int K, int nsl);
 hipError_t transpose_i8(hipStream_t st, const int8_t* in, int8_t* out, int64_t R, int64_t C);
 
 // gemm_bf16.hip: dw[n, k] = sum_m dy[m, n] * x[m, k] (bf16, fp32 accumulate)

@@ -515,18 +515,18 @@ __global__ __launch_bounds__(1024) void rowquant_seg_kernel(Loader load, int8_t*
     // each window is CH chunks of 64 16-byte units; a wave copies a chunk with
     // one global -> LDS DMA (no registers staged), the block's waves taking
     // the NW * CH chunks in turn, before the row is read
+#if defined(__HIP_DEVICE_COMPILE__)
     if constexpr (NW > 0) {
         constexpr int CH = kRowWinUnits / 64;
         const int lane = threadIdx.x & 63;
         for (int c = threadIdx.x >> 6; c < NW * CH; c += blockDim.x >> 6) {
             const int w = c / CH, u = 64 * (c - w * CH);
-#if defined(__HIP_DEVICE_COMPILE__)
             __builtin_amdgcn_global_load_lds(
                 win_unit(load.tab, Loader::win_tab(w), u + lane),
                 (__attribute__((address_space(3))) void*)(win + w * kRowWinSize + 8 * u), 16, 0, 0);
-#endif
         }
     }
+#endif
     const int seg = threadIdx.x >> 4;
     const int sl = threadIdx.x & 15;
     const int r = int(__umul24(seg, s_mul)) >> 12;   // seg / S (exact for seg, S <= 64)

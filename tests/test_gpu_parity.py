@@ -536,6 +536,25 @@ def test_linear_dispatch_sweep(dev, m, n, k):
     assert np.array_equal(bits(y), want), mismatch(bits(y), want)
 
 
+# Too few 128 x 160 output tiles for the chip: the product split in K across
+# blocks (4, 4, 4 and 16 slices), the int32 partial sums added by the dequant
+# pass; ragged row and column tiles; with a bf16 bias, an fp32 bias and none
+@pytest.mark.parametrize("m,n,k", [(1024, 1280, 5120), (2048, 640, 5120), (1000, 1296, 4096),
+                                   (200, 160, 16384)])
+def test_linear_k_slices_exact(dev, m, n, k):
+    x = activation(m, k, seed=m + 2 * k, n_out=4, mult=25.0)
+    w = weight(n, k, seed=n + 3)
+    bias = weight(1, n, seed=n + k + 1, std=0.01)[0]
+    w8, ws = int8.prepare_weight(w.to(dev))
+    acc, xs = O.linear_acc(bits(x), npy(w8))              # the oracle's linear, shared
+    for b in (bias.to(dev), bias.float().to(dev), None):
+        y = int8.linear(x.to(dev), w8, ws, b)
+        bref = None if b is None else O.bf16_to_f32(bits(bias))
+        want = O.dequant(acc, xs, npy(ws), bref)
+        assert np.array_equal(bits(y), want), (None if b is None else b.dtype,
+                                               mismatch(bits(y), want))
+
+
 def test_linear_shapes_and_dtypes(dev):
     x = activation(2 * 3 * 5, 512, seed=3).reshape(2, 3, 5, 512)
     w = weight(48, 512)

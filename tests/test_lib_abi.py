@@ -136,12 +136,35 @@ def test_dx_workspace_size(lib):
     assert lib.xpuint8_linear_dx_int8_workspace_size(4, 32, 300) == -1
 
 
+def k_slices(m, n, k):
+    """The K slices of a product split across blocks: when the 128 x 160
+    output tiles number below 128, the fewest power-of-two slices giving at
+    least 192 blocks, each slice a whole number of 64-byte steps and at least
+    1024 long; 0 when none applies (m <= 64 included)."""
+    if m <= 64 or k % 64:
+        return 0
+    tiles = -(-m // 128) * -(-n // 160)
+    if tiles >= 128:
+        return 0
+    s = 1
+    while tiles * s < 192 and (k // 64) % (2 * s) == 0 and k // (2 * s) >= 1024:
+        s *= 2
+    return s if s > 1 else 0
+
+
 def test_linear_workspace_size(lib):
     """The linear's workspace: the quantized activation (row-major or in the
     block layout, whichever is larger) rounded up to 256 bytes, then its fp32
-    row scales; -1 for a shape the entry point rejects."""
-    for m, n, k in [(4096, 1280, 5120), (4096, 10240, 1280), (3, 16, 256), (2100, 1296, 2304)]:
+    row scales; for a product split in K across blocks, then (from a 256-byte
+    boundary) the slices' int32 [M, N] partial products; -1 for a shape the
+    entry point rejects."""
+    shapes = [(4096, 1280, 5120), (4096, 10240, 1280), (3, 16, 256), (2100, 1296, 2304),
+              (1024, 1280, 5120), (2048, 640, 5120), (1000, 1296, 4096), (1024, 1280, 1280)]
+    assert [k_slices(*s) for s in shapes] == [0, 0, 0, 0, 4, 4, 4, 0]
+    for m, n, k in shapes:
         want = up256(max(m * k, tiled(m, k))) + 4 * m
+        if k_slices(m, n, k):
+            want = up256(want) + k_slices(m, n, k) * m * n * 4
         assert lib.xpuint8_linear_workspace_size(m, n, k) == want, (m, n, k)
     assert lib.xpuint8_linear_workspace_size(4, 32, 300) == -1
     assert lib.xpuint8_linear_workspace_size(4, 24, 512) == -1
