@@ -197,10 +197,11 @@ def measure_side_rows(torch, int8, lib, L, st, dev, K, W, SET, extra, hbm_line, 
                       dev_act, dev_weight, x, w8, ws, bias):
     """The entry points beside the config-3 step, each at the shape its caller
     uses: the int32 GEMM of ``linear_acc``, ``linear``'s fused residual, the
-    standalone epilogues, the activation quantizers, ``dequant_weight`` and an
-    ``int8_linear`` training step (forward + backward) at config 5.  The
+    standalone epilogues, the activation quantizers, ``dequant_weight``, the
+    reference's SDXL shape table (``linear`` against torch's bf16 linear) and
+    an ``int8_linear`` training step (forward + backward) at config 5.  The
     HBM-bound ones are timed cold (rotating buffer sets) and warm; the GEMMs
-    warm, on the config-3 operands."""
+    of config 3 warm, on its operands; the SDXL shapes cold."""
     M, Kd, N = 4096, 1280, 10240
     ops3 = 2.0 * M * N * Kd
     xq, xs = int8.quantize(x)
@@ -317,6 +318,35 @@ def measure_side_rows(torch, int8, lib, L, st, dev, K, W, SET, extra, hbm_line, 
     extra["dequant_weight_n10240_k1280"] = hbm_line(
         bytes_dw, timed(torch, dqw, K, W, SET), timed(torch, lambda i: dqw(0), K, W, SET), sets=ndw)
     del sw, ow
+
+    # the reference's SDXL shape table (docs/sdxl.md:40-47, batch 1 at
+    # 1024x1024, M = 4096 tokens): int8.linear end to end and torch's bf16
+    # F.linear on the same (cold) inputs, with the reference's published
+    # device time on its GPU (Arc B580) beside them
+    sdxl = {}
+    for Ks, Ns, ref_ms in ((5120, 1280, 0.647), (2048, 1280, 0.366), (1280, 1280, 0.289),
+                           (1280, 10240, 1.980)):
+        Ms = 4096
+        nss = n_sets(2 * Ms * Ks + 3 * Ns * Ks + 2 * Ms * Ns)
+        ss = []
+        for i in range(nss):
+            wb = dev_weight(Ns, Ks, 1600 + i)
+            ss.append((dev_act(Ms, Ks, 1700 + i), *int8.prepare_weight(wb),
+                       dev_weight(1, Ns, 1800 + i, 0.01)[0], wb))
+        t_i8 = timed(torch, lambda i: int8.linear(*ss[i % nss][:4]), K, W, SET)
+        t_bf = timed(torch, lambda i: torch.nn.functional.linear(ss[i % nss][0], ss[i % nss][4],
+                                                                 ss[i % nss][3]), K, W, SET)
+        sdxl[f"K{Ks}_N{Ns}_M{Ms}"] = {
+            "int8_linear_ms_cold": round(t_i8, 5),
+            "int8_TOP/s": round(2.0 * Ms * Ns * Ks / (t_i8 * 1e-3) / 1e12, 1),
+            "torch_bf16_linear_ms_cold": round(t_bf, 5),
+            "int8_over_bf16": round(t_i8 / t_bf, 3),
+            "reference_b580_int8_ms": ref_ms}
+        del ss
+    extra["sdxl_shapes"] = sdxl
+    log("[bench] SDXL shapes: " + ", ".join(f"{k} {v['int8_linear_ms_cold'] * 1e3:.1f} us "
+                                            f"(bf16 {v['torch_bf16_linear_ms_cold'] * 1e3:.1f})"
+                                            for k, v in sdxl.items()))
 
     # int8_linear training step at config 5 shapes: forward, then backward
     # (dx, dbias; the weight is frozen int8), for both backward modes
