@@ -437,6 +437,12 @@ __global__ __launch_bounds__(WGM * WGN * 64) void gemm_i8_kernel(
     constexpr int PER_WAVE = (NB + NWAVES - 1) / NWAVES;       // DMA instructions per wave
     constexpr int STAGE_BYTES = NB * 1024;
     __shared__ __attribute__((aligned(1024))) int8_t smem[STAGES * STAGE_BYTES];
+    // K slice blockIdx.y of a split across blocks (EpiSliceI32): K is the
+    // slice's length, the operands' rows keep their full strides
+    if constexpr (IsSliceEpi<Epi>::value) {
+        X += int64_t(blockIdx.y) * K;
+        W += int64_t(blockIdx.y) * K;
+    }
 
     const int tiles = tiles_m * tiles_n;
     int t = blockIdx.x;
@@ -1746,6 +1752,10 @@ bool splitk_applies(int M, int N, int K) {
     return tm * tn < 192 && K >= 1024 && tiles_split >= 128;
 }
 
+// Rows few enough (two 128-row tiles at most) that the slices take the
+// 128 x 128 kernel, whose narrower tiles give more blocks per slice
+static bool slices_small_tiles(int M) { return M <= 256; }
+
 // K slices for a split of the product across blocks, when the output has
 // fewer 128 x 160 tiles than the split-K kernel takes (128): the fewest
 // power-of-two slices that give at least 192 blocks, each slice at least 1024
@@ -1757,6 +1767,13 @@ int gemm_slices(int M, int N, int K) {
     if (M <= 64 || K % 64 != 0) return 0;
     const int64_t tiles = int64_t((M + 127) / 128) * ((N + 159) / 160);
     if (tiles >= 128) return 0;
+    if (slices_small_tiles(M)) {
+        // the 128 x 128 kernel: its tiles, slices down to 512 long
+        const int64_t t128 = int64_t((M + 127) / 128) * ((N + 127) / 128);
+        int s = 1;
+        while (t128 * s < 192 && (K / 64) % (2 * s) == 0 && K / (2 * s) >= 512) s *= 2;
+        return s > 1 ? s : 0;
+    }
     int s = 1;
     while (tiles * s < 192 && (K / 64) % (2 * s) == 0 && K / (2 * s) >= 1024) s *= 2;
     return s > 1 ? s : 0;
@@ -1766,6 +1783,14 @@ int gemm_slices(int M, int N, int K) {
 // (row stride N): the split-K kernel over a (tiles, nsl) grid.
 hipError_t gemm_i32_slices(hipStream_t st, const int8_t* X, int64_t ldx, const int8_t* W,
                            int64_t ldw, int32_t* part, int M, int N, int K, int nsl) {
+    const EpiSliceI32 epi{part, int64_t(N), int64_t(M) * N};
+    if (slices_small_tiles(M)) {
+        const int tm = (M + 127) / 128, tn = (N + 127) / 128;
+        hipLaunchKernelGGL((gemm_i8_kernel<128, 128, 2, 2, 4, EpiSliceI32>),
+                           dim3(unsigned(tm * tn), unsigned(nsl)), dim3(256), 0, st, X, ldx, W,
+                           ldw, M, N, K / nsl, tm, tn, epi);
+        return hipGetLastError();
+    }
     const int tm = (M + 127) / 128, tn = (N + 159) / 160;
     hipLaunchKernelGGL((gemm_i8_splitk_kernel<4, false, false, EpiSliceI32, false>),
                        dim3(unsigned(tm * tn), unsigned(nsl)), dim3(512), 0, st, X, ldx, W, ldw,

@@ -537,10 +537,12 @@ def test_linear_dispatch_sweep(dev, m, n, k):
 
 
 # Too few 128 x 160 output tiles for the chip: the product split in K across
-# blocks (4, 4, 4 and 16 slices), the int32 partial sums added by the dequant
-# pass; ragged row and column tiles; with a bf16 bias, an fp32 bias and none
+# blocks (4, 4 and 4 slices through the split-K kernel; 32, 8 and 2 through
+# the 128 x 128 kernel for M <= 256), the int32 partial sums added by the
+# dequant pass; ragged row and column tiles; with a bf16 bias, an fp32 bias
+# and none
 @pytest.mark.parametrize("m,n,k", [(1024, 1280, 5120), (2048, 640, 5120), (1000, 1296, 4096),
-                                   (200, 160, 16384)])
+                                   (200, 160, 16384), (128, 4096, 4096), (65, 4080, 1024)])
 def test_linear_k_slices_exact(dev, m, n, k):
     x = activation(m, k, seed=m + 2 * k, n_out=4, mult=25.0)
     w = weight(n, k, seed=n + 3)

@@ -140,14 +140,18 @@ def k_slices(m, n, k):
     """The K slices of a product split across blocks: when the 128 x 160
     output tiles number below 128, the fewest power-of-two slices giving at
     least 192 blocks, each slice a whole number of 64-byte steps and at least
-    1024 long; 0 when none applies (m <= 64 included)."""
+    1024 long -- for m <= 256 counted in 128 x 128 tiles with slices down to
+    512 long; 0 when none applies (m <= 64 included)."""
     if m <= 64 or k % 64:
         return 0
     tiles = -(-m // 128) * -(-n // 160)
     if tiles >= 128:
         return 0
+    least = 1024
+    if m <= 256:
+        tiles, least = -(-m // 128) * -(-n // 128), 512
     s = 1
-    while tiles * s < 192 and (k // 64) % (2 * s) == 0 and k // (2 * s) >= 1024:
+    while tiles * s < 192 and (k // 64) % (2 * s) == 0 and k // (2 * s) >= least:
         s *= 2
     return s if s > 1 else 0
 
@@ -159,8 +163,9 @@ def test_linear_workspace_size(lib):
     boundary) the slices' int32 [M, N] partial products; -1 for a shape the
     entry point rejects."""
     shapes = [(4096, 1280, 5120), (4096, 10240, 1280), (3, 16, 256), (2100, 1296, 2304),
-              (1024, 1280, 5120), (2048, 640, 5120), (1000, 1296, 4096), (1024, 1280, 1280)]
-    assert [k_slices(*s) for s in shapes] == [0, 0, 0, 0, 4, 4, 4, 0]
+              (1024, 1280, 5120), (2048, 640, 5120), (1000, 1296, 4096), (1024, 1280, 1280),
+              (128, 4096, 4096), (200, 160, 16384), (65, 4096, 1024)]
+    assert [k_slices(*s) for s in shapes] == [0, 0, 0, 0, 4, 4, 4, 0, 8, 32, 2]
     for m, n, k in shapes:
         want = up256(max(m * k, tiled(m, k))) + 4 * m
         if k_slices(m, n, k):
