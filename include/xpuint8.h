@@ -139,9 +139,10 @@ int xpuint8_linear_gemm_stream(const void *stream, const int8_t *xq, const float
  * MFMA block layout when the split-K kernel takes the shape: narrow outputs
  * with a long K, as the FFN's down-projection), which is why the
  * intermediate is not exposed.  An output too small to fill the GPU (fewer
- * than 128 tiles of 128 x 160, K >= 2048) has its product split in K across
- * blocks; the workspace then also holds the slices' int32 partial products,
- * whose sum is exact.  K % 256 == 0, N % 16 == 0; bias as in
+ * than 128 tiles of 128 x 160, with K long enough to split: K >= 2048, or
+ * K >= 1024 for M <= 256) has its product split in K across blocks; the
+ * workspace then also holds the slices' int32 partial products, whose sum
+ * is exact.  K % 256 == 0, N % 16 == 0; bias as in
  * xpuint8_linear_gemm_stream.  Replaces quantize + torch._int_mm + dequant at
  * python/xpu_kernels/int8/ops.py:622-638 and the down-projection of ffn
  * (ops.py:716-719). */
