@@ -557,6 +557,25 @@ def test_linear_k_slices_exact(dev, m, n, k):
                                                mismatch(bits(y), want))
 
 
+# Each side of every threshold of the linear's GEMM choice: M = 64 / 65 (skinny
+# kernel / K slices on the 128 x 128 kernel), M = 256 / 257 (slices on the
+# 128 x 128 / split-K kernel), 104 tiles of 128 x 160 (slices), exactly 128
+# tiles (the split-K kernel) at K = 1024, 1280 and 2048, and 17 tiles with
+# K = 1280 (too short to split: the 128 x 128 kernel); ragged N
+@pytest.mark.parametrize("m,n,k", [(64, 1280, 2048), (65, 1280, 2048), (256, 2560, 1024),
+                                   (257, 2560, 2048), (1016, 2032, 2048), (1024, 2560, 1024),
+                                   (1024, 2560, 2048), (2048, 1264, 1280), (2048, 1264, 1024),
+                                   (2176, 160, 1280)])
+def test_linear_dispatch_boundaries(dev, m, n, k):
+    x = activation(m, k, seed=3 * m + k, n_out=4, mult=25.0)
+    w = weight(n, k, seed=n + 5)
+    bias = weight(1, n, seed=n + k + 2, std=0.01)[0]
+    w8, ws = int8.prepare_weight(w.to(dev))
+    y = int8.linear(x.to(dev), w8, ws, bias.to(dev))
+    want = O.linear(bits(x), npy(w8), npy(ws), O.bf16_to_f32(bits(bias)))
+    assert np.array_equal(bits(y), want), mismatch(bits(y), want)
+
+
 def test_linear_shapes_and_dtypes(dev):
     x = activation(2 * 3 * 5, 512, seed=3).reshape(2, 3, 5, 512)
     w = weight(48, 512)
