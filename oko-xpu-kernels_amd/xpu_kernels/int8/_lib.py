@@ -159,7 +159,17 @@ def _err(lib, what):
     raise RuntimeError(f"{what}: {lib.xpuint8_last_error()!r}")
 
 
+# torch's accessor of the current stream's raw handle (0.1 us against 2 us for
+# building a torch.cuda.Stream per call; a private name, so the public form
+# stays as the fallback)
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream(device):
+    """The HIP stream behind torch's current stream on ``device``."""
+    if _RAW_STREAM is not None:
+        index = device.index if device.index is not None else torch.cuda.current_device()
+        return ctypes.c_void_p(_RAW_STREAM(index))
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
 
 
