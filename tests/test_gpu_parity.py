@@ -599,6 +599,21 @@ def test_ffn_geglu_exact(dev):
     assert np.array_equal(bits(y), want), mismatch(bits(y), want)
 
 
+@pytest.mark.parametrize("m", [200, 1024])
+def test_ffn_small_batch_k_slices_exact(dev, m):
+    """An FFN whose down-projection (K = 5120, N = 1280) has too few output
+    tiles to fill the chip: the product is split in K across blocks (8 slices
+    on the 128 x 128 kernel at M = 200, 4 on the split-K kernel at M = 1024)."""
+    k, inner = 1280, 5120
+    x = activation(m, k, seed=11 + m)
+    up8, ups = int8.prepare_weight(weight(2 * inner, k, seed=12).to(dev))
+    dn8, dns = int8.prepare_weight(weight(k, inner, seed=13).to(dev))
+    db = weight(1, k, seed=14, std=0.01)[0].float()
+    y = int8.ffn(x.to(dev), up8, ups, dn8, dns, db.to(dev), act="geglu_erf")
+    want = O.ffn(bits(x), npy(up8), npy(ups), npy(dn8), npy(dns), npy(db), act=4)
+    assert np.array_equal(bits(y), want), mismatch(bits(y), want)
+
+
 @pytest.mark.parametrize("act", [3, 4, 5])
 @pytest.mark.parametrize("m,inner,k", [(300, 512, 1280), (64, 1280, 1040), (512, 256, 256)])
 def test_ffn_up_epilogue_exact(dev, act, m, inner, k):
