@@ -201,7 +201,9 @@ int xpuint8_dx_gemm_stream(const void *stream, const int8_t *q, const float *a,
  * [N], dx bf16 [M,K].  K % 256 == 0, N % 16 == 0.  `work` is a device buffer
  * of at least xpuint8_linear_dx_int8_workspace_size(M, N, K) bytes (the
  * quantized gradient, its scales, the transposed weight and the product before
- * the inverse rotation), 16-byte aligned; it is fully written before it is
+ * the inverse rotation; for small batches, whose [M,K] output has too few
+ * tiles to fill the GPU, also the int32 partial products of the contraction
+ * split across blocks), 16-byte aligned; it is fully written before it is
  * read, so it needs no clearing.  Replaces linear_dx_int8
  * (python/xpu_kernels/int8/ops.py:353-377): its torch multiply, the Triton
  * quantize_row, torch._int_mm, dequant and rotate. */

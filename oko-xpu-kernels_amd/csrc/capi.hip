@@ -144,10 +144,12 @@ int check_gemm(int64_t M, int64_t N, int64_t K) {
 // q [M,N] int8 (row-major, or in the MFMA block layout when the split-K
 // kernel reads it) and its row scales a [M] fp32, the transposed weight w8^T
 // [K,N] int8 (the GEMM's K-contiguous operand, for shapes the split-K kernel
-// does not take), and the product before the inverse rotation, bf16 [M,K].
+// does not take), and the product before the inverse rotation, bf16 [M,K];
+// for a product split in K across blocks (gemm_slices of the [M,K] output
+// over the contraction N), then the slices' int32 [M,K] partial products.
 // Each piece starts on a 256-byte boundary.
 struct DxWork {
-    size_t q, a, wt, pre, total;
+    size_t q, a, wt, pre, part, total;
 };
 DxWork dx_work_layout(int64_t M, int64_t N, int64_t K) {
     auto up = [](int64_t b) { return (size_t(b) + 255) & ~size_t(255); };
@@ -156,7 +158,9 @@ DxWork dx_work_layout(int64_t M, int64_t N, int64_t K) {
     w.a = w.q + up(std::max(M * N, tiled_bytes(M, N)));
     w.wt = w.a + up(4 * M);
     w.pre = w.wt + up(N * K);
-    w.total = w.pre + up(2 * M * K);
+    w.part = w.pre + up(2 * M * K);
+    const int nsl = gemm_slices(int(M), int(K), int(N));
+    w.total = w.part + (nsl > 0 ? size_t(nsl) * size_t(M) * size_t(K) * 4 : 0);
     return w;
 }
 
@@ -183,6 +187,27 @@ int dx_chain(hipStream_t st, const void* dy, const float* w_scale, const int8_t*
                          "linear_dx_int8 (quantize_row)"));
         XPU_TRY(launched(gemm_dequant_nn_xt(st, q, w8, K, pre, K, a, int(M), int(K), int(N)),
                          "linear_dx_int8 (gemm)"));
+        return launched(rotate_bf16(st, pre, dx, M, int(K)), "linear_dx_int8 (rotate)");
+    }
+    // too few output tiles for the chip: the contraction split across blocks,
+    // the slices' int32 partial sums added by the dequant pass (unit column
+    // scale, row scale a)
+    if (const int nsl = gemm_slices(int(M), int(K), int(N))) {
+        int32_t* part = reinterpret_cast<int32_t*>(work + L.part);
+        XPU_TRY(launched(quantize_row(st, dy, w_scale, q, a, M, int(N)),
+                         "linear_dx_int8 (quantize_row)"));
+        if (slices_need_nt(int(M))) {
+            XPU_TRY(launched(transpose_i8(st, w8, wt, N, K), "linear_dx_int8 (transpose)"));
+            XPU_TRY(launched(gemm_i32_slices(st, q, N, wt, N, part, int(M), int(K), int(N), nsl),
+                             "linear_dx_int8 (gemm)"));
+        } else {
+            XPU_TRY(launched(gemm_i32_slices_nn(st, q, N, w8, K, part, int(M), int(K), int(N),
+                                                nsl),
+                             "linear_dx_int8 (gemm)"));
+        }
+        XPU_TRY(launched(dequant_slices(st, part, K, nsl, M * K, pre, a, nullptr, nullptr,
+                                        nullptr, M, K),
+                         "linear_dx_int8 (dequant)"));
         return launched(rotate_bf16(st, pre, dx, M, int(K)), "linear_dx_int8 (rotate)");
     }
     XPU_TRY(launched(quantize_row(st, dy, w_scale, q, a, M, int(N)), "linear_dx_int8 (quantize_row)"));

@@ -1187,13 +1187,13 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_splitk_kernel(
     constexpr int STAGE_BYTES = NB * 1024, RING = S * STAGE_BYTES;
     constexpr bool SLICE = IsSliceEpi<Epi>::value;
     static_assert(!Epi::kPaired && (Epi::kStaged || SLICE), "dequant or slice epilogues only");
-    static_assert(!SLICE || (!XT && !WNN), "K slices of row-major operands");
+    static_assert(!SLICE || !XT, "K slices of a row-major X");
     static_assert(2 * RING >= 4 * TN * (TM / 2) * 1024, "half of a team's accumulators fit");
     // K slice blockIdx.y of a split across blocks: K is the slice's length and
     // the operands' rows keep their full strides
     if constexpr (SLICE) {
         X += int64_t(blockIdx.y) * K;
-        W += int64_t(blockIdx.y) * K;
+        W += WNN ? int64_t(blockIdx.y) * K * ldw : int64_t(blockIdx.y) * K;
     }
     static_assert(S >= 3 && S <= 4, "three or four stages");
     __shared__ __attribute__((aligned(1024))) int8_t smem[2 * RING];
@@ -1662,7 +1662,8 @@ __global__ __launch_bounds__(256) void dequant_kernel(const int32_t* __restrict_
         for (int u = 0; u < DQ_U; ++u) {
             const int64_t c = c0 + 1024 * u;
             if (c >= N) break;
-            const float4 w = *reinterpret_cast<const float4*>(ws + c);
+            const float4 w = ws ? *reinterpret_cast<const float4*>(ws + c)
+                                : make_float4(1.f, 1.f, 1.f, 1.f);
             float r0 = float(a[u].x) * (w.x * x), r1 = float(a[u].y) * (w.y * x);
             float r2 = float(a[u].z) * (w.z * x), r3 = float(a[u].w) * (w.w * x);
             if (bias) {
@@ -1797,6 +1798,20 @@ hipError_t gemm_i32_slices(hipStream_t st, const int8_t* X, int64_t ldx, const i
                        M, N, K / nsl, tm, tn, EpiSliceI32{part, int64_t(N), int64_t(M) * N});
     return hipGetLastError();
 }
+
+// The same with B stored [K, N] (the NN product, the split-K kernel's
+// transposing weight reads): for M > 256 only (the 128 x 128 kernel has no NN
+// form; callers transpose B for M <= 256)
+hipError_t gemm_i32_slices_nn(hipStream_t st, const int8_t* X, int64_t ldx, const int8_t* Bkn,
+                              int64_t ldb, int32_t* part, int M, int N, int K, int nsl) {
+    if (slices_small_tiles(M)) return hipErrorInvalidValue;
+    const int tm = (M + 127) / 128, tn = (N + 159) / 160;
+    hipLaunchKernelGGL((gemm_i8_splitk_kernel<4, false, true, EpiSliceI32, false>),
+                       dim3(unsigned(tm * tn), unsigned(nsl)), dim3(512), 0, st, X, ldx, Bkn, ldb,
+                       M, N, K / nsl, tm, tn, EpiSliceI32{part, int64_t(N), int64_t(M) * N});
+    return hipGetLastError();
+}
+bool slices_need_nt(int M) { return slices_small_tiles(M); }
 
 // B[k, n] as stored (the NN product); the 32-bit DMA offsets of the weight
 // need K * ldb below 2^32

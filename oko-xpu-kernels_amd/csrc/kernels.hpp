@@ -79,7 +79,7 @@ hipError_t dequant_epilogue(hipStream_t st, const int32_t* acc, int64_t acc_ld, 
                             const float* xs, const float* ws, const float* bias, int64_t M,
                             int64_t N);
 // the same on the sum of nsl int32 slices sl_stride apart, with an fp32 (bias)
-// or bf16 (bias16) bias or neither
+// or bf16 (bias16) bias or neither; ws == nullptr is a unit column scale
 hipError_t dequant_slices(hipStream_t st, const int32_t* acc, int64_t acc_ld, int nsl,
                           int64_t sl_stride, void* out, const float* xs, const float* ws,
                           const float* bias, const uint16_t* bias16, int64_t M, int64_t N);
@@ -88,6 +88,11 @@ hipError_t dequant_slices(hipStream_t st, const int32_t* acc, int64_t acc_ld, in
 int gemm_slices(int M, int N, int K);
 hipError_t gemm_i32_slices(hipStream_t st, const int8_t* X, int64_t ldx, const int8_t* W,
                            int64_t ldw, int32_t* part, int M, int N, int K, int nsl);
+// the same with B stored [K, N]; only where !slices_need_nt(M) (others
+// transpose B and call gemm_i32_slices); ldb * (K + 64) below 2^32
+hipError_t gemm_i32_slices_nn(hipStream_t st, const int8_t* X, int64_t ldx, const int8_t* Bkn,
+                              int64_t ldb, int32_t* part, int M, int N, int K, int nsl);
+bool slices_need_nt(int M);
 hipError_t transpose_i8(hipStream_t st, const int8_t* in, int8_t* out, int64_t R, int64_t C);
 
 // gemm_bf16.hip: dw[n, k] = sum_m dy[m, n] * x[m, k] (bf16, fp32 accumulate)

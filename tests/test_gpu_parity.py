@@ -770,6 +770,19 @@ def test_linear_dx_int8_split_k_shapes(dev, m, n, k):
     assert np.array_equal(bits(dx), want), mismatch(bits(dx), want)
 
 
+@pytest.mark.parametrize("m,n,k", [(200, 5120, 1280), (1024, 5120, 1280), (300, 2560, 1024)])
+def test_linear_dx_int8_k_slices_exact(dev, m, n, k):
+    """Small batches, too few output tiles for the chip: the contraction is
+    split across blocks (8 slices on the 128 x 128 kernel through the
+    transposed weight at M = 200; 4 and 2 slices on the split-K kernel
+    reading the weight as stored, the last with a ragged 160-column tile)."""
+    dy = activation(m, n, seed=m + n, scale=1e-3, n_out=0)
+    w8, ws = int8.prepare_weight(weight(n, k, seed=k + 1).to(dev))
+    dx = int8.linear_dx_int8(dy.to(dev), w8, ws)
+    want = O.linear_dx_int8(bits(dy), npy(w8), npy(ws))
+    assert np.array_equal(bits(dx), want), mismatch(bits(dx), want)
+
+
 def test_linear_dx_int8_exact(dev):
     m, n, k = 512, 1280, 1280
     dy = activation(m, n, seed=8, scale=1e-3, n_out=0)

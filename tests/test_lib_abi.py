@@ -132,6 +132,13 @@ def test_dx_workspace_size(lib):
     assert lib.xpuint8_linear_dx_int8_workspace_size(m, n, k) == want
     assert lib.xpuint8_linear_dx_int8_workspace_size(3, 16, 256) == (
         up256(tiled(3, 16)) + 256 + 16 * 256 + up256(2 * 3 * 256))
+    # a contraction split across blocks: then the slices' int32 [M,K] partials
+    for m, n, k in [(1024, 5120, 1280), (200, 5120, 1280)]:
+        s = k_slices(m, k, n)
+        assert s in (4, 8)
+        want = (up256(max(m * n, tiled(m, n))) + up256(4 * m) + up256(n * k) + up256(2 * m * k)
+                + s * m * k * 4)
+        assert lib.xpuint8_linear_dx_int8_workspace_size(m, n, k) == want, (m, n, k)
     assert lib.xpuint8_linear_dx_int8_workspace_size(4, 24, 512) == -1
     assert lib.xpuint8_linear_dx_int8_workspace_size(4, 32, 300) == -1
 
