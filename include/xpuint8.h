@@ -257,10 +257,21 @@ int xpuint8_linear_dw_stream(const void *stream, const void *dy, const void *x, 
  * backward): dx[m,k] = sum_n dy[m,n] * w[n,k], dy bf16 [M,N], w bf16 [N,K]
  * (the unrotated weight, e.g. from xpuint8_dequant_weight_stream), dx bf16
  * [M,K]; fp32 accumulation, one RNE rounding.  N % 16 == 0, K % 16 == 0.
+ * `work` may be NULL.  A small batch, whose [M,K] output has too few tiles to
+ * fill the GPU, with a `work` of xpuint8_linear_dx_workspace_size(M, N, K)
+ * bytes (16-byte aligned; no clearing needed) has the contraction split
+ * across blocks: their fp32 partial sums are added in a fixed order, then
+ * rounded once, so the result is as above up to the order of the fp32 sum.
  * Replaces the torch matmul dy @ w of linear_dx
  * (python/xpu_kernels/int8/ops.py:194-204). */
 int xpuint8_linear_dx_stream(const void *stream, const void *dy, const void *w, void *dx,
-                             int64_t M, int64_t N, int64_t K);
+                             int64_t M, int64_t N, int64_t K, void *work, int64_t work_bytes);
+
+/* The workspace xpuint8_linear_dx_stream uses for this shape, in bytes: 0
+ * when the contraction is not split, -1 when the shape is not supported.  No
+ * device needed.  A helper of the entry point above (no reference
+ * counterpart). */
+int64_t xpuint8_linear_dx_workspace_size(int64_t M, int64_t N, int64_t K);
 
 /* RMSNorm + rotary embedding of q or k read straight from the int32
  * accumulator of a quantized qkv projection (one [B,S,H,D] slice of it):

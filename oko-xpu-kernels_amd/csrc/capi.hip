@@ -586,13 +586,30 @@ int xpuint8_linear_dw_stream(const void* stream, const void* dy, const void* x, 
                     "linear_dw");
 }
 
-int xpuint8_linear_dx_stream(const void* stream, const void* dy, const void* w, void* dx,
-                             int64_t M, int64_t N, int64_t K) {
+static int check_linear_dx(int64_t M, int64_t N, int64_t K) {
     if (M <= 0 || N <= 0 || K <= 0) return fail(2, "M, N and K must be positive");
     if (N % 16 != 0 || K % 16 != 0) return fail(2, "N and K must be multiples of 16");
     if (M > kMaxDim || N > kMaxDim || K > kMaxDim) return fail(4, "M, N and K must be < 2^31");
-    XPU_NONNULL(dy); XPU_NONNULL(w); XPU_NONNULL(dx);
+    return 0;
+}
+
+int64_t xpuint8_linear_dx_workspace_size(int64_t M, int64_t N, int64_t K) {
+    if (check_linear_dx(M, N, K) != 0) return -1;
+    const int nsl = bf16_nn_slices(int(M), int(N), int(K));
+    return nsl > 0 ? int64_t(nsl) * M * K * 4 : 0;
+}
+
+int xpuint8_linear_dx_stream(const void* stream, const void* dy, const void* w, void* dx,
+                             int64_t M, int64_t N, int64_t K, void* work, int64_t work_bytes) {
+    XPU_TRY(check_linear_dx(M, N, K));
+    XPU_NONNULL(dy); XPU_NONNULL(w); XPU_NONNULL(dx); XPU_ALIGNED_OPT(work);
     XPU_TRY(ensure_device());
+    // a small batch with a workspace: the contraction split across blocks
+    const int nsl = bf16_nn_slices(int(M), int(N), int(K));
+    if (nsl > 0 && work != nullptr && work_bytes >= int64_t(nsl) * M * K * 4)
+        return launched(gemm_bf16_nn_slices(as_stream(stream), dy, N, w, K, dx, K, int(M), int(N),
+                                            int(K), static_cast<float*>(work), nsl),
+                        "linear_dx");
     return launched(gemm_bf16_nn(as_stream(stream), dy, N, w, K, dx, K, int(M), int(N), int(K)),
                     "linear_dx");
 }

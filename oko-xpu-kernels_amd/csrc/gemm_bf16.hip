@@ -421,10 +421,20 @@ __device__ __forceinline__ v8s plain_read_at(uint32_t addr) {
     return r;
 }
 
-template <int S, bool YT>
+// SL: contraction slice blockIdx.y of a split across blocks (dense dx only):
+// R is the slice's length, A's rows and Y's columns are offset to it, and the
+// slice's fp32 partial sums go to (float*)out + blockIdx.y * sl_stride
+// instead of the bf16 output.
+template <int S, bool YT, bool SL = false>
 __global__ __launch_bounds__(512, 1) void gemm_bf16_splitk_kernel(
     const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ Y, int64_t ldy,
-    uint16_t* __restrict__ out, int64_t ldo, int R, int K, int NBR, int tiles_b, int tiles_k) {
+    uint16_t* __restrict__ out, int64_t ldo, int R, int K, int NBR, int tiles_b, int tiles_k,
+    int64_t sl_stride = 0) {
+    static_assert(!SL || !YT, "contraction slices for the dense dx");
+    if constexpr (SL) {
+        A += int64_t(blockIdx.y) * R * lda;
+        Y += int64_t(blockIdx.y) * R;
+    }
     constexpr int BK = 160, TK = 5;                     // A side: k columns, blocks per wave
     constexpr int TB = YT ? 5 : 4, BB = 32 * TB;        // B side: blocks per wave, tile rows
     constexpr int AB = BK / 16, YB = BB / 16, NB = AB + YB;
@@ -691,14 +701,40 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_splitk_kernel(
                 const int k = k0 + wk * 80 + 16 * a + 4 * (lane >> 4);
                 if (k < K) {
                     const v4f v = acc[a][b];
-                    *reinterpret_cast<uint2*>(out + int64_t(row) * ldo + k) =
-                        make_uint2(cvt_pk_bf16(v[0], v[1]), cvt_pk_bf16(v[2], v[3]));
+                    if constexpr (SL)
+                        *reinterpret_cast<v4f*>(reinterpret_cast<float*>(out) +
+                                                int64_t(blockIdx.y) * sl_stride +
+                                                int64_t(row) * ldo + k) = v;
+                    else
+                        *reinterpret_cast<uint2*>(out + int64_t(row) * ldo + k) =
+                            make_uint2(cvt_pk_bf16(v[0], v[1]), cvt_pk_bf16(v[2], v[3]));
                 }
             }
         }
     };
     if (team == 0) finish(std::integral_constant<int, 0>{});
     else finish(std::integral_constant<int, 1>{});
+}
+
+// out[m, k] = bf16(sum over s of part[s][m, k]), the slices added in order in
+// fp32; four columns per thread (K % 4 == 0), grid-stride.
+__global__ __launch_bounds__(256) void sum_slices_bf16_kernel(const float* __restrict__ part,
+                                                              int nsl, int64_t sl_stride,
+                                                              uint16_t* __restrict__ out,
+                                                              int64_t ldo, int64_t M, int64_t K) {
+    const int64_t q = K / 4, total = M * q;
+    for (int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; t < total;
+         t += int64_t(gridDim.x) * blockDim.x) {
+        const int64_t m = t / q, k = (t - m * q) * 4;
+        const float* p = part + m * K + k;
+        float4 v = *reinterpret_cast<const float4*>(p);
+        for (int s = 1; s < nsl; ++s) {
+            const float4 w = *reinterpret_cast<const float4*>(p + s * sl_stride);
+            v.x = v.x + w.x; v.y = v.y + w.y; v.z = v.z + w.z; v.w = v.w + w.w;
+        }
+        *reinterpret_cast<uint2*>(out + m * ldo + k) =
+            make_uint2(cvt_pk_bf16(v.x, v.y), cvt_pk_bf16(v.z, v.w));
+    }
 }
 
 }  // namespace
@@ -713,6 +749,36 @@ static bool bf16_splitk_applies(int nb, int bb, int R, int K, int64_t lda, int64
     if (yt && int64_t(R) * ldy * 2 >= (int64_t(1) << 32)) return false;
     const int64_t tiles = int64_t((nb + bb - 1) / bb) * ((K + 159) / 160);
     return tiles >= 128 && tiles <= 256;
+}
+
+// Contraction slices of the dense dx (dy [M, N] . w [N, K]) split across
+// blocks, when its 128 x 160 tiles are too few for the split-K kernel (below
+// 128): the fewest power-of-two slices giving at least 192 blocks, each slice
+// a whole number of 32-row steps and at least 1024 rows; 0 when none applies.
+int bf16_nn_slices(int M, int N, int K) {
+    if (M <= 64 || K % 8 || N % kStepRows) return 0;
+    const int64_t tiles = int64_t((M + 127) / 128) * ((K + 159) / 160);
+    if (tiles >= 128) return 0;
+    int s = 1;
+    while (tiles * s < 192 && (N / kStepRows) % (2 * s) == 0 && N / (2 * s) >= 1024) s *= 2;
+    return s > 1 ? s : 0;
+}
+
+hipError_t gemm_bf16_nn_slices(hipStream_t st, const void* dy, int64_t ldy, const void* w,
+                               int64_t ldw, void* out, int64_t ldo, int M, int N, int K,
+                               float* part, int nsl) {
+    const int tm = (M + 127) / 128, tk = (K + 159) / 160;
+    hipLaunchKernelGGL((gemm_bf16_splitk_kernel<4, false, true>),
+                       dim3(unsigned(tm * tk), unsigned(nsl)), dim3(512), 0, st,
+                       static_cast<const uint16_t*>(w), ldw, static_cast<const uint16_t*>(dy), ldy,
+                       reinterpret_cast<uint16_t*>(part), int64_t(K), N / nsl, K, M, tm, tk,
+                       int64_t(M) * K);
+    if (const hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+    int64_t blocks = (int64_t(M) * (K / 4) + 255) / 256;
+    if (blocks > (int64_t(1) << 20)) blocks = int64_t(1) << 20;
+    hipLaunchKernelGGL(sum_slices_bf16_kernel, dim3(unsigned(blocks)), dim3(256), 0, st, part, nsl,
+                       int64_t(M) * K, static_cast<uint16_t*>(out), ldo, int64_t(M), int64_t(K));
+    return hipGetLastError();
 }
 
 hipError_t gemm_bf16_nn(hipStream_t st, const void* dy, int64_t ldy, const void* w, int64_t ldw,

@@ -95,6 +95,13 @@ hipError_t gemm_i32_slices_nn(hipStream_t st, const int8_t* X, int64_t ldx, cons
 bool slices_need_nt(int M);
 hipError_t transpose_i8(hipStream_t st, const int8_t* in, int8_t* out, int64_t R, int64_t C);
 
+// gemm_bf16.hip: the dense dx with its contraction split across blocks
+// (bf16_nn_slices slices, 0 when none applies): the slices' fp32 partials in
+// part (nsl * M * K floats), then their sum rounded to bf16 into out
+int bf16_nn_slices(int M, int N, int K);
+hipError_t gemm_bf16_nn_slices(hipStream_t st, const void* dy, int64_t ldy, const void* w,
+                               int64_t ldw, void* out, int64_t ldo, int M, int N, int K,
+                               float* part, int nsl);
 // gemm_bf16.hip: dw[n, k] = sum_m dy[m, n] * x[m, k] (bf16, fp32 accumulate)
 hipError_t gemm_bf16_tn(hipStream_t st, const void* dy, int64_t ldy, const void* x, int64_t ldx,
                         void* dw, int64_t ldo, int R, int N, int K);

@@ -79,7 +79,8 @@ def _signatures():
         "xpuint8_prepare_weight_stream": ([vp] * 4 + [i64] * 2, c_int),
         "xpuint8_quantize_row_stream": ([vp] * 5 + [i64] * 2, c_int),
         "xpuint8_linear_dw_stream": ([vp] * 4 + [i64] * 3, c_int),
-        "xpuint8_linear_dx_stream": ([vp] * 4 + [i64] * 3, c_int),
+        "xpuint8_linear_dx_stream": ([vp] * 4 + [i64] * 3 + [vp, i64], c_int),
+        "xpuint8_linear_dx_workspace_size": ([i64] * 3, i64),
         "xpuint8_rms_rope_dequant_stream": ([vp, vp] + [i64] * 3 + [vp] + [i64] * 2 + [vp, vp]
                                             + [i64] * 7 + [vp, vp] + [i64] * 4
                                             + [ctypes.c_float, i32], c_int),

@@ -172,8 +172,12 @@ def linear_dx(dy, w):
         m = dy2.shape[0]
         dx = torch.empty((m, k), device=dy.device, dtype=torch.bfloat16)
         if m:
+            # a small batch splits the contraction across blocks (fp32
+            # partials in the workspace)
+            need = int(lib.xpuint8_linear_dx_workspace_size(m, n, k))
+            work = torch.empty(need, device=dy.device, dtype=torch.uint8) if need > 0 else None
             rc = lib.xpuint8_linear_dx_stream(_stream(dy.device), _ptr(dy2), _ptr(w2), _ptr(dx),
-                                              m, n, k)
+                                              m, n, k, _opt(work), max(need, 0))
             if rc != 0:
                 _err(lib, "linear_dx")
         return dx.reshape(*dy.shape[:-1], k)

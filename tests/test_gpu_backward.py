@@ -36,9 +36,12 @@ def _bf16_bound(got_bf16_bits, ref, mag):
 
 # (2100, 2048, 1200) and (4000, 2080, 1280) take the split-K kernel with
 # ragged rows and columns and, for the second, an odd number of 32-row
-# contraction steps (the teams' halves differ by one)
+# contraction steps (the teams' halves differ by one); small batches whose
+# contraction is split across blocks (129 x 640 and 1024 x 1280: 4 slices,
+# 200 x 1280 and the ragged 777 x 1040: 2)
 @pytest.mark.parametrize("m,n,k", [(4096, 5120, 1280), (77, 48, 144), (1, 16, 16), (300, 1040, 272),
-                                   (129, 4096, 640), (2100, 2048, 1200), (4000, 2080, 1280)])
+                                   (129, 4096, 640), (2100, 2048, 1200), (4000, 2080, 1280),
+                                   (1024, 5120, 1280), (200, 2048, 1280), (777, 3072, 1040)])
 def test_linear_dx_dense(dev, m, n, k):
     g = torch.Generator().manual_seed(m + n + k)
     dy = (torch.randn(m, n, generator=g) * 1e-3).to(torch.bfloat16)

@@ -163,6 +163,19 @@ def k_slices(m, n, k):
     return s if s > 1 else 0
 
 
+def test_linear_dx_workspace_size(lib):
+    """The dense dx's optional workspace: fp32 [M, K] partial sums per slice
+    when its 128 x 160 output tiles number below 128 (the fewest power-of-two
+    slices giving 192 blocks, each a whole number of 32-row steps of at least
+    1024 rows), else 0; -1 for a shape the entry point rejects."""
+    assert lib.xpuint8_linear_dx_workspace_size(1024, 5120, 1280) == 4 * 1024 * 1280 * 4
+    assert lib.xpuint8_linear_dx_workspace_size(200, 2048, 1280) == 2 * 200 * 1280 * 4
+    assert lib.xpuint8_linear_dx_workspace_size(4096, 5120, 1280) == 0     # 256 tiles
+    assert lib.xpuint8_linear_dx_workspace_size(64, 5120, 1280) == 0       # M <= 64
+    assert lib.xpuint8_linear_dx_workspace_size(300, 1040, 272) == 0       # 1040 % 32
+    assert lib.xpuint8_linear_dx_workspace_size(4, 24, 512) == -1
+
+
 def test_linear_workspace_size(lib):
     """The linear's workspace: the quantized activation (row-major or in the
     block layout, whichever is larger) rounded up to 256 bytes, then its fp32
