@@ -140,7 +140,8 @@ int xpuint8_linear_gemm_stream(const void *stream, const int8_t *xq, const float
  * with a long K, as the FFN's down-projection), which is why the
  * intermediate is not exposed.  An output too small to fill the GPU (fewer
  * than 128 tiles of 128 x 160, with K long enough to split: K >= 2048, or
- * K >= 1024 for M <= 256) has its product split in K across blocks; the
+ * K >= 1024 for M <= 256; for 33 <= M <= 128, fewer than 256 blocks of 32
+ * columns with K >= 2048) has its product split in K across blocks; the
  * workspace then also holds the slices' int32 partial products, whose sum
  * is exact.  K % 256 == 0, N % 16 == 0; bias as in
  * xpuint8_linear_gemm_stream.  Replaces quantize + torch._int_mm + dequant at
@@ -184,6 +185,29 @@ int xpuint8_linear_gemm_residual_stream(const void *stream, const int8_t *xq,
 int xpuint8_ffn_up_stream(const void *stream, const int8_t *xq, const float *x_scale,
                           const int8_t *w8, const float *w_scale, void *out, int64_t M, int64_t N,
                           int64_t K, int32_t activation);
+
+/* The whole FFN in one call:
+ *   (xq, xs) = xpuint8_convrot_quantize_stream(x)            x bf16 [M,K]
+ *   v        = xpuint8_ffn_up_stream(xq, xs, up_w8, up_scale) bf16 [M,inner]
+ *   out      = xpuint8_linear_stream(v, down_w8, down_scale, bias)  bf16 [M,K]
+ * bit for bit, with up_w8 [2*inner, K] for activations 3 and 4 and
+ * [inner, K] for 5, up_scale fp32 per up row, down_w8 int8 [K, inner],
+ * down_scale fp32 [K], bias as in xpuint8_linear_gemm_stream (the
+ * up-projection is unbiased).  The intermediates live in `work`, a device
+ * buffer of at least xpuint8_ffn_workspace_size(M, inner, K, activation)
+ * bytes, 16-byte aligned; it needs no clearing.  K % 256 == 0,
+ * inner % 256 == 0.  Replaces ffn (python/xpu_kernels/int8/ops.py:649-719):
+ * its quantize, torch._int_mm, dequant_act_quantize, torch._int_mm and
+ * dequant, in four kernels (five when the down-projection is split in K). */
+int xpuint8_ffn_stream(const void *stream, const void *x, const int8_t *up_w8,
+                       const float *up_scale, const int8_t *down_w8, const float *down_scale,
+                       const void *bias, int32_t bias_bf16, void *out, int64_t M, int64_t inner,
+                       int64_t K, int32_t activation, void *work, int64_t work_bytes);
+
+/* The workspace xpuint8_ffn_stream needs, in bytes, or -1 when the shape or
+ * the activation is not supported.  No device needed.  A helper of the entry
+ * point above, with no counterpart in the reference. */
+int64_t xpuint8_ffn_workspace_size(int64_t M, int64_t inner, int64_t K, int32_t activation);
 
 /* linear_dx_int8's GEMM: dx[m,k] = bf16(float(sum_n q[m,n] w8[n,k]) * a[m]),
  * the NN product with the row-scale epilogue.  `work` holds w8^T (K*N bytes).

@@ -240,6 +240,65 @@ size_t linear_work_bytes(int64_t M, int64_t N, int64_t K) {
     return linear_work_q_bytes(M, K) + 4 * size_t(M);
 }
 
+// quantize + GEMM + dequant of xpuint8_linear_stream on checked arguments.
+int linear_run(hipStream_t st, const void* x, const int8_t* w8, const float* w_scale,
+               const void* bias, int32_t bias_bf16, void* out, int64_t M, int64_t N, int64_t K,
+               void* work) {
+    int8_t* q = static_cast<int8_t*>(work);
+    float* xs = reinterpret_cast<float*>(static_cast<char*>(work) + linear_work_q_bytes(M, K));
+    const float* b32 = bias_bf16 ? nullptr : static_cast<const float*>(bias);
+    const uint16_t* b16 = bias_bf16 ? static_cast<const uint16_t*>(bias) : nullptr;
+    // too few output tiles for the chip: the product split in K across
+    // blocks, each slice's int32 partial sums in the workspace, then one pass
+    // that adds them and applies the dequant
+    if (const int nsl = gemm_slices(int(M), int(N), int(K))) {
+        int32_t* part = reinterpret_cast<int32_t*>(static_cast<char*>(work) +
+                                                   linear_work_part_offset(M, K));
+        XPU_TRY(launched(convrot_quantize(st, x, q, xs, M, int(K), 0), "linear (quantize)"));
+        XPU_TRY(launched(gemm_i32_slices(st, q, K, w8, K, part, int(M), int(N), int(K), nsl),
+                         "linear (gemm)"));
+        return launched(dequant_slices(st, part, N, nsl, M * N, out, xs, w_scale, b32, b16, M, N),
+                        "linear (dequant)");
+    }
+    // narrow outputs with a long K take the split-K kernel, which reads q in
+    // the MFMA block layout; the other shapes a row-major q
+    if (splitk_applies(int(M), int(N), int(K)) && rowquant_can_tile(int(K))) {
+        XPU_TRY(launched(convrot_quantize_tiled(st, x, q, xs, M, int(K)), "linear (quantize)"));
+        return launched(gemm_dequant_xt(st, q, w8, K, out, N, xs, w_scale, b32, b16, int(M),
+                                        int(N), int(K)),
+                        "linear (gemm)");
+    }
+    XPU_TRY(launched(convrot_quantize(st, x, q, xs, M, int(K), 0), "linear (quantize)"));
+    return launched(gemm_dequant(st, q, K, w8, K, out, N, xs, w_scale, b32, b16, int(M), int(N),
+                                 int(K)),
+                    "linear (gemm)");
+}
+
+// The four launches of the FFN after its up-projection's quantize: the
+// up-projection GEMM with the activation in its store, then the linear of
+// the activation.  Workspace: the activation bf16 [M, inner], then one
+// region that first holds x quantized (row-major q, then its row scales on a
+// 256-byte boundary) and then, once the up-projection has read it, the
+// down-projection's linear workspace.
+size_t ffn_work_region_offset(int64_t M, int64_t inner) {
+    return (size_t(M) * size_t(inner) * 2 + 255) & ~size_t(255);
+}
+size_t ffn_work_bytes(int64_t M, int64_t inner, int64_t K) {
+    const size_t up = ((size_t(M) * size_t(K) + 255) & ~size_t(255)) + 4 * size_t(M);
+    return ffn_work_region_offset(M, inner) + std::max(up, linear_work_bytes(M, K, inner));
+}
+
+int ffn_check(int64_t M, int64_t inner, int64_t K, int32_t activation) {
+    if (activation != 3 && activation != 4 && activation != 5)
+        return fail(6, "ffn supports activation 3 (situ), 4 (GEGLU) or 5 (GELU-erf)");
+    XPU_TRY(check_rows(M, K));           // x rotated: K % 256
+    XPU_TRY(check_rows(M, inner));       // the activation rotated: inner % 256
+    XPU_TRY(check_epilogue(M, inner));
+    XPU_TRY(check_epilogue(M, K));
+    XPU_TRY(check_gemm(M, act_paired(activation) ? 2 * inner : inner, K));
+    return check_gemm(M, K, inner);
+}
+
 int act_ok(int32_t act) {
     if (act < 1 || act > 5)
         return fail(6, "activation must be 1 (GELU-tanh), 2 (SwiGLU), 3 (situ), 4 (GEGLU) "
@@ -461,35 +520,36 @@ int xpuint8_linear_stream(const void* stream, const void* x, const int8_t* w8,
     if (work_bytes < int64_t(linear_work_bytes(M, N, K)))
         return fail(2, "work must hold xpuint8_linear_workspace_size(M, N, K) bytes");
     XPU_TRY(ensure_device());
+    return linear_run(as_stream(stream), x, w8, w_scale, bias, bias_bf16, out, M, N, K, work);
+}
+
+int64_t xpuint8_ffn_workspace_size(int64_t M, int64_t inner, int64_t K, int32_t activation) {
+    if (ffn_check(M, inner, K, activation) != 0) return -1;
+    return int64_t(ffn_work_bytes(M, inner, K));
+}
+
+int xpuint8_ffn_stream(const void* stream, const void* x, const int8_t* up_w8,
+                       const float* up_scale, const int8_t* down_w8, const float* down_scale,
+                       const void* bias, int32_t bias_bf16, void* out, int64_t M, int64_t inner,
+                       int64_t K, int32_t activation, void* work, int64_t work_bytes) {
+    XPU_TRY(ffn_check(M, inner, K, activation));
+    XPU_NONNULL(x); XPU_NONNULL(up_w8); XPU_NONNULL(up_scale); XPU_NONNULL(down_w8);
+    XPU_NONNULL(down_scale); XPU_NONNULL(out); XPU_NONNULL(work);
+    XPU_ALIGNED_OPT(bias);
+    if (bias_bf16 != 0 && bias_bf16 != 1) return fail(2, "bias_bf16 must be 0 or 1");
+    if (work_bytes < int64_t(ffn_work_bytes(M, inner, K)))
+        return fail(2, "work must hold xpuint8_ffn_workspace_size(M, inner, K, activation) bytes");
+    XPU_TRY(ensure_device());
     hipStream_t st = as_stream(stream);
-    int8_t* q = static_cast<int8_t*>(work);
-    float* xs = reinterpret_cast<float*>(static_cast<char*>(work) + linear_work_q_bytes(M, K));
-    const float* b32 = bias_bf16 ? nullptr : static_cast<const float*>(bias);
-    const uint16_t* b16 = bias_bf16 ? static_cast<const uint16_t*>(bias) : nullptr;
-    // too few output tiles for the chip: the product split in K across
-    // blocks, each slice's int32 partial sums in the workspace, then one pass
-    // that adds them and applies the dequant
-    if (const int nsl = gemm_slices(int(M), int(N), int(K))) {
-        int32_t* part = reinterpret_cast<int32_t*>(static_cast<char*>(work) +
-                                                   linear_work_part_offset(M, K));
-        XPU_TRY(launched(convrot_quantize(st, x, q, xs, M, int(K), 0), "linear (quantize)"));
-        XPU_TRY(launched(gemm_i32_slices(st, q, K, w8, K, part, int(M), int(N), int(K), nsl),
-                         "linear (gemm)"));
-        return launched(dequant_slices(st, part, N, nsl, M * N, out, xs, w_scale, b32, b16, M, N),
-                        "linear (dequant)");
-    }
-    // narrow outputs with a long K take the split-K kernel, which reads q in
-    // the MFMA block layout; the other shapes a row-major q
-    if (splitk_applies(int(M), int(N), int(K)) && rowquant_can_tile(int(K))) {
-        XPU_TRY(launched(convrot_quantize_tiled(st, x, q, xs, M, int(K)), "linear (quantize)"));
-        return launched(gemm_dequant_xt(st, q, w8, K, out, N, xs, w_scale, b32, b16, int(M),
-                                        int(N), int(K)),
-                        "linear (gemm)");
-    }
-    XPU_TRY(launched(convrot_quantize(st, x, q, xs, M, int(K), 0), "linear (quantize)"));
-    return launched(gemm_dequant(st, q, K, w8, K, out, N, xs, w_scale, b32, b16, int(M), int(N),
-                                 int(K)),
-                    "linear (gemm)");
+    char* v = static_cast<char*>(work);
+    char* region = v + ffn_work_region_offset(M, inner);
+    int8_t* xq = reinterpret_cast<int8_t*>(region);
+    float* xs = reinterpret_cast<float*>(region + ((size_t(M) * size_t(K) + 255) & ~size_t(255)));
+    XPU_TRY(launched(convrot_quantize(st, x, xq, xs, M, int(K), 0), "ffn (quantize)"));
+    XPU_TRY(launched(gemm_act(st, xq, K, up_w8, K, v, inner, xs, up_scale, int(M), int(inner),
+                              int(K), activation),
+                     "ffn (up projection)"));
+    return linear_run(st, v, down_w8, down_scale, bias, bias_bf16, out, M, K, inner, region);
 }
 
 int xpuint8_linear_gemm_residual_stream(const void* stream, const int8_t* xq,

@@ -281,9 +281,15 @@ struct EpiAct {
     __device__ __forceinline__ void store16(int m, int n, const uint4& v) const {
         *reinterpret_cast<uint4*>(out + int64_t(m) * ldo + n) = v;
     }
-    // unstaged form (small tiles, unpaired activations only)
+    // unstaged forms: one block of four columns (small tiles, unpaired
+    // activations), or the first and second halves' blocks of the same four
+    // columns (the skinny kernel, paired activations)
     __device__ __forceinline__ void operator()(int m, int n, const v4i& v) const {
         *reinterpret_cast<uint2*>(out + int64_t(m) * ldo + n) = convert(v, row(m), col(n));
+    }
+    __device__ __forceinline__ void pair(int m, int n, const v4i& a, const v4i& b) const {
+        *reinterpret_cast<uint2*>(out + int64_t(m) * ldo + n) =
+            convert2(a, b, row(m), col(n), col(half + n));
     }
 };
 
@@ -1465,18 +1471,37 @@ hipError_t launch_splitk(hipStream_t st, const int8_t* X, int64_t ldx, const int
 // per-block form of the same Epi.  NW follows the number of K steps (about
 // four per wave): at M=16, N=4096 and K=4096 sixteen waves cut the cold call
 // from 8.7 to 7.2 us, while at K=1280 four waves stay fastest (6.8 us against
-// 7.7 with eight and 8.6 with sixteen).
-template <int MB, int NW, class Epi>
+// 7.7 with eight and 8.6 with sixteen).  A paired epilogue (the FFN's
+// up-projection) takes the same kernel with two weight blocks per step, rows
+// n and half + n, so that both operands of its activation meet in one lane.
+template <int MB, int NW, int NB, class Epi>
 __global__ __launch_bounds__(NW * 64) void gemm_i8_skinny_kernel(
     const int8_t* __restrict__ X, int64_t ldx, const int8_t* __restrict__ W, int64_t ldw, int M,
     int N, int K, Epi epi) {
-    constexpr int D = NW >= 16 ? 4 : (MB <= 2 ? 8 : 4);     // steps in flight per wave
-    __shared__ v4i part[NW][MB][64];
+    // NB weight blocks of 16 rows per block: rows n0 + 16p, or, for a paired
+    // epilogue (an FFN's up-projection), rows n0 and half + n0, the operands
+    // of the activation at output column n0
+    constexpr bool PAIRED = Epi::kPaired;
+    static_assert(!PAIRED || NB == 2, "a paired epilogue's halves are the two weight blocks");
+    constexpr int D = NW >= 16 ? 4 : (MB * NB <= 2 ? 8 : (MB * NB <= 8 ? 4 : 2));  // steps in flight
+    __shared__ v4i part[NW][NB * MB][64];
+    // K slice blockIdx.y of a split across blocks (EpiSliceI32): K is the
+    // slice's length, the operands' rows keep their full strides
+    if constexpr (IsSliceEpi<Epi>::value) {
+        X += int64_t(blockIdx.y) * K;
+        W += int64_t(blockIdx.y) * K;
+    }
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int n0 = blockIdx.x * 16;
+    const int n0 = blockIdx.x * (PAIRED ? 16 : 16 * NB);
     const int kb = 16 * (lane >> 4);                         // lane's bytes within a step
-    const int8_t* wrow = W + int64_t(min(n0 + (lane & 15), N - 1)) * ldw + kb;
+    const int8_t* wrow[NB];
+#pragma unroll
+    for (int p = 0; p < NB; ++p) {
+        const int r = PAIRED ? min(n0 + (lane & 15), N - 1) + (p ? pair_offset(epi) : 0)
+                             : min(n0 + 16 * p + (lane & 15), N - 1);
+        wrow[p] = W + int64_t(r) * ldw + kb;
+    }
     const int8_t* xrow[MB];
 #pragma unroll
     for (int b = 0; b < MB; ++b) xrow[b] = X + int64_t(min(16 * b + (lane & 15), M - 1)) * ldx + kb;
@@ -1484,65 +1509,118 @@ __global__ __launch_bounds__(NW * 64) void gemm_i8_skinny_kernel(
     // the wave's t-th step (pairing consecutive steps in one wave, so it reads
     // both halves of a 128-byte row segment back to back, measured slower)
     auto stepidx = [&](int t) { return wave + NW * t; };
-    v4i wbuf[D], xbuf[D][MB];
+    v4i wbuf[D][NB], xbuf[D][MB];
     auto load = [&](int slot, int step) {
         const int k = step * 64;
         if (step < S && k + kb < K) {
-            wbuf[slot] = *reinterpret_cast<const v4i*>(wrow + k);
+#pragma unroll
+            for (int p = 0; p < NB; ++p) wbuf[slot][p] = *reinterpret_cast<const v4i*>(wrow[p] + k);
 #pragma unroll
             for (int b = 0; b < MB; ++b) xbuf[slot][b] = *reinterpret_cast<const v4i*>(xrow[b] + k);
         } else {
-            wbuf[slot] = v4i{0, 0, 0, 0};
+#pragma unroll
+            for (int p = 0; p < NB; ++p) wbuf[slot][p] = v4i{0, 0, 0, 0};
 #pragma unroll
             for (int b = 0; b < MB; ++b) xbuf[slot][b] = v4i{0, 0, 0, 0};
         }
     };
-    v4i acc[MB];
+    v4i acc[NB][MB];
 #pragma unroll
-    for (int b = 0; b < MB; ++b) acc[b] = v4i{0, 0, 0, 0};
+    for (int p = 0; p < NB; ++p)
+#pragma unroll
+        for (int b = 0; b < MB; ++b) acc[p][b] = v4i{0, 0, 0, 0};
 #pragma unroll
     for (int j = 0; j < D; ++j) load(j, stepidx(j));
     for (int s0 = 0; stepidx(s0) < S; s0 += D) {
 #pragma unroll
         for (int j = 0; j < D; ++j) {
 #pragma unroll
-            for (int b = 0; b < MB; ++b)
-                acc[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wbuf[j], xbuf[j][b], acc[b], 0, 0, 0);
+            for (int p = 0; p < NB; ++p)
+#pragma unroll
+                for (int b = 0; b < MB; ++b)
+                    acc[p][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wbuf[j][p], xbuf[j][b],
+                                                                      acc[p][b], 0, 0, 0);
             load(j, stepidx(s0 + j + D));
         }
     }
 #pragma unroll
-    for (int b = 0; b < MB; ++b) part[wave][b][lane] = acc[b];
-    __syncthreads();
-    // wave w finishes m-blocks w, w+NW, ...: lane l holds rows 4*(l/16)+i of
-    // the weight block (n) for x row l%16 (m)
-    for (int b = wave; b < MB; b += NW) {
-        v4i v = part[0][b][lane];
+    for (int p = 0; p < NB; ++p)
 #pragma unroll
-        for (int w = 1; w < NW; ++w) v += part[w][b][lane];
-        const int m = 16 * b + (lane & 15);
-        const int n = n0 + 4 * (lane >> 4);
-        if (m < M && n < N) epi(m, n, v);
+        for (int b = 0; b < MB; ++b) part[wave][p * MB + b][lane] = acc[p][b];
+    __syncthreads();
+    // lane l holds rows 4*(l/16)+i of a weight block (n) for x row l%16 (m)
+    if constexpr (PAIRED) {
+        // wave w finishes m-blocks w, w+NW, ...: both halves in one lane
+        for (int b = wave; b < MB; b += NW) {
+            v4i v = part[0][b][lane], v2 = part[0][MB + b][lane];
+#pragma unroll
+            for (int w = 1; w < NW; ++w) {
+                v += part[w][b][lane];
+                v2 += part[w][MB + b][lane];
+            }
+            const int m = 16 * b + (lane & 15);
+            const int n = n0 + 4 * (lane >> 4);
+            if (m < M && n < N) epi.pair(m, n, v, v2);
+        }
+    } else {
+        // wave w finishes (weight block, m-block) pairs w, w+NW, ...
+        for (int t = wave; t < NB * MB; t += NW) {
+            v4i v = part[0][t][lane];
+#pragma unroll
+            for (int w = 1; w < NW; ++w) v += part[w][t][lane];
+            const int m = 16 * (t % MB) + (lane & 15);
+            const int n = n0 + 16 * (t / MB) + 4 * (lane >> 4);
+            if (m < M && n < N) epi(m, n, v);
+        }
     }
 }
 
-template <class Epi>
+// The skinny kernel over a (ceil(N / 16NB), nsl) grid (nsl > 1: K slices of
+// an EpiSliceI32, K being the slice's length) with NW waves by the number of
+// K steps.  M <= 64 for any epilogue; up to 128 (8 m-blocks) for a paired or
+// slice epilogue.
+template <int NB, class Epi>
 hipError_t launch_skinny(hipStream_t st, const int8_t* X, int64_t ldx, const int8_t* W,
-                         int64_t ldw, int M, int N, int K, const Epi& epi) {
-    const dim3 grid(unsigned((N + 15) / 16));
+                         int64_t ldw, int M, int N, int K, const Epi& epi, int nsl = 1) {
+    constexpr bool kWide = Epi::kPaired || IsSliceEpi<Epi>::value;
+    const int cols = Epi::kPaired ? 16 : 16 * NB;
+    const dim3 grid(unsigned((N + cols - 1) / cols), unsigned(nsl));
     const int S = (K + 63) / 64;
     auto go = [&](auto NWc) {
         constexpr int NWV = decltype(NWc)::value;
         const dim3 block(NWV * 64);
+#define XPU_SKINNY(MBV)                                                                         \
+    hipLaunchKernelGGL((gemm_i8_skinny_kernel<MBV, NWV, NB, Epi>), grid, block, 0, st, X, ldx, W, \
+                       ldw, M, N, K, epi)
         switch ((M + 15) / 16) {
-            case 1: hipLaunchKernelGGL((gemm_i8_skinny_kernel<1, NWV, Epi>), grid, block, 0, st, X, ldx, W, ldw, M, N, K, epi); break;
-            case 2: hipLaunchKernelGGL((gemm_i8_skinny_kernel<2, NWV, Epi>), grid, block, 0, st, X, ldx, W, ldw, M, N, K, epi); break;
-            case 3: hipLaunchKernelGGL((gemm_i8_skinny_kernel<3, NWV, Epi>), grid, block, 0, st, X, ldx, W, ldw, M, N, K, epi); break;
-            default: hipLaunchKernelGGL((gemm_i8_skinny_kernel<4, NWV, Epi>), grid, block, 0, st, X, ldx, W, ldw, M, N, K, epi); break;
+            case 1: XPU_SKINNY(1); break;
+            case 2: XPU_SKINNY(2); break;
+            case 3: XPU_SKINNY(3); break;
+            case 4: XPU_SKINNY(4); break;
+            default:
+                if constexpr (kWide) {
+                    switch ((M + 15) / 16) {
+                        case 5: XPU_SKINNY(5); break;
+                        case 6: XPU_SKINNY(6); break;
+                        case 7: XPU_SKINNY(7); break;
+                        default: XPU_SKINNY(8); break;
+                    }
+                } else {
+                    XPU_SKINNY(4);
+                }
+                break;
         }
+#undef XPU_SKINNY
     };
-    if (S >= 64) go(std::integral_constant<int, 16>{});
-    else if (S >= 32) go(std::integral_constant<int, 8>{});
+    // two weight blocks per step (paired or NB = 2): at most 8 waves (LDS for
+    // the partial sums: NW x NB*MB x 1 KB)
+    if constexpr (NB == 1 && !kWide) {
+        if (S >= 64) {
+            go(std::integral_constant<int, 16>{});
+            return hipGetLastError();
+        }
+    }
+    if (S >= 32) go(std::integral_constant<int, 8>{});
     else go(std::integral_constant<int, 4>{});
     return hipGetLastError();
 }
@@ -1554,12 +1632,16 @@ hipError_t launch_skinny(hipStream_t st, const int8_t* X, int64_t ldx, const int
 // gives at least 192 tiles; otherwise the small one (128 x 128, 4 waves of
 // 64 x 64, four stages); M <= 64 takes the weight-streaming skinny kernel;
 // a narrow output with K >= 2048 (too few large tiles) the split-K kernel.
-// Paired epilogues take the ping-pong tile (as 4 x 2 waves) or the large one.
+// Paired epilogues take the skinny kernel at M <= 64, else the ping-pong tile
+// (as 4 x 2 waves) or the large one.
+constexpr int kSkinnyPairedM = 128;
+
 template <class Epi>
 hipError_t launch_gemm(hipStream_t st, const int8_t* X, int64_t ldx, const int8_t* W, int64_t ldw,
                        int M, int N, int K, const Epi& epi) {
     constexpr int BM = 256, BN = 160, STAGES = 2;
     if constexpr (Epi::kPaired) {
+        if (M <= kSkinnyPairedM) return launch_skinny<2>(st, X, ldx, W, ldw, M, N, K, epi);
         // the ping-pong tile, 4 x 2 waves of 64 x 160 (five whole pairs each),
         // when it gives one tile per CU (5% faster at the FFN up-projection)
         const int tm = (M + BM - 1) / BM, tn_pp = (N + 159) / 160;
@@ -1585,7 +1667,7 @@ hipError_t launch_gemm(hipStream_t st, const int8_t* X, int64_t ldx, const int8_
                                tm, tn, epi);
         return hipGetLastError();
     } else {
-        if (M <= 64) return launch_skinny(st, X, ldx, W, ldw, M, N, K, epi);
+        if (M <= 64) return launch_skinny<1>(st, X, ldx, W, ldw, M, N, K, epi);
         const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
         if constexpr (Epi::kStaged) {
             // narrow output, long K: split K inside 128 x 160 tiles instead
@@ -1619,11 +1701,12 @@ hipError_t launch_gemm(hipStream_t st, const int8_t* X, int64_t ldx, const int8_
 }
 
 // ------------------------------------------------------- standalone dequant
-// A block converts DQ_COLS columns of one row: lane t of the block takes four
-// columns at 4t + 1024u (u < DQ_U), so each wave-wide 16-byte load covers
-// 1 KB of the accumulator row without gaps and each 8-byte store 512 bytes of
-// the output row.  The (row, column block) pair of a block is one scalar
-// division per block; blocks stride over the M * ceil(N / DQ_COLS) pairs.
+// A block of T threads converts 4TU columns of one row: lane t takes four
+// columns at 4t + 4Tu (u < U), so each wave-wide 16-byte load covers 1 KB of
+// the accumulator row without gaps and each 8-byte store 512 bytes of the
+// output row.  The (row, column block) pair of a block is one scalar division
+// per block; blocks stride over the M * ceil(N / 4TU) pairs.  T = 256 and
+// U = DQ_U (DQ_COLS columns) by default.
 // (Measured at M = 4096, cold: 2 slots per block were fastest or within 2% at
 // N = 1280, 5120 and 10240; 1 slot was 5-18% slower there, up to 4 slots 16%
 // slower at N = 5120; 1 slot was 1 us faster at N = 3072.)
@@ -1633,34 +1716,39 @@ hipError_t launch_gemm(hipStream_t st, const int8_t* X, int64_t ldx, const int8_
 // (bias16, widened exactly) or absent.
 constexpr int DQ_U = 2, DQ_COLS = 256 * 4 * DQ_U;
 
-__global__ __launch_bounds__(256) void dequant_kernel(const int32_t* __restrict__ acc,
-                                                     int64_t acc_ld, uint16_t* __restrict__ out,
-                                                     const float* __restrict__ xs,
-                                                     const float* __restrict__ ws,
-                                                     const float* __restrict__ bias,
-                                                     const uint16_t* __restrict__ bias16,
-                                                     int64_t M, int64_t N, int nsl,
-                                                     int64_t sl_stride) {
-    const int64_t chunks = (N + DQ_COLS - 1) / DQ_COLS, tasks = M * chunks;
+// Few rows (fewer than two default blocks per CU: the sum of K slices of a
+// small batch) take T = 64, U = 1, 256 columns a block, so that more blocks
+// share the slices' loads (M=200, N=1280, 8 slices: 21.2 -> 19.1 us for the
+// whole linear).
+template <int T, int U>
+__global__ __launch_bounds__(T) void dequant_kernel(const int32_t* __restrict__ acc,
+                                                   int64_t acc_ld, uint16_t* __restrict__ out,
+                                                   const float* __restrict__ xs,
+                                                   const float* __restrict__ ws,
+                                                   const float* __restrict__ bias,
+                                                   const uint16_t* __restrict__ bias16, int64_t M,
+                                                   int64_t N, int nsl, int64_t sl_stride) {
+    constexpr int COLS = 4 * T * U, STEP = 4 * T;
+    const int64_t chunks = (N + COLS - 1) / COLS, tasks = M * chunks;
     for (int64_t bt = blockIdx.x; bt < tasks; bt += gridDim.x) {
         const int64_t m = bt / chunks;
-        const int64_t c0 = (bt - m * chunks) * DQ_COLS + 4 * int64_t(threadIdx.x);
+        const int64_t c0 = (bt - m * chunks) * COLS + 4 * int64_t(threadIdx.x);
         const int32_t* pa = acc + m * acc_ld;
         uint16_t* po = out + m * N;
         const float x = xs[m];
-        i32x4 a[DQ_U];
+        i32x4 a[U];
 #pragma unroll
-        for (int u = 0; u < DQ_U; ++u)
-            if (c0 + 1024 * u < N) a[u] = load16_i(pa + c0 + 1024 * u);
+        for (int u = 0; u < U; ++u)
+            if (c0 + STEP * u < N) a[u] = load16_i(pa + c0 + STEP * u);
 #pragma unroll 2
         for (int sl = 1; sl < nsl; ++sl) {
 #pragma unroll
-            for (int u = 0; u < DQ_U; ++u)
-                if (c0 + 1024 * u < N) a[u] += load16_i(pa + sl * sl_stride + c0 + 1024 * u);
+            for (int u = 0; u < U; ++u)
+                if (c0 + STEP * u < N) a[u] += load16_i(pa + sl * sl_stride + c0 + STEP * u);
         }
 #pragma unroll
-        for (int u = 0; u < DQ_U; ++u) {
-            const int64_t c = c0 + 1024 * u;
+        for (int u = 0; u < U; ++u) {
+            const int64_t c = c0 + STEP * u;
             if (c >= N) break;
             const float4 w = ws ? *reinterpret_cast<const float4*>(ws + c)
                                 : make_float4(1.f, 1.f, 1.f, 1.f);
@@ -1757,15 +1845,38 @@ bool splitk_applies(int M, int N, int K) {
 // 128 x 128 kernel, whose narrower tiles give more blocks per slice
 static bool slices_small_tiles(int M) { return M <= 256; }
 
-// K slices for a split of the product across blocks, when the output has
-// fewer 128 x 160 tiles than the split-K kernel takes (128): the fewest
-// power-of-two slices that give at least 192 blocks, each slice at least 1024
-// long and a whole number of 64-byte steps; 0 when no split applies (M <= 64,
-// 128 tiles or more, or K too short).  (With 128-191 tiles the split-K kernel
+// K slices on the skinny kernel (two weight blocks per block, slices of at
+// least 1024) for batches of 33-128 rows: above 64 rows in place of the
+// 128 x 128 kernel, at 33-64 rows only where the unsplit skinny kernel has
+// fewer than 128 blocks (N < 2048).  Measured cold, with the dequant pass
+// that adds the slices included: M=64, N=1280, K=5120 16.5 -> 12.5 us; M=100
+// 19.4 -> 14.5; M=128, N=4096, K=4096 22.8 -> 19.9; but M=1 7.8 -> 8.9 and
+// M=16 9.5 -> 9.9 (N=1280, K=5120), M=48, N=3072, K=3072 10.7 -> 11.7.
+// Slices of 512 were 1.5-2.5 us slower than slices of 1024 at M=64-128, and
+// one weight block per block 0.5-20 us slower.
+constexpr int kSkinnySliceNB = 2, kSkinnySliceMin = 1024;
+// The skinny kernel's slice count: the fewest (power of two) that give at
+// least 256 blocks; 0 when it does not apply or no split fits.
+static int skinny_slices(int M, int N, int K) {
+    if (M <= 32 || M > 128 || (M <= 64 && N >= 2048) || K % 64 != 0) return 0;
+    const int64_t blocks = (N + 16 * kSkinnySliceNB - 1) / (16 * kSkinnySliceNB);
+    int s = 1;
+    while (blocks * s < 256 && (K / 64) % (2 * s) == 0 && K / (2 * s) >= kSkinnySliceMin) s *= 2;
+    return s > 1 ? s : 0;
+}
+
+// K slices for a split of the product across blocks: the skinny kernel's
+// (above) where they apply; else, when the output has fewer 128 x 160 tiles
+// than the split-K kernel takes (128) and M > 64, the fewest power-of-two
+// slices that give at least 192 blocks, each slice at least 1024 long (512 on
+// the 128 x 128 kernel, M <= 256) and a whole number of 64-byte steps; 0 when
+// no split applies (128 tiles or more, or K too short).  (With 128-191 tiles the split-K kernel
 // alone measured faster: 28.8 against 41.2 us at M=2100, N=1296, K=2304, and
 // 1 us at M=2048 and 4096 with 128 tiles.)
 int gemm_slices(int M, int N, int K) {
-    if (M <= 64 || K % 64 != 0) return 0;
+    if (K % 64 != 0) return 0;
+    if (const int s = skinny_slices(M, N, K)) return s;
+    if (M <= 64) return 0;
     const int64_t tiles = int64_t((M + 127) / 128) * ((N + 159) / 160);
     if (tiles >= 128) return 0;
     if (slices_small_tiles(M)) {
@@ -1780,11 +1891,14 @@ int gemm_slices(int M, int N, int K) {
     return s > 1 ? s : 0;
 }
 
-// The int32 partial products of nsl K slices, slice s at part + s * M * N
-// (row stride N): the split-K kernel over a (tiles, nsl) grid.
+// The int32 partial products of nsl = gemm_slices(M, N, K) K slices, slice s
+// at part + s * M * N (row stride N): the skinny, 128 x 128 or split-K kernel
+// over a (tiles, nsl) grid, as gemm_slices chose.
 hipError_t gemm_i32_slices(hipStream_t st, const int8_t* X, int64_t ldx, const int8_t* W,
                            int64_t ldw, int32_t* part, int M, int N, int K, int nsl) {
     const EpiSliceI32 epi{part, int64_t(N), int64_t(M) * N};
+    if (skinny_slices(M, N, K) == nsl)
+        return launch_skinny<kSkinnySliceNB>(st, X, ldx, W, ldw, M, N, K / nsl, epi, nsl);
     if (slices_small_tiles(M)) {
         const int tm = (M + 127) / 128, tn = (N + 127) / 128;
         hipLaunchKernelGGL((gemm_i8_kernel<128, 128, 2, 2, 4, EpiSliceI32>),
@@ -1893,10 +2007,16 @@ hipError_t dequant_slices(hipStream_t st, const int32_t* acc, int64_t acc_ld, in
                           int64_t sl_stride, void* out, const float* xs, const float* ws,
                           const float* bias, const uint16_t* bias16, int64_t M, int64_t N) {
     int64_t blocks = M * ((N + DQ_COLS - 1) / DQ_COLS);
-    if (blocks > (int64_t(1) << 20)) blocks = int64_t(1) << 20;
     if (blocks == 0) return hipSuccess;
-    hipLaunchKernelGGL(dequant_kernel, dim3(unsigned(blocks)), dim3(256), 0, st, acc, acc_ld,
-                       static_cast<uint16_t*>(out), xs, ws, bias, bias16, M, N, nsl, sl_stride);
+    uint16_t* o = static_cast<uint16_t*>(out);
+    if (blocks < 2 * device_cus()) {
+        hipLaunchKernelGGL((dequant_kernel<64, 1>), dim3(unsigned(M * ((N + 255) / 256))), dim3(64),
+                           0, st, acc, acc_ld, o, xs, ws, bias, bias16, M, N, nsl, sl_stride);
+        return hipGetLastError();
+    }
+    if (blocks > (int64_t(1) << 20)) blocks = int64_t(1) << 20;
+    hipLaunchKernelGGL((dequant_kernel<256, DQ_U>), dim3(unsigned(blocks)), dim3(256), 0, st, acc,
+                       acc_ld, o, xs, ws, bias, bias16, M, N, nsl, sl_stride);
     return hipGetLastError();
 }
 

@@ -72,6 +72,8 @@ def _signatures():
         "xpuint8_linear_workspace_size": ([i64] * 3, i64),
         "xpuint8_linear_gemm_residual_stream": ([vp] * 6 + [i32] + [vp] * 3 + [i64] * 3, c_int),
         "xpuint8_ffn_up_stream": ([vp] * 6 + [i64] * 3 + [i32], c_int),
+        "xpuint8_ffn_stream": ([vp] * 7 + [i32, vp] + [i64] * 3 + [i32, vp, i64], c_int),
+        "xpuint8_ffn_workspace_size": ([i64] * 3 + [i32], i64),
         "xpuint8_dx_gemm_stream": ([vp] * 5 + [i64] * 3 + [vp], c_int),
         "xpuint8_linear_dx_int8_stream": ([vp] * 5 + [i64] * 3 + [vp, i64], c_int),
         "xpuint8_linear_dx_int8_workspace_size": ([i64] * 3, i64),

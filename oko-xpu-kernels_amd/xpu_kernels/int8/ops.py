@@ -625,11 +625,13 @@ def ffn(x, up_w8, up_scale, down_w8, down_scale, down_bias=None, act="situ"):
     (``[hidden | gate]``) for a paired activation and [ffn, K] for
     ``gelu_erf``; ``down_w8`` is [K, ffn].  The up projection is unbiased.
 
-    Four kernels: rotate+quantize of x; the up-projection GEMM whose epilogue
-    dequantizes each half and applies the activation, writing the bf16
-    activation [M, ffn] (its hidden and gate columns are computed in the same
-    lanes); rotate+quantize of that; the down-projection GEMM with the dequant
-    (+bias) epilogue.  The codes equal the reference's fused
+    One library call (xpuint8_ffn_stream) of four kernels: rotate+quantize of
+    x; the up-projection GEMM whose epilogue dequantizes each half and
+    applies the activation, writing the bf16 activation [M, ffn] (its hidden
+    and gate columns are computed in the same lanes); rotate+quantize of
+    that; the down-projection GEMM with the dequant (+bias) epilogue (at small
+    M split in K across blocks, with one more kernel that adds the slices).
+    The codes equal the reference's fused
     dequant+activation+quantize of the int32 accumulator bit for bit (the
     bf16 activation is exactly the value that kernel forms), without writing
     the [M, 2*ffn] int32 accumulator."""
@@ -676,19 +678,23 @@ def ffn(x, up_w8, up_scale, down_w8, down_scale, down_bias=None, act="situ"):
         x2 = x2.contiguous()
 
     lib = _lib()
-    xq, xs = quantize(x2)
     uw8 = _c(up_w8)
     us = expand_scale(up_scale, n, device)
-    v = torch.empty((m, inner), device=device, dtype=torch.bfloat16)
-    rc = lib.xpuint8_ffn_up_stream(_stream(device), _ptr(xq), _ptr(xs), _ptr(uw8), _ptr(us),
-                                   _ptr(v), m, inner, k, ACTIVATIONS[act])
-    if rc != 0:
-        _err(lib, "ffn (up projection)")
     dw8 = _c(down_w8)
     ds = expand_scale(down_scale, k, device)
     b, b16 = _bias_arg(down_bias, k, device)
-    # rotate+quantize of the activation and the down-projection in one call
-    out = _linear_bf16(lib, v, dw8, ds, b, b16, m, k, inner)
+    code = ACTIVATIONS[act]
+    need = lib.xpuint8_ffn_workspace_size(m, inner, k, code)
+    if need < 0:
+        _err(lib, "ffn")
+    # the four (five) kernels in one library call, the intermediates in `work`
+    work = torch.empty(int(need), device=device, dtype=torch.uint8)
+    out = torch.empty((m, k), device=device, dtype=torch.bfloat16)
+    rc = lib.xpuint8_ffn_stream(_stream(device), _ptr(x2), _ptr(uw8), _ptr(us), _ptr(dw8),
+                                _ptr(ds), _opt(b), b16, _ptr(out), m, inner, k, code,
+                                _ptr(work), int(need))
+    if rc != 0:
+        _err(lib, "ffn")
     out = out.reshape(*x.shape[:-1], k)
     return out if input_dtype == torch.bfloat16 else out.to(dtype=input_dtype)
 

@@ -537,12 +537,15 @@ def test_linear_dispatch_sweep(dev, m, n, k):
 
 
 # Too few 128 x 160 output tiles for the chip: the product split in K across
-# blocks (4, 4 and 4 slices through the split-K kernel; 32, 8 and 2 through
-# the 128 x 128 kernel for M <= 256), the int32 partial sums added by the
-# dequant pass; ragged row and column tiles; with a bf16 bias, an fp32 bias
-# and none
+# blocks (4, 4 and 4 slices through the split-K kernel; 32 and 2 through the
+# 128 x 128 kernel for M <= 256; 2, 4, 4 and 2 through the skinny kernel for
+# 33 <= M <= 128, with 8, 4, 7 and 3 row blocks), the int32 partial sums
+# added by the dequant pass; ragged row and column tiles (1296 columns: a
+# half-empty last pair of weight blocks); with a bf16 bias, an fp32 bias and
+# none
 @pytest.mark.parametrize("m,n,k", [(1024, 1280, 5120), (2048, 640, 5120), (1000, 1296, 4096),
-                                   (200, 160, 16384), (128, 4096, 4096), (65, 4080, 1024)])
+                                   (200, 160, 16384), (128, 4096, 4096), (65, 4080, 1024),
+                                   (64, 1280, 5120), (100, 1296, 5120), (33, 1040, 2048)])
 def test_linear_k_slices_exact(dev, m, n, k):
     x = activation(m, k, seed=m + 2 * k, n_out=4, mult=25.0)
     w = weight(n, k, seed=n + 3)
@@ -557,12 +560,19 @@ def test_linear_k_slices_exact(dev, m, n, k):
                                                mismatch(bits(y), want))
 
 
-# Each side of every threshold of the linear's GEMM choice: M = 64 / 65 (skinny
-# kernel / K slices on the 128 x 128 kernel), M = 256 / 257 (slices on the
-# 128 x 128 / split-K kernel), 104 tiles of 128 x 160 (slices), exactly 128
-# tiles (the split-K kernel) at K = 1024, 1280 and 2048, and 17 tiles with
-# K = 1280 (too short to split: the 128 x 128 kernel); ragged N
-@pytest.mark.parametrize("m,n,k", [(64, 1280, 2048), (65, 1280, 2048), (256, 2560, 1024),
+# Each side of every threshold of the linear's GEMM choice: M = 32 / 33
+# (skinny kernel / K slices on it), N = 2048 / 2032 at M = 64 (the skinny
+# kernel whole / in K slices), M = 64 / 65 at N = 2048 (skinny kernel / K
+# slices on it), M = 128 / 129 (slices on the skinny / 128 x 128 kernel), no
+# skinny slice of 1024 at M = 128, N = 5120, K = 1280 (slices on the 128 x 128
+# kernel), M = 256 / 257 (slices on the 128 x 128 / split-K kernel), 104 tiles
+# of 128 x 160 (slices), exactly 128 tiles (the split-K kernel) at K = 1024,
+# 1280 and 2048, and 17 tiles with K = 1280 (too short to split: the
+# 128 x 128 kernel); ragged N
+@pytest.mark.parametrize("m,n,k", [(32, 1280, 2048), (33, 1280, 2048), (64, 2048, 2048),
+                                   (64, 2032, 2048), (65, 2048, 2048), (128, 1280, 4096),
+                                   (129, 1280, 4096), (128, 5120, 1280),
+                                   (64, 1280, 2048), (65, 1280, 2048), (256, 2560, 1024),
                                    (257, 2560, 2048), (1016, 2032, 2048), (1024, 2560, 1024),
                                    (1024, 2560, 2048), (2048, 1264, 1280), (2048, 1264, 1024),
                                    (2176, 160, 1280)])
@@ -599,11 +609,14 @@ def test_ffn_geglu_exact(dev):
     assert np.array_equal(bits(y), want), mismatch(bits(y), want)
 
 
-@pytest.mark.parametrize("m", [200, 1024])
+@pytest.mark.parametrize("m", [1, 64, 128, 200, 1024])
 def test_ffn_small_batch_k_slices_exact(dev, m):
     """An FFN whose down-projection (K = 5120, N = 1280) has too few output
-    tiles to fill the chip: the product is split in K across blocks (8 slices
-    on the 128 x 128 kernel at M = 200, 4 on the split-K kernel at M = 1024)."""
+    tiles to fill the chip: the product is split in K across blocks (4 slices
+    on the skinny kernel at M = 64 and 128, 8 on the 128 x 128 kernel at
+    M = 200, 4 on the split-K kernel at M = 1024; the skinny kernel whole at
+    M = 1).  Up to M = 128 the up-projection takes the skinny kernel with the
+    hidden and gate rows in one block."""
     k, inner = 1280, 5120
     x = activation(m, k, seed=11 + m)
     up8, ups = int8.prepare_weight(weight(2 * inner, k, seed=12).to(dev))
@@ -614,12 +627,42 @@ def test_ffn_small_batch_k_slices_exact(dev, m):
     assert np.array_equal(bits(y), want), mismatch(bits(y), want)
 
 
+def test_ffn_stream_dirty_workspace_exact(dev):
+    """xpuint8_ffn_stream through the C ABI on a workspace full of 0xFF, with a
+    bf16 bias, then again on the same (now used) workspace with a smaller M.
+    The down-projection is split in K across blocks in both (2 slices on the
+    split-K kernel at M = 1000, 4 on the 128 x 128 kernel at M = 130); both
+    equal the oracle."""
+    k, inner = 1280, 2048
+    up8, ups = int8.prepare_weight(weight(2 * inner, k, seed=21).to(dev))
+    dn8, dns = int8.prepare_weight(weight(k, inner, seed=22).to(dev))
+    db = weight(1, k, seed=23, std=0.01)[0].to(dev)
+    lib = L._lib()
+    need = lib.xpuint8_ffn_workspace_size(1000, inner, k, 4)
+    work = torch.full((need,), 255, device=dev, dtype=torch.uint8)
+    for m in (1000, 130):
+        assert lib.xpuint8_ffn_workspace_size(m, inner, k, 4) <= need
+        x = activation(m, k, seed=24 + m).to(dev)
+        out = torch.empty((m, k), device=dev, dtype=torch.bfloat16)
+        rc = lib.xpuint8_ffn_stream(L._stream(dev), L._ptr(x), L._ptr(up8), L._ptr(ups),
+                                    L._ptr(dn8), L._ptr(dns), L._ptr(db), 1, L._ptr(out), m,
+                                    inner, k, 4, L._ptr(work), need)
+        assert rc == 0, lib.xpuint8_last_error()
+        want = O.ffn(bits(x.cpu()), npy(up8), npy(ups), npy(dn8), npy(dns),
+                     O.bf16_to_f32(bits(db.cpu())), act=4)
+        assert np.array_equal(bits(out), want), (m, mismatch(bits(out), want))
+
+
 @pytest.mark.parametrize("act", [3, 4, 5])
-@pytest.mark.parametrize("m,inner,k", [(300, 512, 1280), (64, 1280, 1040), (512, 256, 256)])
+@pytest.mark.parametrize("m,inner,k", [(300, 512, 1280), (64, 1280, 1040), (512, 256, 256),
+                                       (1, 512, 1280), (17, 768, 256), (40, 256, 4096),
+                                       (100, 512, 1280), (128, 768, 1040)])
 def test_ffn_up_epilogue_exact(dev, act, m, inner, k):
     """The up-projection GEMM's activation epilogue against the oracle's
     dequant_act of the int32 product (ragged M, a partial last column tile,
-    K not a multiple of 64)."""
+    K not a multiple of 64).  M <= 64 (M <= 128 for the paired activations)
+    takes the weight-streaming skinny kernel (4 waves at K = 256 and
+    1040-1280, 8 at K = 4096)."""
     check_ffn_up(dev, act, m, inner, k)
 
 
@@ -770,12 +813,15 @@ def test_linear_dx_int8_split_k_shapes(dev, m, n, k):
     assert np.array_equal(bits(dx), want), mismatch(bits(dx), want)
 
 
-@pytest.mark.parametrize("m,n,k", [(200, 5120, 1280), (1024, 5120, 1280), (300, 2560, 1024)])
+@pytest.mark.parametrize("m,n,k", [(200, 5120, 1280), (1024, 5120, 1280), (300, 2560, 1024),
+                                   (64, 5120, 1280), (100, 5120, 1280)])
 def test_linear_dx_int8_k_slices_exact(dev, m, n, k):
     """Small batches, too few output tiles for the chip: the contraction is
     split across blocks (8 slices on the 128 x 128 kernel through the
     transposed weight at M = 200; 4 and 2 slices on the split-K kernel
-    reading the weight as stored, the last with a ragged 160-column tile)."""
+    reading the weight as stored, the last with a ragged 160-column tile; 4
+    slices on the skinny kernel through the transposed weight at M = 64 and
+    100)."""
     dy = activation(m, n, seed=m + n, scale=1e-3, n_out=0)
     w8, ws = int8.prepare_weight(weight(n, k, seed=k + 1).to(dev))
     dx = int8.linear_dx_int8(dy.to(dev), w8, ws)

@@ -69,6 +69,12 @@ def _rc(lib, fn, *args):
     ("xpuint8_ffn_up_stream", (Z, P, P, P, P, P, 4, 512, 512, 2), 6, "activation"),
     ("xpuint8_ffn_up_stream", (Z, P, P, P, P, P, 4, 24, 512, 4), 2, "16"),
     ("xpuint8_ffn_up_stream", (Z, P, P, Z, P, P, 4, 512, 512, 4), 6, "null"),
+    ("xpuint8_ffn_stream", (Z, P, P, P, P, P, Z, 0, P, 4, 512, 512, 2, P, 1 << 24), 6, "activation"),
+    ("xpuint8_ffn_stream", (Z, P, P, P, P, P, Z, 0, P, 4, 400, 512, 4, P, 1 << 24), 3, "256"),
+    ("xpuint8_ffn_stream", (Z, P, P, P, P, P, Z, 0, P, 4, 512, 300, 4, P, 1 << 24), 3, "256"),
+    ("xpuint8_ffn_stream", (Z, P, P, P, Z, P, Z, 0, P, 4, 512, 512, 4, P, 1 << 24), 6, "null"),
+    ("xpuint8_ffn_stream", (Z, P, P, P, P, P, Z, 2, P, 4, 512, 512, 4, P, 1 << 24), 2, "bias_bf16"),
+    ("xpuint8_ffn_stream", (Z, P, P, P, P, P, Z, 0, P, 4, 512, 512, 4, P, 64), 2, "workspace_size"),
     ("xpuint8_dx_gemm_stream", (Z, P, P, P, P, 4, 24, 512, P), 2, "16"),
     ("xpuint8_linear_dx_int8_stream", (Z, P, P, P, P, 4, 32, 300, P, 1 << 20), 3, "256"),
     ("xpuint8_linear_dx_int8_stream", (Z, P, P, P, P, 4, 24, 512, P, 1 << 20), 2, "16"),
@@ -144,12 +150,23 @@ def test_dx_workspace_size(lib):
 
 
 def k_slices(m, n, k):
-    """The K slices of a product split across blocks: when the 128 x 160
-    output tiles number below 128, the fewest power-of-two slices giving at
-    least 192 blocks, each slice a whole number of 64-byte steps and at least
-    1024 long -- for m <= 256 counted in 128 x 128 tiles with slices down to
-    512 long; 0 when none applies (m <= 64 included)."""
-    if m <= 64 or k % 64:
+    """The K slices of a product split across blocks.  First the skinny
+    kernel's, for 33 <= m <= 128 (at m <= 64 only with n < 2048): the fewest
+    power-of-two slices giving at least 256 blocks of 32 output columns, each
+    slice a whole number of 64-byte steps and at least 1024 long.  Otherwise,
+    when the 128 x 160 output tiles number below 128, the fewest power-of-two
+    slices giving at least 192 blocks, each slice a whole number of 64-byte
+    steps and at least 1024 long -- for m <= 256 counted in 128 x 128 tiles
+    with slices down to 512 long; 0 when none applies (m <= 64 included)."""
+    if k % 64:
+        return 0
+    if 32 < m <= 128 and (m > 64 or n < 2048):
+        blocks, s = -(-n // 32), 1
+        while blocks * s < 256 and (k // 64) % (2 * s) == 0 and k // (2 * s) >= 1024:
+            s *= 2
+        if s > 1:
+            return s
+    if m <= 64:
         return 0
     tiles = -(-m // 128) * -(-n // 160)
     if tiles >= 128:
@@ -184,8 +201,9 @@ def test_linear_workspace_size(lib):
     entry point rejects."""
     shapes = [(4096, 1280, 5120), (4096, 10240, 1280), (3, 16, 256), (2100, 1296, 2304),
               (1024, 1280, 5120), (2048, 640, 5120), (1000, 1296, 4096), (1024, 1280, 1280),
-              (128, 4096, 4096), (200, 160, 16384), (65, 4096, 1024)]
-    assert [k_slices(*s) for s in shapes] == [0, 0, 0, 0, 4, 4, 4, 0, 8, 32, 2]
+              (128, 4096, 4096), (200, 160, 16384), (65, 4096, 1024), (64, 1280, 5120),
+              (100, 1280, 5120), (48, 3072, 3072), (16, 1280, 5120), (128, 5120, 1280)]
+    assert [k_slices(*s) for s in shapes] == [0, 0, 0, 0, 4, 4, 4, 0, 2, 32, 2, 4, 4, 0, 0, 2]
     for m, n, k in shapes:
         want = up256(max(m * k, tiled(m, k))) + 4 * m
         if k_slices(m, n, k):
@@ -194,3 +212,20 @@ def test_linear_workspace_size(lib):
     assert lib.xpuint8_linear_workspace_size(4, 32, 300) == -1
     assert lib.xpuint8_linear_workspace_size(4, 24, 512) == -1
     assert lib.xpuint8_linear_workspace_size(0, 32, 512) == -1
+
+
+def test_ffn_workspace_size(lib):
+    """The FFN's workspace: the bf16 [M, inner] activation rounded up to 256
+    bytes, then one region that holds x quantized (row-major, then its fp32
+    row scales from a 256-byte boundary) and afterwards the down-projection's
+    linear workspace, whichever is larger; -1 for a shape or an activation the
+    entry point rejects."""
+    for m, inner, k in [(4096, 5120, 1280), (128, 5120, 1280), (1, 256, 256), (200, 1024, 512),
+                        (4096, 10240, 2560), (64, 256, 4096)]:
+        region = max(up256(m * k) + 4 * m, lib.xpuint8_linear_workspace_size(m, k, inner))
+        for act in (3, 4, 5):
+            assert lib.xpuint8_ffn_workspace_size(m, inner, k, act) == up256(2 * m * inner) + region
+    assert lib.xpuint8_ffn_workspace_size(4, 512, 512, 2) == -1      # activation
+    assert lib.xpuint8_ffn_workspace_size(4, 400, 512, 3) == -1      # inner % 256
+    assert lib.xpuint8_ffn_workspace_size(4, 512, 300, 3) == -1      # K % 256
+    assert lib.xpuint8_ffn_workspace_size(0, 512, 512, 3) == -1
