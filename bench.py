@@ -366,6 +366,63 @@ def measure_side_rows(torch, int8, lib, L, st, dev, K, W, SET, extra, hbm_line, 
         log(f"[bench] int8_linear step ({mode} backward): {ms_st:.4f} ms")
 
 
+def measure_small_batch(torch, int8, lib, L, st, dev, K, W, SET, extra, dev_act, dev_weight):
+    """Small batches (batched decode) at config 4's widths, weights cold
+    (rotating sets of > 640 MB): the whole FFN (x [M,1280] -> GEGLU [M,5120]
+    -> [M,1280], bf16 bias) as one ``xpuint8_ffn_stream`` call and the linear
+    of its down-projection shape (K=5120, N=1280) as one
+    ``xpuint8_linear_stream`` call, both on preallocated buffers, and the
+    ``int8.ffn`` API call (host work included) beside them, at M = 1, 64, 128.
+    At these sizes the weights are most of the traffic (19.66 MB per FFN,
+    6.55 MB per linear); ``weights_GB/s`` is that over the call's time."""
+    k, f = 1280, 5120
+    nf = n_sets(3 * f * k)
+    ffw = [int8.prepare_weight(dev_weight(2 * f, k, 2000 + i)) + int8.prepare_weight(
+        dev_weight(k, f, 2100 + i)) for i in range(nf)]
+    bias = dev_weight(1, k, 2200, 0.01)[0]
+    res = {}
+    for m in (1, 64, 128):
+        x = dev_act(m, k, 2300 + m)
+        y = torch.empty((m, k), dtype=torch.bfloat16, device=dev)
+        need = lib.xpuint8_ffn_workspace_size(m, f, k, 4)
+        work = torch.empty(max(1, need), dtype=torch.uint8, device=dev)
+
+        def ffn(i):
+            up8, ups, dn8, dns = ffw[i % nf]
+            rc = lib.xpuint8_ffn_stream(st, L._ptr(x), L._ptr(up8), L._ptr(ups), L._ptr(dn8),
+                                        L._ptr(dns), L._ptr(bias), 1, L._ptr(y), m, f, k, 4,
+                                        L._ptr(work), need)
+            if rc != 0:
+                raise RuntimeError(lib.xpuint8_last_error().decode())
+        ms_ffn = timed(torch, ffn, K, W, SET)
+        ms_api = timed(torch, lambda i: int8.ffn(x, *ffw[i % nf], bias, act="geglu_erf"),
+                       K, W, SET)
+        xd = dev_act(m, f, 2400 + m)
+        yd = torch.empty((m, k), dtype=torch.bfloat16, device=dev)
+        needl = lib.xpuint8_linear_workspace_size(m, k, f)
+        workl = torch.empty(max(1, needl), dtype=torch.uint8, device=dev)
+
+        def down(i):
+            dn8, dns = ffw[i % nf][2:]
+            rc = lib.xpuint8_linear_stream(st, L._ptr(xd), L._ptr(dn8), L._ptr(dns),
+                                           L._ptr(bias), 1, L._ptr(yd), m, k, f,
+                                           L._ptr(workl), needl)
+            if rc != 0:
+                raise RuntimeError(lib.xpuint8_last_error().decode())
+        ms_lin = timed(torch, down, K, W, SET)
+        res[f"M{m}"] = {"ffn_ms_cold": round(ms_ffn, 5),
+                        "ffn_weights_GB/s": round(3 * f * k / (ms_ffn * 1e-3) / 1e9, 1),
+                        "ffn_api_ms_cold": round(ms_api, 5),
+                        "linear_k5120_n1280_ms_cold": round(ms_lin, 5),
+                        "linear_weights_GB/s": round(f * k / (ms_lin * 1e-3) / 1e9, 1)}
+        del work, workl
+    extra["small_batch_c4_widths"] = res
+    log("[bench] small batches: " + ", ".join(
+        f"M={m[1:]} ffn {v['ffn_ms_cold'] * 1e3:.1f} us (API {v['ffn_api_ms_cold'] * 1e3:.1f}), "
+        f"linear {v['linear_k5120_n1280_ms_cold'] * 1e3:.1f} us" for m, v in res.items()))
+    del ffw
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -385,6 +442,9 @@ def main():
                     help="only the entry points beside the path (linear_acc, residual, dequant, "
                          "dequant_slice, quantize_act, dequant_act_quantize, dequant_weight, "
                          "int8_linear step), for profiling")
+    ap.add_argument("--only-small", action="store_true",
+                    help="only the small-batch FFN and linear lines (M = 1, 64, 128 at config "
+                         "4's widths), for profiling")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run a plain copy kernel (torch neg over 256 MiB in and out, "
                          "exactly 256 MiB) so counter runs can scale FETCH_SIZE/WRITE_SIZE")
@@ -442,6 +502,11 @@ def main():
     x = activation(torch, M, Kd).to(dev)
     w8, ws = int8.prepare_weight(weight(torch, N, Kd).to(dev))
     bias = weight(torch, 1, N, seed=2, std=0.01)[0].to(dev)
+    if args.only_small:
+        measure_small_batch(torch, int8, lib, L, st, dev, K, W, SET, extra, dev_act, dev_weight)
+        print(json.dumps({"only_small": True, "steps": K, "warmup": W, "extra": extra}),
+              flush=True)
+        return
     if args.only_side:
         measure_side_rows(torch, int8, lib, L, st, dev, K, W, SET, extra, hbm_line, dev_gen,
                           dev_act, dev_weight, x, w8, ws, bias)
@@ -663,6 +728,7 @@ def main():
         log(f"[bench] rms+rope dequant: {ms_rope:.4f} / {ms_rope_warm:.4f} ms")
         measure_side_rows(torch, int8, lib, L, st, dev, K, W, SET, extra, hbm_line, dev_gen,
                           dev_act, dev_weight, x, w8, ws, bias)
+        measure_small_batch(torch, int8, lib, L, st, dev, K, W, SET, extra, dev_act, dev_weight)
 
     line = {
         "metric": "int8_linear TOPS (M=4096,K=1280,N=10240); rotate+quant HBM GB/s",
