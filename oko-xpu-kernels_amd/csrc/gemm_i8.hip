@@ -1472,17 +1472,24 @@ hipError_t launch_splitk(hipStream_t st, const int8_t* X, int64_t ldx, const int
 // four per wave): at M=16, N=4096 and K=4096 sixteen waves cut the cold call
 // from 8.7 to 7.2 us, while at K=1280 four waves stay fastest (6.8 us against
 // 7.7 with eight and 8.6 with sixteen).  A paired epilogue (the FFN's
-// up-projection) takes the same kernel with two weight blocks per step, rows
-// n and half + n, so that both operands of its activation meet in one lane.
+// up-projection) takes the same kernel with the rows n and half + n of each
+// output column block in the block, so that both operands of its activation
+// meet in one lane: two column blocks (four weight blocks) per block, which
+// at ffn = 5120, K = 1280 took 6.0 / 9.4 / 13.5 us cold at M = 1 / 64 / 128
+// against 6.3 / 11.2 / 16.5 with one (every block reads all of X, so fewer,
+// wider blocks read less of it).
 template <int MB, int NW, int NB, class Epi>
 __global__ __launch_bounds__(NW * 64) void gemm_i8_skinny_kernel(
     const int8_t* __restrict__ X, int64_t ldx, const int8_t* __restrict__ W, int64_t ldw, int M,
     int N, int K, Epi epi) {
     // NB weight blocks of 16 rows per block: rows n0 + 16p, or, for a paired
-    // epilogue (an FFN's up-projection), rows n0 and half + n0, the operands
-    // of the activation at output column n0
+    // epilogue (an FFN's up-projection), NB / 2 column blocks of both halves:
+    // rows n0 + 16c (p = c) and half + n0 + 16c (p = NB/2 + c), the operands of
+    // the activation at output columns n0 + 16c
     constexpr bool PAIRED = Epi::kPaired;
-    static_assert(!PAIRED || NB == 2, "a paired epilogue's halves are the two weight blocks");
+    constexpr int NC = PAIRED ? NB / 2 : NB;                 // output column blocks
+    static_assert(!PAIRED || NB % 2 == 0, "a paired epilogue takes both halves of each block");
+    static_assert(NW * NB * MB <= 160, "the partial sums fit in the CU's 160 KB of LDS");
     constexpr int D = NW >= 16 ? 4 : (MB * NB <= 2 ? 8 : (MB * NB <= 8 ? 4 : 2));  // steps in flight
     __shared__ v4i part[NW][NB * MB][64];
     // K slice blockIdx.y of a split across blocks (EpiSliceI32): K is the
@@ -1493,13 +1500,13 @@ __global__ __launch_bounds__(NW * 64) void gemm_i8_skinny_kernel(
     }
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int n0 = blockIdx.x * (PAIRED ? 16 : 16 * NB);
+    const int n0 = blockIdx.x * 16 * NC;
     const int kb = 16 * (lane >> 4);                         // lane's bytes within a step
     const int8_t* wrow[NB];
 #pragma unroll
     for (int p = 0; p < NB; ++p) {
-        const int r = PAIRED ? min(n0 + (lane & 15), N - 1) + (p ? pair_offset(epi) : 0)
-                             : min(n0 + 16 * p + (lane & 15), N - 1);
+        const int r = min(n0 + 16 * (p % NC) + (lane & 15), N - 1) +
+                      (p >= NC ? pair_offset(epi) : 0);
         wrow[p] = W + int64_t(r) * ldw + kb;
     }
     const int8_t* xrow[MB];
@@ -1550,16 +1557,17 @@ __global__ __launch_bounds__(NW * 64) void gemm_i8_skinny_kernel(
     __syncthreads();
     // lane l holds rows 4*(l/16)+i of a weight block (n) for x row l%16 (m)
     if constexpr (PAIRED) {
-        // wave w finishes m-blocks w, w+NW, ...: both halves in one lane
-        for (int b = wave; b < MB; b += NW) {
-            v4i v = part[0][b][lane], v2 = part[0][MB + b][lane];
+        // wave w finishes (column block, m-block) pairs w, w+NW, ...: both
+        // halves in one lane
+        for (int t = wave; t < NC * MB; t += NW) {
+            v4i v = part[0][t][lane], v2 = part[0][NC * MB + t][lane];
 #pragma unroll
             for (int w = 1; w < NW; ++w) {
-                v += part[w][b][lane];
-                v2 += part[w][MB + b][lane];
+                v += part[w][t][lane];
+                v2 += part[w][NC * MB + t][lane];
             }
-            const int m = 16 * b + (lane & 15);
-            const int n = n0 + 4 * (lane >> 4);
+            const int m = 16 * (t % MB) + (lane & 15);
+            const int n = n0 + 16 * (t / MB) + 4 * (lane >> 4);
             if (m < M && n < N) epi.pair(m, n, v, v2);
         }
     } else {
@@ -1583,7 +1591,7 @@ template <int NB, class Epi>
 hipError_t launch_skinny(hipStream_t st, const int8_t* X, int64_t ldx, const int8_t* W,
                          int64_t ldw, int M, int N, int K, const Epi& epi, int nsl = 1) {
     constexpr bool kWide = Epi::kPaired || IsSliceEpi<Epi>::value;
-    const int cols = Epi::kPaired ? 16 : 16 * NB;
+    const int cols = Epi::kPaired ? 8 * NB : 16 * NB;
     const dim3 grid(unsigned((N + cols - 1) / cols), unsigned(nsl));
     const int S = (K + 63) / 64;
     auto go = [&](auto NWc) {
@@ -1612,16 +1620,21 @@ hipError_t launch_skinny(hipStream_t st, const int8_t* X, int64_t ldx, const int
         }
 #undef XPU_SKINNY
     };
-    // two weight blocks per step (paired or NB = 2): at most 8 waves (LDS for
-    // the partial sums: NW x NB*MB x 1 KB)
+    // LDS for the partial sums is NW x NB*MB x 1 KB: 16 waves for one weight
+    // block and M <= 64, 8 for two weight blocks, 4 for four
     if constexpr (NB == 1 && !kWide) {
         if (S >= 64) {
             go(std::integral_constant<int, 16>{});
             return hipGetLastError();
         }
     }
-    if (S >= 32) go(std::integral_constant<int, 8>{});
-    else go(std::integral_constant<int, 4>{});
+    if constexpr (NB <= 2) {
+        if (S >= 32) {
+            go(std::integral_constant<int, 8>{});
+            return hipGetLastError();
+        }
+    }
+    go(std::integral_constant<int, 4>{});
     return hipGetLastError();
 }
 
@@ -1641,7 +1654,7 @@ hipError_t launch_gemm(hipStream_t st, const int8_t* X, int64_t ldx, const int8_
                        int M, int N, int K, const Epi& epi) {
     constexpr int BM = 256, BN = 160, STAGES = 2;
     if constexpr (Epi::kPaired) {
-        if (M <= kSkinnyPairedM) return launch_skinny<2>(st, X, ldx, W, ldw, M, N, K, epi);
+        if (M <= kSkinnyPairedM) return launch_skinny<4>(st, X, ldx, W, ldw, M, N, K, epi);
         // the ping-pong tile, 4 x 2 waves of 64 x 160 (five whole pairs each),
         // when it gives one tile per CU (5% faster at the FFN up-projection)
         const int tm = (M + BM - 1) / BM, tn_pp = (N + 159) / 160;
