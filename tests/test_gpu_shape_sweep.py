@@ -1,0 +1,105 @@
+"""Seeded random shapes over the whole dispatch space of the linear, the FFN and
+linear_dx_int8, each bit-exact against the oracle.
+
+The GEMM a call takes depends on M, N and K: the skinny kernel (M <= 64,
+M <= 128 for the FFN's paired up-projection), K slices on the skinny, the
+128 x 128 or the split-K kernel for outputs too small to fill the chip, the
+split-K kernel on the activation in MFMA-block order, the two-block and the
+persistent kernels.  The fixed-shape tests sit on each side of every
+threshold; these draw shapes between them (ragged M, N any multiple of 16, K
+any multiple of 256), so that no combination of tile remainders and slice
+counts goes untested.  Shapes are drawn once from fixed seeds and appear in
+the test ids.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from gpu_util import activation, bits, mismatch, npy, weight
+from xpu_kernels import int8
+
+pytestmark = pytest.mark.gpu
+
+
+def _draw_m(rng):
+    band = int(rng.integers(0, 4))
+    lo, hi = [(1, 65), (65, 129), (129, 513), (513, 2600)][band]
+    return int(rng.integers(lo, hi))
+
+
+def _linear_shapes(count, seed=20261202):
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < count:
+        m = _draw_m(rng)
+        n = 16 * int(rng.integers(1, 385))            # 16 .. 6144
+        k = 256 * int(rng.integers(1, 33))            # 256 .. 8192
+        if m * n * k <= 8e9:
+            out.append((m, n, k))
+    return out
+
+
+def _ffn_shapes(count, seed=20261203):
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < count:
+        m = _draw_m(rng)
+        k = 256 * int(rng.integers(1, 9))             # model width 256 .. 2048
+        inner = 256 * int(rng.integers(1, 17))        # 256 .. 4096
+        act = int(rng.choice([3, 4, 5]))
+        if m * inner * k <= 3e9:
+            out.append((m, k, inner, act))
+    return out
+
+
+def _dx_shapes(count, seed=20261204):
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < count:
+        m = _draw_m(rng)
+        n = 16 * int(rng.integers(1, 385))            # contraction 16 .. 6144
+        k = 256 * int(rng.integers(1, 21))            # output width 256 .. 5120
+        if m * n * k <= 4e9:
+            out.append((m, n, k))
+    return out
+
+
+LINEAR = _linear_shapes(30)
+FFN = _ffn_shapes(10)
+DX = _dx_shapes(10)
+
+
+@pytest.mark.parametrize("m,n,k", LINEAR, ids=[f"{m}x{n}x{k}" for m, n, k in LINEAR])
+def test_linear_random_shapes_exact(dev, m, n, k):
+    x = activation(m, k, seed=m + 7 * n + k, n_out=3, mult=25.0)
+    w8, ws = int8.prepare_weight(weight(n, k, seed=n + k).to(dev))
+    bias = weight(1, n, seed=n + 3 * k, std=0.01)[0]
+    y = int8.linear(x.to(dev), w8, ws, bias.to(dev))
+    want = O.linear(bits(x), npy(w8), npy(ws), O.bf16_to_f32(bits(bias)))
+    assert np.array_equal(bits(y), want), mismatch(bits(y), want)
+
+
+@pytest.mark.parametrize("m,k,inner,act", FFN,
+                         ids=[f"{m}x{k}x{inner}-act{a}" for m, k, inner, a in FFN])
+def test_ffn_random_shapes_exact(dev, m, k, inner, act):
+    name = {3: "situ", 4: "geglu_erf", 5: "gelu_erf"}[act]
+    rows = 2 * inner if act in O.PAIRED else inner
+    x = activation(m, k, seed=m + k + inner)
+    up8, ups = int8.prepare_weight(weight(rows, k, seed=inner + 1).to(dev))
+    dn8, dns = int8.prepare_weight(weight(k, inner, seed=inner + 2).to(dev))
+    db = weight(1, k, seed=k + 5, std=0.01)[0]
+    y = int8.ffn(x.to(dev), up8, ups, dn8, dns, db.to(dev), act=name)
+    want = O.ffn(bits(x), npy(up8), npy(ups), npy(dn8), npy(dns), O.bf16_to_f32(bits(db)),
+                 act=act)
+    assert np.array_equal(bits(y), want), mismatch(bits(y), want)
+
+
+@pytest.mark.parametrize("m,n,k", DX, ids=[f"{m}x{n}x{k}" for m, n, k in DX])
+def test_linear_dx_int8_random_shapes_exact(dev, m, n, k):
+    dy = activation(m, n, seed=m + n + 2 * k, scale=1e-3, n_out=0)
+    w8, ws = int8.prepare_weight(weight(n, k, seed=k + n).to(dev))
+    dx = int8.linear_dx_int8(dy.to(dev), w8, ws)
+    want = O.linear_dx_int8(bits(dy), npy(w8), npy(ws))
+    assert np.array_equal(bits(dx), want), mismatch(bits(dx), want)
