@@ -103,3 +103,83 @@ def test_linear_dx_int8_random_shapes_exact(dev, m, n, k):
     dx = int8.linear_dx_int8(dy.to(dev), w8, ws)
     want = O.linear_dx_int8(bits(dy), npy(w8), npy(ws))
     assert np.array_equal(bits(dx), want), mismatch(bits(dx), want)
+
+
+# ------------------------------------------------------------ row kernels
+# The row kernels pick their launch shape from K: rows per block (4, 2 or 1
+# for K = 256-2048, longer rows), one or two groups per lane (K up to 16384
+# or 32768), the two-pass kernel beyond; the quantize_row one also takes any
+# N % 16 (a partial last group).
+
+def _row_shapes(count, seed, kmax_groups, elems=3e7):
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < count:
+        g = int(rng.integers(1, kmax_groups + 1))
+        m = int(rng.integers(1, 3000))
+        if m * 256 * g <= elems:
+            out.append((m, 256 * g))
+    return out
+
+
+QUANT = _row_shapes(12, 20261205, 280)
+ACTQ = [(m, k, a) for (m, k), a in zip(_row_shapes(10, 20261206, 40, 1e7),
+                                       np.random.default_rng(7).integers(1, 6, 10).tolist())]
+QROW = [(m, 16 * int(n)) for m, n in zip(np.random.default_rng(8).integers(1, 2500, 10).tolist(),
+                                        np.random.default_rng(9).integers(1, 1200, 10).tolist())]
+WPREP = _row_shapes(6, 20261207, 40, 2e7)
+
+
+@pytest.mark.parametrize("m,k", QUANT, ids=[f"{m}x{k}" for m, k in QUANT])
+def test_quantize_and_rotate_random_shapes_exact(dev, m, k):
+    x = activation(m, k, seed=m + k)
+    q, s = int8.quantize(x.to(dev))
+    wq, ws = O.convrot_quantize(bits(x))
+    assert np.array_equal(npy(s).view(np.uint32), ws.view(np.uint32)), mismatch(npy(s), ws)
+    assert np.array_equal(npy(q), wq), mismatch(npy(q), wq)
+    got = bits(int8.rotate(x.to(dev)))
+    want = O.rotate_bf16(bits(x))
+    assert np.array_equal(got, want), mismatch(got, want)
+
+
+@pytest.mark.parametrize("m,k,act", ACTQ, ids=[f"{m}x{k}-act{a}" for m, k, a in ACTQ])
+def test_quantize_act_random_shapes_exact(dev, m, k, act):
+    name = {v: kk for kk, v in int8.ACTIVATIONS.items()}[act]
+    width = 2 * k if act in O.PAIRED else k
+    x = activation(m, width, seed=act + m + k, scale=1.5)
+    q, s = int8.quantize_act(x.to(dev), name)
+    wq, ws = O.quantize_act(bits(x), act)
+    assert np.array_equal(npy(s), ws), mismatch(npy(s), ws)
+    assert np.array_equal(npy(q), wq), mismatch(npy(q), wq)
+    if act in (3, 4, 5):
+        # the same activation from an int32 accumulator
+        rng = np.random.default_rng(m + k)
+        acc = rng.integers(-300000, 300000, (m, width)).astype(np.int32)
+        xs = rng.uniform(1e-3, 3e-2, m).astype(np.float32)
+        wsc = rng.uniform(1e-4, 1e-3, width).astype(np.float32)
+        t = lambda a: torch.from_numpy(a).to(dev)
+        q2, s2 = int8.dequant_act_quantize(t(acc), t(xs), t(wsc), name)
+        wq2, ws2 = O.dequant_act_quantize(acc, xs, wsc, act)
+        assert np.array_equal(npy(s2), ws2) and np.array_equal(npy(q2), wq2), \
+            mismatch(npy(q2), wq2)
+
+
+@pytest.mark.parametrize("m,n", QROW, ids=[f"{m}x{n}" for m, n in QROW])
+def test_quantize_row_random_shapes_exact(dev, m, n):
+    dy = activation(m, n, seed=m + n, scale=1e-3, n_out=0)
+    q, s = int8.quantize_row(dy.to(dev))
+    wq, ws = O.quantize_row(bits(dy))
+    assert np.array_equal(npy(s).view(np.uint32), ws.view(np.uint32))
+    assert np.array_equal(npy(q), wq), mismatch(npy(q), wq)
+
+
+@pytest.mark.parametrize("n,k", WPREP, ids=[f"{n}x{k}" for n, k in WPREP])
+def test_prepare_and_dequant_weight_random_shapes_exact(dev, n, k):
+    w = weight(n, k, seed=n + k)
+    q, s = int8.prepare_weight(w.to(dev))
+    wq, ws = O.prepare_weight(bits(w))
+    assert np.array_equal(npy(s).view(np.uint32), ws.view(np.uint32)), mismatch(npy(s), ws)
+    assert np.array_equal(npy(q), wq), mismatch(npy(q), wq)
+    got = bits(int8.dequant_weight(q, s))
+    want = O.dequant_weight(wq, ws)
+    assert np.array_equal(got, want), mismatch(got, want)
