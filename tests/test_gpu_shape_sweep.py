@@ -183,3 +183,49 @@ def test_prepare_and_dequant_weight_random_shapes_exact(dev, n, k):
     got = bits(int8.dequant_weight(q, s))
     want = O.dequant_weight(wq, ws)
     assert np.array_equal(got, want), mismatch(got, want)
+
+
+# ------------------------------------------------------- bf16 dense GEMMs
+# linear_dx (dy @ w) and linear_dw (dy^T @ x) in bf16: the split-K kernel,
+# K slices for small batches, the 128 x 128 TN / NN kernels for the shapes
+# the split-K kernel does not take (dims % 16 only).  Bar: each element
+# within one bf16 rounding of the float64 product plus the fp32 accumulation
+# error, 2^-8 |ref| + 2^-14 sum |a||b|.
+
+def _dense_shapes(count, seed):
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < count:
+        m = _draw_m(rng)
+        n = 16 * int(rng.integers(1, 320))
+        k = 16 * int(rng.integers(1, 320))
+        if m * n * k <= 4e9:
+            out.append((m, n, k))
+    return out
+
+
+DENSE = _dense_shapes(12, 20261208)
+
+
+def _bound_ok(got_bits, ref, mag):
+    got = O.bf16_to_f32(got_bits).astype(np.float64)
+    bound = 2.0 ** -8 * np.abs(ref) + 2.0 ** -14 * mag
+    err = np.abs(got - ref)
+    return bool(np.all(err <= bound)), float(np.max(err / np.maximum(bound, 1e-300)))
+
+
+@pytest.mark.parametrize("m,n,k", DENSE, ids=[f"{m}x{n}x{k}" for m, n, k in DENSE])
+def test_linear_dx_dw_random_shapes(dev, m, n, k):
+    g = torch.Generator().manual_seed(m + 3 * n + k)
+    dy = (torch.randn(m, n, generator=g) * 1e-3).to(torch.bfloat16)
+    w = (torch.randn(n, k, generator=g) * 0.02).to(torch.bfloat16)
+    x = torch.randn(m, k, generator=g).to(torch.bfloat16)
+    a_dy = np.abs(O.bf16_to_f32(bits(dy)).astype(np.float64))
+    dx = int8.linear_dx(dy.to(dev), w.to(dev))
+    ok, worst = _bound_ok(bits(dx), O.linear_dx(bits(dy), bits(w)),
+                          a_dy @ np.abs(O.bf16_to_f32(bits(w)).astype(np.float64)))
+    assert ok, ("dx", worst)
+    dw = int8.linear_dw(dy.to(dev), x.to(dev))
+    ok, worst = _bound_ok(bits(dw), O.linear_dw(bits(dy), bits(x)),
+                          a_dy.T @ np.abs(O.bf16_to_f32(bits(x)).astype(np.float64)))
+    assert ok, ("dw", worst)
