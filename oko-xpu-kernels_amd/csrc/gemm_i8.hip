@@ -1493,10 +1493,16 @@ __global__ __launch_bounds__(NW * 64) void gemm_i8_skinny_kernel(
     constexpr int D = NW >= 16 ? 4 : (MB * NB <= 2 ? 8 : (MB * NB <= 8 ? 4 : 2));  // steps in flight
     __shared__ v4i part[NW][NB * MB][64];
     // K slice blockIdx.y of a split across blocks (EpiSliceI32): K is the
-    // slice's length, the operands' rows keep their full strides
+    // slice's length, the operands' rows keep their full strides.  Otherwise
+    // blockIdx.y is a chunk of 16 * MB rows (batches above 128 rows)
+    int m_base = 0;
     if constexpr (IsSliceEpi<Epi>::value) {
         X += int64_t(blockIdx.y) * K;
         W += int64_t(blockIdx.y) * K;
+    } else {
+        m_base = int(blockIdx.y) * 16 * MB;
+        X += int64_t(m_base) * ldx;
+        M -= m_base;
     }
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -1568,7 +1574,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_i8_skinny_kernel(
             }
             const int m = 16 * (t % MB) + (lane & 15);
             const int n = n0 + 16 * (t / MB) + 4 * (lane >> 4);
-            if (m < M && n < N) epi.pair(m, n, v, v2);
+            if (m < M && n < N) epi.pair(m_base + m, n, v, v2);
         }
     } else {
         // wave w finishes (weight block, m-block) pairs w, w+NW, ...
@@ -1578,7 +1584,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_i8_skinny_kernel(
             for (int w = 1; w < NW; ++w) v += part[w][t][lane];
             const int m = 16 * (t % MB) + (lane & 15);
             const int n = n0 + 16 * (t / MB) + 4 * (lane >> 4);
-            if (m < M && n < N) epi(m, n, v);
+            if (m < M && n < N) epi(m_base + m, n, v);
         }
     }
 }
@@ -1586,13 +1592,16 @@ __global__ __launch_bounds__(NW * 64) void gemm_i8_skinny_kernel(
 // The skinny kernel over a (ceil(N / 16NB), nsl) grid (nsl > 1: K slices of
 // an EpiSliceI32, K being the slice's length) with NW waves by the number of
 // K steps.  M <= 64 for any epilogue; up to 128 (8 m-blocks) for a paired or
-// slice epilogue.
+// slice epilogue; a paired epilogue above 128 rows over a (ceil(N / 8NB),
+// ceil(M / 128)) grid of 128-row chunks.
 template <int NB, class Epi>
 hipError_t launch_skinny(hipStream_t st, const int8_t* X, int64_t ldx, const int8_t* W,
                          int64_t ldw, int M, int N, int K, const Epi& epi, int nsl = 1) {
     constexpr bool kWide = Epi::kPaired || IsSliceEpi<Epi>::value;
     const int cols = Epi::kPaired ? 8 * NB : 16 * NB;
-    const dim3 grid(unsigned((N + cols - 1) / cols), unsigned(nsl));
+    const int chunks = Epi::kPaired && M > 128 ? (M + 127) / 128 : 1;
+    const dim3 grid(unsigned((N + cols - 1) / cols), unsigned(chunks > 1 ? chunks : nsl));
+    const int mrows = chunks > 1 ? 128 : M;     // rows per block (the last chunk ragged)
     const int S = (K + 63) / 64;
     auto go = [&](auto NWc) {
         constexpr int NWV = decltype(NWc)::value;
@@ -1600,14 +1609,14 @@ hipError_t launch_skinny(hipStream_t st, const int8_t* X, int64_t ldx, const int
 #define XPU_SKINNY(MBV)                                                                         \
     hipLaunchKernelGGL((gemm_i8_skinny_kernel<MBV, NWV, NB, Epi>), grid, block, 0, st, X, ldx, W, \
                        ldw, M, N, K, epi)
-        switch ((M + 15) / 16) {
+        switch ((mrows + 15) / 16) {
             case 1: XPU_SKINNY(1); break;
             case 2: XPU_SKINNY(2); break;
             case 3: XPU_SKINNY(3); break;
             case 4: XPU_SKINNY(4); break;
             default:
                 if constexpr (kWide) {
-                    switch ((M + 15) / 16) {
+                    switch ((mrows + 15) / 16) {
                         case 5: XPU_SKINNY(5); break;
                         case 6: XPU_SKINNY(6); break;
                         case 7: XPU_SKINNY(7); break;
@@ -1645,9 +1654,11 @@ hipError_t launch_skinny(hipStream_t st, const int8_t* X, int64_t ldx, const int
 // gives at least 192 tiles; otherwise the small one (128 x 128, 4 waves of
 // 64 x 64, four stages); M <= 64 takes the weight-streaming skinny kernel;
 // a narrow output with K >= 2048 (too few large tiles) the split-K kernel.
-// Paired epilogues take the skinny kernel at M <= 64, else the ping-pong tile
-// (as 4 x 2 waves) or the large one.
-constexpr int kSkinnyPairedM = 128;
+// Paired epilogues take the skinny kernel at M <= 256 (in 128-row chunks
+// above 128: at ffn = 5120, K = 1280, cold, 23.5 -> 14.4 us at M = 129 and
+// 25.4 -> 22.7 us at M = 256, though 1.7 us slower warm there), else the
+// ping-pong tile (as 4 x 2 waves) or the large one.
+constexpr int kSkinnyPairedM = 256;
 
 template <class Epi>
 hipError_t launch_gemm(hipStream_t st, const int8_t* X, int64_t ldx, const int8_t* W, int64_t ldw,

@@ -656,15 +656,17 @@ def test_ffn_stream_dirty_workspace_exact(dev):
 @pytest.mark.parametrize("act", [3, 4, 5])
 @pytest.mark.parametrize("m,inner,k", [(300, 512, 1280), (64, 1280, 1040), (512, 256, 256),
                                        (1, 512, 1280), (17, 768, 256), (40, 256, 4096),
-                                       (100, 512, 1280), (128, 768, 1040), (50, 784, 512)])
+                                       (100, 512, 1280), (128, 768, 1040), (50, 784, 512),
+                                       (200, 512, 1280), (256, 784, 1040)])
 def test_ffn_up_epilogue_exact(dev, act, m, inner, k):
     """The up-projection GEMM's activation epilogue against the oracle's
     dequant_act of the int32 product (ragged M, a partial last column tile,
-    K not a multiple of 64).  M <= 64 (M <= 128 for the paired activations)
+    K not a multiple of 64).  M <= 64 (M <= 256 for the paired activations)
     takes the weight-streaming skinny kernel: for the paired ones two output
     column blocks (hidden and gate rows of each) per block, 4 waves, the last
-    block half past the end at 784 columns; for GELU one block of 16 rows,
-    4 waves, 16 at K = 4096."""
+    block half past the end at 784 columns, above 128 rows in 128-row chunks
+    over grid.y (72 and 128 rows in the second chunk); for GELU one block of
+    16 rows, 4 waves, 16 at K = 4096."""
     check_ffn_up(dev, act, m, inner, k)
 
 
