@@ -372,7 +372,8 @@ def measure_small_batch(torch, int8, lib, L, st, dev, K, W, SET, extra, dev_act,
     -> [M,1280], bf16 bias) as one ``xpuint8_ffn_stream`` call and the linear
     of its down-projection shape (K=5120, N=1280) as one
     ``xpuint8_linear_stream`` call, both on preallocated buffers, and the
-    ``int8.ffn`` API call (host work included) beside them, at M = 1, 64, 128.
+    ``int8.ffn`` API call (host work included) beside them, at M = 1, 64, 128,
+    200.
     At these sizes the weights are most of the traffic (19.66 MB per FFN,
     6.55 MB per linear); ``weights_GB/s`` is that over the call's time."""
     k, f = 1280, 5120
@@ -381,7 +382,7 @@ def measure_small_batch(torch, int8, lib, L, st, dev, K, W, SET, extra, dev_act,
         dev_weight(k, f, 2100 + i)) for i in range(nf)]
     bias = dev_weight(1, k, 2200, 0.01)[0]
     res = {}
-    for m in (1, 64, 128):
+    for m in (1, 64, 128, 200):
         x = dev_act(m, k, 2300 + m)
         y = torch.empty((m, k), dtype=torch.bfloat16, device=dev)
         need = lib.xpuint8_ffn_workspace_size(m, f, k, 4)
@@ -443,8 +444,8 @@ def main():
                          "dequant_slice, quantize_act, dequant_act_quantize, dequant_weight, "
                          "int8_linear step), for profiling")
     ap.add_argument("--only-small", action="store_true",
-                    help="only the small-batch FFN and linear lines (M = 1, 64, 128 at config "
-                         "4's widths), for profiling")
+                    help="only the small-batch FFN and linear lines (M = 1, 64, 128, 200 at "
+                         "config 4's widths), for profiling")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run a plain copy kernel (torch neg over 256 MiB in and out, "
                          "exactly 256 MiB) so counter runs can scale FETCH_SIZE/WRITE_SIZE")
