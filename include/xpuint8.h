@@ -131,6 +131,29 @@ int xpuint8_linear_gemm_stream(const void *stream, const int8_t *xq, const float
                                const int8_t *w8, const float *w_scale, const void *bias,
                                int32_t bias_bf16, void *out, int64_t M, int64_t N, int64_t K);
 
+/* x quantized as by xpuint8_convrot_quantize_stream, with q written in the
+ * MFMA block layout that the GEMM of xpuint8_linear_stream reads: block
+ * (m/16, k/64) of 16 rows x 64 bytes is the 1 KB at
+ * ((m/16) * ceil(K/64) + k/64) * 1024, row r = m%16 at 64r in it and the
+ * row's 16-byte chunk c = (k%64)/16 at 16 * (c ^ ((r >> 1) & 3)).  q holds
+ * ceil(M/16) * ceil(K/64) * 1024 bytes; rows past M in the last block are
+ * left unwritten.  K % 256 == 0, K <= 16384 (or K / 256 even, up to 32768).
+ * No counterpart in the
+ * reference: it exposes the intermediate the one-call linear keeps
+ * internally, so that the GEMM can be run (and timed) on its own. */
+int xpuint8_convrot_quantize_tiled_stream(const void *stream, const void *x, int8_t *q,
+                                          float *scale, int64_t M, int64_t K);
+
+/* xpuint8_linear_gemm_stream with xq in that block layout, bit for bit the
+ * same result.  Only for the shapes whose GEMM reads it (the persistent
+ * kernel: M > 64 with ceil(M/256) * ceil(N/320) tiles >= the CU count; the
+ * split-K kernel: narrow outputs with K >= 1024); other shapes return an
+ * error.  No counterpart in the reference (see above). */
+int xpuint8_linear_gemm_tiled_stream(const void *stream, const int8_t *xq, const float *x_scale,
+                                     const int8_t *w8, const float *w_scale, const void *bias,
+                                     int32_t bias_bf16, void *out, int64_t M, int64_t N,
+                                     int64_t K);
+
 /* The whole INT8 linear in one call: out = xpuint8_linear_gemm_stream of
  * xpuint8_convrot_quantize_stream(x), bit for bit, with x bf16 [M,K], the
  * quantized activation and its row scales kept in `work` (a device buffer of

@@ -268,6 +268,13 @@ int linear_run(hipStream_t st, const void* x, const int8_t* w8, const float* w_s
                                         int(N), int(K)),
                         "linear (gemm)");
     }
+    // the persistent kernel reads q in the MFMA block layout too
+    if (pp_applies(int(M), int(N), int(K), false) && rowquant_can_tile(int(K))) {
+        XPU_TRY(launched(convrot_quantize_tiled(st, x, q, xs, M, int(K)), "linear (quantize)"));
+        return launched(gemm_dequant_pp_xt(st, q, w8, K, out, N, xs, w_scale, b32, b16, int(M),
+                                           int(N), int(K)),
+                        "linear (gemm)");
+    }
     XPU_TRY(launched(convrot_quantize(st, x, q, xs, M, int(K), 0), "linear (quantize)"));
     return launched(gemm_dequant(st, q, K, w8, K, out, N, xs, w_scale, b32, b16, int(M), int(N),
                                  int(K)),
@@ -284,7 +291,7 @@ size_t ffn_work_region_offset(int64_t M, int64_t inner) {
     return (size_t(M) * size_t(inner) * 2 + 255) & ~size_t(255);
 }
 size_t ffn_work_bytes(int64_t M, int64_t inner, int64_t K) {
-    const size_t up = ((size_t(M) * size_t(K) + 255) & ~size_t(255)) + 4 * size_t(M);
+    const size_t up = linear_work_q_bytes(M, K) + 4 * size_t(M);
     return ffn_work_region_offset(M, inner) + std::max(up, linear_work_bytes(M, K, inner));
 }
 
@@ -352,6 +359,16 @@ int xpuint8_convrot_quantize_stream(const void* stream, const void* x, int8_t* q
     XPU_TRY(ensure_device());
     return launched(convrot_quantize(as_stream(stream), x, q, scale, M, int(K), 0),
                     "convrot_quantize");
+}
+
+int xpuint8_convrot_quantize_tiled_stream(const void* stream, const void* x, int8_t* q,
+                                          float* scale, int64_t M, int64_t K) {
+    XPU_TRY(check_rows(M, K));
+    XPU_NONNULL(x); XPU_NONNULL(q); XPU_NONNULL(scale);
+    if (!rowquant_can_tile(int(K))) return fail(2, "convrot_quantize_tiled: K too long");
+    XPU_TRY(ensure_device());
+    return launched(convrot_quantize_tiled(as_stream(stream), x, q, scale, M, int(K)),
+                    "convrot_quantize_tiled");
 }
 
 int xpuint8_convrot_quantize(const void* x, int8_t* q, float* scale, int64_t M, int64_t K) {
@@ -503,6 +520,32 @@ int xpuint8_linear_gemm_stream(const void* stream, const int8_t* xq, const float
                     "linear_gemm");
 }
 
+int xpuint8_linear_gemm_tiled_stream(const void* stream, const int8_t* xq, const float* x_scale,
+                                     const int8_t* w8, const float* w_scale, const void* bias,
+                                     int32_t bias_bf16, void* out, int64_t M, int64_t N,
+                                     int64_t K) {
+    XPU_TRY(check_rows(M, K));
+    XPU_TRY(check_epilogue(M, N));
+    XPU_TRY(check_gemm(M, N, K));
+    XPU_NONNULL(xq); XPU_NONNULL(x_scale); XPU_NONNULL(w8); XPU_NONNULL(w_scale);
+    XPU_NONNULL(out);
+    XPU_ALIGNED_OPT(bias);
+    if (bias_bf16 != 0 && bias_bf16 != 1) return fail(2, "bias_bf16 must be 0 or 1");
+    XPU_TRY(ensure_device());
+    const float* b32 = bias_bf16 ? nullptr : static_cast<const float*>(bias);
+    const uint16_t* b16 = bias_bf16 ? static_cast<const uint16_t*>(bias) : nullptr;
+    hipStream_t st = as_stream(stream);
+    if (pp_applies(int(M), int(N), int(K), false))
+        return launched(gemm_dequant_pp_xt(st, xq, w8, K, out, N, x_scale, w_scale, b32, b16,
+                                           int(M), int(N), int(K)),
+                        "linear_gemm_tiled");
+    if (splitk_applies(int(M), int(N), int(K)) && gemm_slices(int(M), int(N), int(K)) == 0)
+        return launched(gemm_dequant_xt(st, xq, w8, K, out, N, x_scale, w_scale, b32, b16,
+                                        int(M), int(N), int(K)),
+                        "linear_gemm_tiled");
+    return fail(2, "linear_gemm_tiled: this shape does not read x in the block layout");
+}
+
 int64_t xpuint8_linear_workspace_size(int64_t M, int64_t N, int64_t K) {
     if (check_rows(M, K) != 0 || check_epilogue(M, N) != 0 || check_gemm(M, N, K) != 0) return -1;
     return int64_t(linear_work_bytes(M, N, K));
@@ -544,11 +587,20 @@ int xpuint8_ffn_stream(const void* stream, const void* x, const int8_t* up_w8,
     char* v = static_cast<char*>(work);
     char* region = v + ffn_work_region_offset(M, inner);
     int8_t* xq = reinterpret_cast<int8_t*>(region);
-    float* xs = reinterpret_cast<float*>(region + ((size_t(M) * size_t(K) + 255) & ~size_t(255)));
-    XPU_TRY(launched(convrot_quantize(st, x, xq, xs, M, int(K), 0), "ffn (quantize)"));
-    XPU_TRY(launched(gemm_act(st, xq, K, up_w8, K, v, inner, xs, up_scale, int(M), int(inner),
-                              int(K), activation),
-                     "ffn (up projection)"));
+    float* xs = reinterpret_cast<float*>(region + linear_work_q_bytes(M, K));
+    // the persistent up-projection reads xq in the MFMA block layout
+    if (pp_applies(int(M), int(inner), int(K), act_paired(activation)) &&
+        rowquant_can_tile(int(K))) {
+        XPU_TRY(launched(convrot_quantize_tiled(st, x, xq, xs, M, int(K)), "ffn (quantize)"));
+        XPU_TRY(launched(gemm_act_pp_xt(st, xq, up_w8, K, v, inner, xs, up_scale, int(M),
+                                        int(inner), int(K), activation),
+                         "ffn (up projection)"));
+    } else {
+        XPU_TRY(launched(convrot_quantize(st, x, xq, xs, M, int(K), 0), "ffn (quantize)"));
+        XPU_TRY(launched(gemm_act(st, xq, K, up_w8, K, v, inner, xs, up_scale, int(M),
+                                  int(inner), int(K), activation),
+                         "ffn (up projection)"));
+    }
     return linear_run(st, v, down_w8, down_scale, bias, bias_bf16, out, M, K, inner, region);
 }
 

@@ -64,6 +64,16 @@ hipError_t gemm_dequant_xt(hipStream_t st, const int8_t* At, const int8_t* B, in
                            const float* bias, const uint16_t* bias16, int M, int N, int K);
 hipError_t gemm_dequant_nn_xt(hipStream_t st, const int8_t* At, const int8_t* Bkn, int64_t ldb,
                               void* out, int64_t ldo, const float* xs, int M, int N, int K);
+// whether the persistent ping-pong kernel takes the dequant GEMM (paired:
+// the FFN's up-projection) of this shape, and those GEMMs with A in the MFMA
+// block layout on that kernel
+bool pp_applies(int M, int N, int K, bool paired);
+hipError_t gemm_dequant_pp_xt(hipStream_t st, const int8_t* At, const int8_t* B, int64_t ldb,
+                              void* out, int64_t ldo, const float* xs, const float* ws,
+                              const float* bias, const uint16_t* bias16, int M, int N, int K);
+hipError_t gemm_act_pp_xt(hipStream_t st, const int8_t* At, const int8_t* B, int64_t ldb,
+                          void* out, int64_t ldo, const float* xs, const float* ws, int M, int N,
+                          int K, int act);
 // the same with the residual update out = bf16(res + d * rscale[n]) (bf16 res, rscale)
 hipError_t gemm_dequant_residual(hipStream_t st, const int8_t* A, int64_t lda, const int8_t* B,
                                  int64_t ldb, void* out, int64_t ldo, const float* xs,

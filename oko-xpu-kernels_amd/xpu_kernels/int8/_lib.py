@@ -53,6 +53,7 @@ def _signatures():
         "xpuint8_last_error": ([], c_str),
         "xpuint8_convrot_quantize": ([vp] * 3 + [i64] * 2, c_int),
         "xpuint8_convrot_quantize_stream": ([vp] * 4 + [i64] * 2, c_int),
+        "xpuint8_convrot_quantize_tiled_stream": ([vp] * 4 + [i64] * 2, c_int),
         "xpuint8_convrot_quantize_act": ([vp] * 3 + [i64] * 2 + [i32], c_int),
         "xpuint8_convrot_quantize_act_stream": ([vp] * 4 + [i64] * 2 + [i32], c_int),
         "xpuint8_dequant_weight": ([vp] * 3 + [i64] * 2, c_int),
@@ -68,6 +69,7 @@ def _signatures():
         "xpuint8_int8_gemm_stream": ([vp] * 4 + [i64] * 3, c_int),
         "xpuint8_int8_gemm_nn_stream": ([vp] * 4 + [i64] * 3 + [vp], c_int),
         "xpuint8_linear_gemm_stream": ([vp] * 6 + [i32, vp] + [i64] * 3, c_int),
+        "xpuint8_linear_gemm_tiled_stream": ([vp] * 6 + [i32, vp] + [i64] * 3, c_int),
         "xpuint8_linear_stream": ([vp] * 5 + [i32, vp] + [i64] * 3 + [vp, i64], c_int),
         "xpuint8_linear_workspace_size": ([i64] * 3, i64),
         "xpuint8_linear_gemm_residual_stream": ([vp] * 6 + [i32] + [vp] * 3 + [i64] * 3, c_int),
