@@ -273,7 +273,11 @@ int64_t xpuint8_linear_dx_int8_workspace_size(int64_t M, int64_t N, int64_t K);
  * (config 5, M=4096 N=5120 K=1280, needs 38 MB).  Every call on a device
  * shares that array: calls that overlap on one device (two streams, two
  * threads) race and must be serialised by the caller.  The result equals
- * xpuint8_linear_dx_int8_stream's bit for bit. */
+ * xpuint8_linear_dx_int8_stream's bit for bit.  Under stream capture: the
+ * library's set-up of a device (a synchronous upload of the activation
+ * tables and the lookup of this array's address, on the first call on that
+ * device) cannot be captured, so run it before the capture begins --
+ * xpuint8_init() with the device current, or any uncaptured call on it. */
 int xpuint8_linear_dx_int8_noalloc_stream(const void *stream, const void *dy, const float *w_scale,
                                           const int8_t *w8, void *dx, int64_t M, int64_t N,
                                           int64_t K);

@@ -761,7 +761,13 @@ int bf16_nn_slices(int M, int N, int K) {
     if (tiles >= 128) return 0;
     int s = 1;
     while (tiles * s < 192 && (N / kStepRows) % (2 * s) == 0 && N / (2 * s) >= 1024) s *= 2;
-    return s > 1 ? s : 0;
+    if (s == 1) return 0;
+    // the split-K kernel's 32-bit byte offsets: a slice's rows of w (N / s
+    // rows of K) and a 128-row block of dy (rows of N); beyond them the
+    // unsplit kernel takes the shape
+    if (int64_t(N / s) * K * 2 >= (int64_t(1) << 32) || 128 * int64_t(N) * 2 >= (int64_t(1) << 31))
+        return 0;
+    return s;
 }
 
 hipError_t gemm_bf16_nn_slices(hipStream_t st, const void* dy, int64_t ldy, const void* w,

@@ -511,7 +511,9 @@ def linear(x, w8, w_scale, bias=None, act: Optional[str] = None, residual=None,
     """INT8 ConvRot linear: bf16/fp32 [.., K] -> bf16/fp32 [.., N] (ops.py:591-646).
 
     Two kernels: rotate+quantize of ``x`` (with ``act`` fused into its load),
-    then the MFMA GEMM with the dequant (+bias) epilogue fused into its store.
+    then the MFMA GEMM with the dequant (+bias) epilogue fused into its store;
+    a product too small to fill the GPU is split in K across blocks, and a
+    third kernel adds the slices' int32 sums and applies the dequant.
     ``residual``/``residual_scale`` apply ``residual + residual_scale * out``;
     ``return_acc`` returns ``(int32 [M, N], fp32 [M], fp32 [N])`` instead.
     """

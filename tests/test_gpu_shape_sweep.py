@@ -1,11 +1,12 @@
 """Seeded random shapes over the whole dispatch space of the linear, the FFN and
 linear_dx_int8, each bit-exact against the oracle.
 
-The GEMM a call takes depends on M, N and K: the skinny kernel (M <= 64,
-M <= 128 for the FFN's paired up-projection), K slices on the skinny, the
-128 x 128 or the split-K kernel for outputs too small to fill the chip, the
-split-K kernel on the activation in MFMA-block order, the two-block and the
-persistent kernels.  The fixed-shape tests sit on each side of every
+The GEMM a call takes depends on M, N and K: the skinny kernel (M <= 64;
+M <= 256 for the FFN's paired up-projection, in 128-row chunks above 128),
+K slices on the skinny, the 128 x 128 or the split-K kernel for outputs too
+small to fill the chip (then a dequant pass that adds the slices), the
+split-K and the persistent kernels on the activation in MFMA-block order,
+and the two-block kernel.  The fixed-shape tests sit on each side of every
 threshold; these draw shapes between them (ragged M, N any multiple of 16, K
 any multiple of 256), so that no combination of tile remainders and slice
 counts goes untested.  Shapes are drawn once from fixed seeds and appear in

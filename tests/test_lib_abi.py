@@ -191,6 +191,9 @@ def test_linear_dx_workspace_size(lib):
     assert lib.xpuint8_linear_dx_workspace_size(64, 5120, 1280) == 0       # M <= 64
     assert lib.xpuint8_linear_dx_workspace_size(300, 1040, 272) == 0       # 1040 % 32
     assert lib.xpuint8_linear_dx_workspace_size(4, 24, 512) == -1
+    # a slice's w rows past 2^32 bytes (2 slices of 107520 rows x 20000):
+    # the unsplit kernel, no workspace
+    assert lib.xpuint8_linear_dx_workspace_size(100, 215040, 20000) == 0
 
 
 def test_linear_workspace_size(lib):
