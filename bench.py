@@ -642,9 +642,22 @@ def main():
         dn8, dns = int8.prepare_weight(weight(torch, 1280, 5120, seed=5).to(dev))
         db = weight(torch, 1, 1280, seed=6, std=0.01)[0].to(dev)
         ms_f = timed(torch, lambda i: int8.ffn(xf, up8, ups, dn8, dns, db, act="geglu_erf"), K, W, SET)
+        # cold: each call its own (x, up, down, bias) set, > 640 MB between reuses
+        n4 = n_sets(2 * 4096 * 1280 + 10240 * 1280 + 1280 * 5120 + 2 * 4096 * 1280)
+        sets4 = [(xf, up8, ups, dn8, dns, db)]
+        for i in range(1, n4):
+            u8, us = int8.prepare_weight(dev_weight(10240, 1280, 900 + i))
+            d8, ds = int8.prepare_weight(dev_weight(1280, 5120, 950 + i))
+            sets4.append((dev_act(4096, 1280, 1000 + i), u8, us, d8, ds,
+                          dev_weight(1, 1280, 1050 + i, 0.01)[0]))
+        ms_f_cold = timed(torch, lambda i: int8.ffn(*sets4[i % n4], act="geglu_erf"), K, W, SET)
+        del sets4
         ops4 = 2.0 * 4096 * 1280 * 10240 + 2.0 * 4096 * 5120 * 1280
-        extra["config4_ffn"] = {"ms": round(ms_f, 5), "TOP/s": round(ops4 / (ms_f * 1e-3) / 1e12, 1)}
-        log(f"[bench] config 4: ffn {ms_f:.4f} ms")
+        extra["config4_ffn"] = {"ms_cold": round(ms_f_cold, 5),
+                                "TOP/s_cold": round(ops4 / (ms_f_cold * 1e-3) / 1e12, 1),
+                                "ms_warm": round(ms_f, 5),
+                                "TOP/s_warm": round(ops4 / (ms_f * 1e-3) / 1e12, 1), "sets": n4}
+        log(f"[bench] config 4: ffn {ms_f_cold:.4f} ms cold / {ms_f:.4f} warm")
         # ------------------------------------------------------ config 5
         w5_8, w5_s = int8.prepare_weight(weight(torch, 5120, 1280, seed=7).to(dev))
         dy = (torch.randn(4096, 5120, generator=torch.Generator().manual_seed(8)) * 1e-3
@@ -654,11 +667,27 @@ def main():
         ms_dw = timed(torch, lambda i: int8.linear_dw(dy, x5), K, W, SET)
         w5d = int8.dequant_weight(w5_8, w5_s)
         ms_dxd = timed(torch, lambda i: int8.linear_dx(dy, w5d), K, W, SET)
+        # cold: each call its own (dy, w8, w_scale, x, w) set, > 640 MB between reuses
+        n5 = n_sets(2 * 4096 * 5120 + 5120 * 1280 + 2 * 4096 * 1280 + 2 * 5120 * 1280)
+        sets5 = [(dy, w5_8, w5_s, x5, w5d)]
+        for i in range(1, n5):
+            wi8, wis = int8.prepare_weight(dev_weight(5120, 1280, 1100 + i))
+            sets5.append(((torch.randn(4096, 5120, device=dev, generator=dev_gen(1150 + i)) * 1e-3)
+                          .to(torch.bfloat16), wi8, wis, dev_act(4096, 1280, 1200 + i),
+                          int8.dequant_weight(wi8, wis)))
+        ms_dx_c = timed(torch, lambda i: int8.linear_dx_int8(*sets5[i % n5][:3]), K, W, SET)
+        ms_dw_c = timed(torch, lambda i: int8.linear_dw(sets5[i % n5][0], sets5[i % n5][3]), K, W, SET)
+        ms_dxd_c = timed(torch, lambda i: int8.linear_dx(sets5[i % n5][0], sets5[i % n5][4]), K, W, SET)
+        del sets5
         ops5 = 2.0 * 4096 * 5120 * 1280
-        extra["config5_dx_int8"] = {"ms": round(ms_dx, 5), "TOP/s": round(ops5 / (ms_dx * 1e-3) / 1e12, 1)}
-        extra["config5_dw"] = {"ms": round(ms_dw, 5), "TFLOP/s": round(ops5 / (ms_dw * 1e-3) / 1e12, 1)}
-        extra["config5_dx_dense"] = {"ms": round(ms_dxd, 5),
-                                     "TFLOP/s": round(ops5 / (ms_dxd * 1e-3) / 1e12, 1)}
+
+        def ops_line(unit, cold, warm):
+            return {"ms_cold": round(cold, 5), f"{unit}_cold": round(ops5 / (cold * 1e-3) / 1e12, 1),
+                    "ms_warm": round(warm, 5), f"{unit}_warm": round(ops5 / (warm * 1e-3) / 1e12, 1),
+                    "sets": n5}
+        extra["config5_dx_int8"] = ops_line("TOP/s", ms_dx_c, ms_dx)
+        extra["config5_dw"] = ops_line("TFLOP/s", ms_dw_c, ms_dw)
+        extra["config5_dx_dense"] = ops_line("TFLOP/s", ms_dxd_c, ms_dxd)
         bytes_rq = 3 * 4096 * 5120 + 4 * 4096
         nrq = n_sets(bytes_rq)
         setsr = [(dy if i == 0 else (torch.randn(4096, 5120, device=dev, generator=dev_gen(600 + i))
@@ -706,7 +735,8 @@ def main():
                                                api_ms=round(ms_sk_api, 5),
                                                api_graph_replay_ms=round(ms_sk_graph, 5))
         del sk, graph
-        log(f"[bench] config 5: dx {ms_dx:.4f} ms, dW {ms_dw:.4f} ms, dense dx {ms_dxd:.4f} ms, "
+        log(f"[bench] config 5: dx {ms_dx_c:.4f} / {ms_dx:.4f} ms, dW {ms_dw_c:.4f} / {ms_dw:.4f} ms, "
+            f"dense dx {ms_dxd_c:.4f} / {ms_dxd:.4f} ms (cold / warm), "
             f"quantize_row {ms_rq:.4f} / {ms_rq_warm:.4f} ms, skinny {ms_sk:.4f} / "
             f"{ms_sk_warm:.4f} ms (API {ms_sk_api:.4f}, graph replay {ms_sk_graph:.4f})")
 

@@ -297,6 +297,21 @@ int xpuint8_prepare_weight_stream(const void *stream, const void *w, int8_t *q, 
 int xpuint8_quantize_row_stream(const void *stream, const void *x, const float *col_scale,
                                 int8_t *q, float *scale, int64_t M, int64_t N);
 
+/* Column sums of a bf16 matrix, out[n] = bf16(sum_m x[m,n]): x bf16 [M,N],
+ * out bf16 [N], N % 16 == 0.  The bias gradient dy.sum(dim=0) of the
+ * reference's backward (python/xpu_kernels/int8/ops.py:276, 821), which torch
+ * reduces in an order of its own; here the order is fixed: fp32 sums of 32
+ * consecutive rows, each in row order, then those sums in order, rounded to
+ * bf16 (to nearest even) once.  work: xpuint8_column_sum_workspace_size(M, N)
+ * bytes (the fp32 partial sums), 16-byte aligned. */
+int xpuint8_column_sum_stream(const void *stream, const void *x, void *out, int64_t M, int64_t N,
+                              void *work, int64_t work_bytes);
+
+/* The workspace xpuint8_column_sum_stream needs, in bytes, or -1 when the
+ * shape is not supported.  No device needed.  No counterpart in the
+ * reference. */
+int64_t xpuint8_column_sum_workspace_size(int64_t M, int64_t N);
+
 /* The weight gradient of a linear: dw[n,k] = sum_m dy[m,n] * x[m,k], dy bf16
  * [M,N], x bf16 [M,K], dw bf16 [N,K]; fp32 accumulation, one RNE rounding.
  * N % 16 == 0, K % 16 == 0.  Replaces the torch matmul dy^T @ x of linear_dw

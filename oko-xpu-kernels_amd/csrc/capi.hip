@@ -653,6 +653,22 @@ int xpuint8_dx_gemm_stream(const void* stream, const int8_t* q, const float* a, 
                     "dx_gemm");
 }
 
+int64_t xpuint8_column_sum_workspace_size(int64_t M, int64_t N) {
+    if (check_epilogue(M, N) != 0) return -1;
+    return colsum_work_bytes(M, N);
+}
+
+int xpuint8_column_sum_stream(const void* stream, const void* x, void* out, int64_t M, int64_t N,
+                              void* work, int64_t work_bytes) {
+    XPU_TRY(check_epilogue(M, N));
+    XPU_NONNULL(x); XPU_NONNULL(out); XPU_NONNULL(work);
+    if (work_bytes < colsum_work_bytes(M, N))
+        return fail(2, "work must hold xpuint8_column_sum_workspace_size(M, N) bytes");
+    XPU_TRY(ensure_device());
+    return launched(column_sum_bf16(as_stream(stream), x, out, M, int(N), static_cast<float*>(work)),
+                    "column_sum");
+}
+
 int64_t xpuint8_linear_dx_int8_workspace_size(int64_t M, int64_t N, int64_t K) {
     if (check_dx(M, N, K) != 0) return -1;
     return int64_t(dx_work_layout(M, N, K).total);

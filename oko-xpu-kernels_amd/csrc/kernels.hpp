@@ -42,6 +42,12 @@ bool rowquant_can_tile(int K);
 hipError_t convrot_quantize_tiled(hipStream_t st, const void* x, int8_t* q, float* scale,
                                   int64_t M, int K);
 
+// bf16 column sums out[n] = bf16(sum_m x[m, n]) (N % 8 == 0) through fp32
+// partials in part (colsum_work_bytes(M, N) bytes)
+int64_t colsum_work_bytes(int64_t M, int64_t N);
+hipError_t column_sum_bf16(hipStream_t st, const void* x, void* out, int64_t M, int N,
+                           float* part);
+
 // gemm_i8.hip
 hipError_t gemm_i32(hipStream_t st, const int8_t* A, int64_t lda, const int8_t* B, int64_t ldb,
                     int32_t* C, int64_t ldc, int M, int N, int K);

@@ -755,6 +755,81 @@ hipError_t launch_rotate(hipStream_t st, const Loader& ld, uint16_t* out, int64_
     return hipGetLastError();
 }
 
+
+// ------------------------------------------------------------ column sums
+// out[n] = bf16(sum over m of x[m, n]) for bf16 x [M, N] (N % 8 == 0), the
+// bias gradient dy.sum(dim=0) of the reference's backward
+// (python/xpu_kernels/int8/ops.py:276), in a fixed order: fp32 sums of
+// kColChunk consecutive rows, each in row order (colsum_part_kernel: a lane
+// takes 8 columns, 16-byte loads, one chunk of rows), then the chunk sums
+// (colsum_final_kernel): eight interleaved running sums, sum w over chunks w,
+// w + 8, w + 16, ... in order, added in the order w = 0..7; one rounding to
+// bf16.  HBM-bound: one
+// read of x plus 4 bytes per column per chunk of partials.
+constexpr int kColChunk = 32, kColCols = 2048;
+
+__global__ __launch_bounds__(256) void colsum_part_kernel(const uint16_t* __restrict__ x,
+                                                          float* __restrict__ part, int64_t M,
+                                                          int N) {
+    const int n = blockIdx.x * kColCols + threadIdx.x * 8;
+    if (n >= N) return;
+    const int64_t m0 = int64_t(blockIdx.y) * kColChunk;
+    const int rows = int(min(int64_t(kColChunk), M - m0));
+    const uint16_t* p = x + m0 * N + n;
+    float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    // eight rows' loads in flight, summed in row order
+    for (int r0 = 0; r0 < rows; r0 += 8) {
+        uint4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (r0 + u < rows) v[u] = *reinterpret_cast<const uint4*>(p + int64_t(r0 + u) * N);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            if (r0 + u < rows) {
+                a[0] += bf16lo(v[u].x); a[1] += bf16hi(v[u].x);
+                a[2] += bf16lo(v[u].y); a[3] += bf16hi(v[u].y);
+                a[4] += bf16lo(v[u].z); a[5] += bf16hi(v[u].z);
+                a[6] += bf16lo(v[u].w); a[7] += bf16hi(v[u].w);
+            }
+        }
+    }
+    float* o = part + int64_t(blockIdx.y) * N + n;
+    *reinterpret_cast<float4*>(o) = make_float4(a[0], a[1], a[2], a[3]);
+    *reinterpret_cast<float4*>(o + 4) = make_float4(a[4], a[5], a[6], a[7]);
+}
+
+// The chunk sums of 64 columns per block of 8 waves: wave w adds chunks w,
+// w + 8, w + 16, ... in that order (all its loads issued first), then the
+// eight wave sums are added in wave order.
+__global__ __launch_bounds__(512) void colsum_final_kernel(const float* __restrict__ part,
+                                                           uint16_t* __restrict__ out, int chunks,
+                                                           int N) {
+    __shared__ float t[8][64];
+    const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+    const int n = blockIdx.x * 64 + l;
+    const int nc = min(n, N - 1);
+    float a = 0.f;
+    for (int c0 = w; c0 < chunks; c0 += 8 * 16) {
+        float v[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int c = c0 + 8 * i;
+            v[i] = c < chunks ? part[int64_t(c) * N + nc] : 0.f;
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            if (c0 + 8 * i < chunks) a += v[i];
+    }
+    t[w][l] = a;
+    __syncthreads();
+    if (w == 0 && n < N) {
+        float s = t[0][l];
+#pragma unroll
+        for (int i = 1; i < 8; ++i) s += t[i][l];
+        out[n] = uint16_t(f32_to_bf16_bits(s));
+    }
+}
+
 }  // namespace
 
 // ------------------------------------------------------------------- entry
@@ -818,6 +893,22 @@ hipError_t convrot_quantize_tiled(hipStream_t st, const void* x, int8_t* q, floa
                                   int64_t M, int K) {
     return launch_rowquant<true, kRecip, LoadBF16, true>(
         st, LoadBF16{static_cast<const uint16_t*>(x), K}, q, scale, M, K);
+}
+
+int64_t colsum_work_bytes(int64_t M, int64_t N) {
+    return ((M + kColChunk - 1) / kColChunk) * N * 4;
+}
+
+hipError_t column_sum_bf16(hipStream_t st, const void* x, void* out, int64_t M, int N,
+                           float* part) {
+    const int chunks = int((M + kColChunk - 1) / kColChunk);
+    hipLaunchKernelGGL(colsum_part_kernel, dim3(unsigned((N + kColCols - 1) / kColCols),
+                                                unsigned(chunks)),
+                       dim3(256), 0, st, static_cast<const uint16_t*>(x), part, M, N);
+    if (const hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+    hipLaunchKernelGGL(colsum_final_kernel, dim3(unsigned((N + 63) / 64)), dim3(512), 0, st, part,
+                       static_cast<uint16_t*>(out), chunks, N);
+    return hipGetLastError();
 }
 
 }  // namespace xpuint8

@@ -23,6 +23,7 @@ from ._lib import ACTIVATIONS, PAIRED_ACTIVATIONS, available, device_name, load
 from .ops import (
     Int8Linear,
     TrainableInt8Linear,
+    column_sum,
     dequant,
     dequant_act_quantize,
     dequant_slice,

@@ -78,6 +78,8 @@ def _signatures():
         "xpuint8_ffn_workspace_size": ([i64] * 3 + [i32], i64),
         "xpuint8_dx_gemm_stream": ([vp] * 5 + [i64] * 3 + [vp], c_int),
         "xpuint8_linear_dx_int8_stream": ([vp] * 5 + [i64] * 3 + [vp, i64], c_int),
+        "xpuint8_column_sum_stream": ([vp] * 3 + [i64] * 2 + [vp, i64], c_int),
+        "xpuint8_column_sum_workspace_size": ([i64] * 2, i64),
         "xpuint8_linear_dx_int8_workspace_size": ([i64] * 3, i64),
         "xpuint8_linear_dx_int8_noalloc_stream": ([vp] * 5 + [i64] * 3, c_int),
         "xpuint8_prepare_weight_stream": ([vp] * 4 + [i64] * 2, c_int),

@@ -213,6 +213,30 @@ def linear_dw(dy, x):
     return dy2.transpose(0, 1) @ x2
 
 
+def column_sum(dy):
+    """``dy.sum(dim=0)``, the bias gradient of the reference's backward
+    (ops.py:276, 821).  A 2-D bf16 ``dy`` on the GPU (columns a multiple of
+    16) takes one HIP column-sum pass (fp32 sums of 32-row chunks in row
+    order, then the chunks in order, one bf16 rounding) instead of torch's
+    reduction, whose order is its own; anything else is torch's sum."""
+    if (isinstance(dy, torch.Tensor) and dy.dim() == 2 and dy.dtype == torch.bfloat16
+            and dy.is_cuda and dy.shape[0] > 0 and dy.shape[1] % 16 == 0):
+        lib = _lib()
+        m, n = int(dy.shape[0]), int(dy.shape[1])
+        d2 = _c(dy)
+        nbytes = lib.xpuint8_column_sum_workspace_size(m, n)
+        if nbytes < 0:
+            _err(lib, "column_sum")
+        work = torch.empty((max(nbytes, 16),), device=dy.device, dtype=torch.int8)
+        out = torch.empty((n,), device=dy.device, dtype=torch.bfloat16)
+        rc = lib.xpuint8_column_sum_stream(_stream(dy.device), _ptr(d2), _ptr(out), m, n,
+                                           _ptr(work), nbytes)
+        if rc != 0:
+            _err(lib, "column_sum")
+        return out
+    return dy.sum(dim=0)
+
+
 class _Int8LinearFn(torch.autograd.Function):
     """The INT8 linear as an autograd op (ops.py:241-289): forward is
     :func:`linear`; backward is dbias plus dx through :func:`linear_dx_int8`
@@ -229,7 +253,7 @@ class _Int8LinearFn(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dy):
         w8, w_scale = ctx.saved_tensors
-        dbias = dy.sum(dim=0) if ctx.needs_input_grad[3] else None
+        dbias = column_sum(dy) if ctx.needs_input_grad[3] else None
         dy = dy.to(torch.bfloat16)
         if ctx.mode == "int8":
             dx = linear_dx_int8(dy, w8, w_scale)
@@ -756,7 +780,7 @@ class _TrainableInt8LinearFn(torch.autograd.Function):
         # reference's matmul would refuse the mixed dtypes)
         dx = linear_dx(dy if dy.dtype == w.dtype else dy.to(w.dtype), w)
         dw = linear_dw(dy, x2)
-        db = dy.sum(dim=0) if ctx.has_bias else None
+        db = column_sum(dy) if ctx.has_bias else None
         if dw.dtype != weight.dtype:
             dw = dw.to(weight.dtype)
         return (dx.reshape(x.shape[:-1] + (dx.shape[-1],)), dw, db, None)

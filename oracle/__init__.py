@@ -47,6 +47,9 @@ PINNING = {
     "linear_dx_int8": "torch chain of ops.py:366-377 (bf16 mul, torch._int_mm); "
                       "float64 dy@W within INT8 error",
     "linear_dw": "torch float64 matmul",
+    "column_sum": "float64 exact sums within the float32 chunked-summation bound before "
+                  "the one bf16 rounding; closed forms (constant columns sum to M*v, "
+                  "+v/-v pairs to zero); torch's dy.sum(0) on bf16 within one bf16 ulp",
     "linear_dx": "torch float64 matmul dy @ w; transposed-operand identity with linear_dw",
     "activate": "torch bf16 eager chains (gelu_tanh, silu*u, situ, h*gelu(g), gelu) "
                 "within 1 bf16 ulp on <0.5% of elements; float64 closed forms "

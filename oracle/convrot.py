@@ -15,8 +15,11 @@ __all__ = [
     "hadamard256_matrix", "rotate_bf16", "convrot_quantize", "quantize_from_rotated",
     "prepare_weight", "prepare_weight_fused", "quantize_row", "int_mm", "dequant",
     "linear_acc", "linear", "dequant_weight", "linear_dx_int8", "linear_dx", "linear_dw",
-    "convrot_int8_linear", "expand_scale",
+    "convrot_int8_linear", "expand_scale", "column_sum", "COL_CHUNK",
 ]
+
+#: rows per fp32 partial sum of column_sum (the build's fixed order)
+COL_CHUNK = 32
 
 #: the ConvRot group size (src/xpuint8.cpp:71)
 GS = 256
@@ -286,6 +289,35 @@ def linear_dw(dy_bf16, x_bf16) -> np.ndarray:
     dy = bf16_to_f32(dy_bf16).astype(np.float64).reshape(-1, np.asarray(dy_bf16).shape[-1])
     x = bf16_to_f32(x_bf16).astype(np.float64).reshape(-1, np.asarray(x_bf16).shape[-1])
     return dy.T @ x
+
+
+def column_sum(x_bf16: np.ndarray) -> np.ndarray:
+    """``dy.sum(dim=0)`` of a bf16 [M, N] matrix, the bias gradient of the
+    reference's backward (python/xpu_kernels/int8/ops.py:276, 821), in the
+    build's fixed order: float32 sums of ``COL_CHUNK`` consecutive rows, each
+    in row order; then eight running sums, sum w over chunks w, w + 8,
+    w + 16, ... in order; then those eight added in order w = 0..7; one
+    rounding to bf16.  (torch's own reduction order is unspecified; both are
+    within the float32 summation bound of the exact sum before the one bf16
+    rounding.)  Returns bf16 bits."""
+    x = bf16_to_f32(x_bf16)
+    m, n = x.shape
+    chunks = []
+    for c0 in range(0, m, COL_CHUNK):
+        a = np.zeros(n, dtype=np.float32)
+        for r in range(c0, min(m, c0 + COL_CHUNK)):
+            a = (a + x[r]).astype(np.float32)
+        chunks.append(a)
+    lanes = []
+    for w in range(8):
+        a = np.zeros(n, dtype=np.float32)
+        for c in range(w, len(chunks), 8):
+            a = (a + chunks[c]).astype(np.float32)
+        lanes.append(a)
+    tot = lanes[0]
+    for a in lanes[1:]:
+        tot = (tot + a).astype(np.float32)
+    return f32_to_bf16(tot)
 
 
 def convrot_int8_linear(x_rot_f32, weight, weight_scale, bias_bf16=None) -> np.ndarray:

@@ -69,7 +69,7 @@ def test_linear_dx_dense_batched_input(dev):
 def test_int8_linear_dense_backward(dev):
     """int8_linear(mode="dense"): dx = linear_dx(bf16(dy), dequant_weight(w8, ws)),
     the dequantized weight bit-exact against the oracle and the product within
-    the bf16 bound of float64; dbias = dy.sum(0)."""
+    the bf16 bound of float64; dbias = dy.sum(0) (the column-sum kernel)."""
     m, n, k = 256, 512, 1280
     x = activation(m, k, seed=21).to(dev).requires_grad_(True)
     w8, ws = int8.prepare_weight(weight(n, k, seed=22).to(dev))
@@ -86,7 +86,8 @@ def test_int8_linear_dense_backward(dev):
     ok, worst = _bf16_bound(bits(x.grad), ref, mag)
     assert ok, worst
     assert x.grad.dtype == torch.bfloat16
-    assert torch.equal(bias.grad, dy.to(dev).sum(0))
+    # dbias: the HIP column sum, bit for bit the oracle's fixed order
+    assert np.array_equal(bits(bias.grad), O.column_sum(bits(dy)))
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
