@@ -439,6 +439,8 @@ def main():
     ap.add_argument("--only-gemm", action="store_true",
                     help="the config-3 GEMM alone, cold, and nothing else (for profiling: its "
                          "launches are then the only ones of that kernel in the run)")
+    ap.add_argument("--only-c45", action="store_true",
+                    help="only configs 4 and 5 (FFN, backward, skinny), for profiling")
     ap.add_argument("--only-side", action="store_true",
                     help="only the entry points beside the path (linear_acc, residual, dequant, "
                          "dequant_slice, quantize_act, dequant_act_quantize, dequant_weight, "
@@ -521,7 +523,7 @@ def main():
         sets3.append((dev_act(M, Kd, 200 + i), wi8, wis, dev_weight(1, N, 300 + i, 0.01)[0]))
     log(f"[bench] config 3 linear {M}x{Kd}x{N}: {W} warm-up + {K} timed steps, "
         f"cold over {n3} input sets")
-    if args.only_gemm or args.only_rowquant:
+    if args.only_gemm or args.only_rowquant or args.only_c45:
         ms = ms_warm = float("nan")
     else:
         ms = timed(torch, lambda i: int8.linear(*sets3[i % n3]), K, W, SET)
@@ -551,14 +553,14 @@ def main():
         lib.xpuint8_linear_gemm_tiled_stream(st, L._ptr(xq), L._ptr(xs), L._ptr(wi8), L._ptr(wis),
                                              L._ptr(bi), 1, L._ptr(out), M, N, Kd)
     ms_gemm = ms_gemm_warm = float("nan")
-    if not args.only_rowquant:
+    if not (args.only_rowquant or args.only_c45):
         ms_gemm = timed(torch, gemm, K, W, SET)
     if args.only_gemm:
         print(json.dumps({"only_gemm": True, "gemm_ms_cold": round(ms_gemm, 5),
                           "TOP/s": round(ops3 / (ms_gemm * 1e-3) / 1e12, 1),
                           "steps": K, "warmup": W, "sets": ng}), flush=True)
         return
-    if not args.only_rowquant:
+    if not (args.only_rowquant or args.only_c45):
         ms_gemm_warm = timed(torch, lambda i: gemm(0), K, W, SET)
     gemm_tops = ops3 / (ms_gemm * 1e-3) / 1e12
     q3 = [(torch.empty(tiled_bytes, device=dev, dtype=torch.int8),
@@ -570,7 +572,7 @@ def main():
         lib.xpuint8_convrot_quantize_tiled_stream(st, L._ptr(xi), L._ptr(qi), L._ptr(si), M, Kd)
     bytes_q3 = 3 * M * Kd + 4 * M
     ms_q3 = ms_q3_warm = float("nan")
-    if not args.only_rowquant:
+    if not (args.only_rowquant or args.only_c45):
         ms_q3 = timed(torch, quant3, K, W, SET)
         ms_q3_warm = timed(torch, lambda i: quant3(0), K, W, SET)
     log(f"[bench] step {ms:.4f} ms cold / {ms_warm:.4f} warm = {value:.1f} TOP/s; GEMM "
@@ -584,7 +586,7 @@ def main():
     extra["config3_quantize"] = hbm_line(bytes_q3, ms_q3, ms_q3_warm)
     del gsets
 
-    if not args.only_main:
+    if not (args.only_main or args.only_c45):
         # ------------------------------------------------------ config 2
         # kernel throughput: the C entry points on preallocated outputs (the
         # python wrapper's own host cost, ~10 us per call, would otherwise
@@ -766,6 +768,10 @@ def main():
                                                             sets=nro)
         del accs, qsl
         log(f"[bench] rms+rope dequant: {ms_rope:.4f} / {ms_rope_warm:.4f} ms")
+        if args.only_c45:
+            print(json.dumps({"only_c45": True, "steps": K, "warmup": W, "extra": extra}),
+                  flush=True)
+            return
         measure_side_rows(torch, int8, lib, L, st, dev, K, W, SET, extra, hbm_line, dev_gen,
                           dev_act, dev_weight, x, w8, ws, bias)
         measure_small_batch(torch, int8, lib, L, st, dev, K, W, SET, extra, dev_act, dev_weight)
