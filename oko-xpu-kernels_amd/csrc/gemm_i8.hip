@@ -1393,6 +1393,21 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_splitk_kernel(
         __builtin_amdgcn_sched_barrier(0);
     };
 
+    // The epilogue's row and column operands (this team's half of the wave's
+    // rows, all of its columns), loaded before the operands so that their
+    // latency is paid under the main loop.
+    constexpr int H = TM / 2;
+    float xrow[H];
+    typename std::conditional_t<SLICE, EpiDequant, Epi>::Col ccol[TN];
+    if constexpr (!SLICE) {
+        const int mh = m0 + wm * WM + (team == 0 ? 0 : 16 * H);
+#pragma unroll
+        for (int b = 0; b < H; ++b) xrow[b] = epi.row(min(mh + 16 * b + (lane & 15), M - 1));
+#pragma unroll
+        for (int a = 0; a < TN; ++a)
+            ccol[a] = epi.col(min(n0 + wn * WN + 16 * a + 4 * (lane >> 4), N - 4));
+    }
+
     for (int s = 0; s < S - 1; ++s)
         if (s < nst) issue(s);
     if (nst > 0) wait_batches(min(S - 2, nst - 1));
@@ -1422,8 +1437,46 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_splitk_kernel(
         }
     }
 
-    // team 1 -> team 0 through LDS, TM/2 rows of blocks at a time
     v4i* xchg = reinterpret_cast<v4i*>(smem);
+    if constexpr (!SLICE) {
+        // The two teams' partial sums meet in LDS, and each team finishes half
+        // of the tile: team 0 the wave's row blocks [0, H), team 1 [H, TM).
+        // Each wave hands the other half to its partner (same wt, other team)
+        // and adds the partner's half of its own; then all 8 waves run the
+        // epilogue (staging areas past the hand-over area).
+        static_assert(8 * TN * H * 1024 + 8 * 32 * 256 <= 2 * RING, "hand-over and staging fit");
+        __syncthreads();                                    // the ring's last reads are done
+        v4i mine[TN][H];
+        if (team == 0) {
+#pragma unroll
+            for (int a = 0; a < TN; ++a)
+#pragma unroll
+                for (int bb = 0; bb < H; ++bb) {
+                    xchg[((wave * TN + a) * H + bb) * 64 + lane] = acc[a][H + bb];
+                    mine[a][bb] = acc[a][bb];
+                }
+        } else {
+#pragma unroll
+            for (int a = 0; a < TN; ++a)
+#pragma unroll
+                for (int bb = 0; bb < H; ++bb) {
+                    xchg[((wave * TN + a) * H + bb) * 64 + lane] = acc[a][bb];
+                    mine[a][bb] = acc[a][H + bb];
+                }
+        }
+        __syncthreads();
+        const int pw = wave ^ 4;
+#pragma unroll
+        for (int a = 0; a < TN; ++a)
+#pragma unroll
+            for (int bb = 0; bb < H; ++bb) mine[a][bb] += xchg[((pw * TN + a) * H + bb) * 64 + lane];
+        staged_store<H, TN, WN, Epi, 2>(epi, mine, [&](int b) { return xrow[b]; }, ccol,
+                                        smem + 8 * TN * H * 1024 + wave * (32 * 256),
+                                        m0 + wm * WM + (team == 0 ? 0 : 16 * H), n0 + wn * WN, M,
+                                        N, lane);
+        return;
+    }
+    // K slices: team 1 -> team 0 through LDS, TM/2 rows of blocks at a time
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         __syncthreads();
@@ -1458,9 +1511,6 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_splitk_kernel(
                 }
             }
         }
-    } else if (team == 0) {
-        staged_epilogue<TM, TN, WN, Epi>(epi, acc, smem + wt * (32 * 256), m0 + wm * WM,
-                                         n0 + wn * WN, M, N, lane);
     }
 }
 
