@@ -768,34 +768,38 @@ hipError_t launch_rotate(hipStream_t st, const Loader& ld, uint16_t* out, int64_
 // read of x plus 4 bytes per column per chunk of partials.
 constexpr int kColChunk = 32, kColCols = 2048;
 
+// Chunk c of rows for every block row c = blockIdx.y, blockIdx.y + gridDim.y, ...
+// (the grid's y extent is capped at 65535).
 __global__ __launch_bounds__(256) void colsum_part_kernel(const uint16_t* __restrict__ x,
                                                           float* __restrict__ part, int64_t M,
-                                                          int N) {
+                                                          int N, int chunks) {
     const int n = blockIdx.x * kColCols + threadIdx.x * 8;
     if (n >= N) return;
-    const int64_t m0 = int64_t(blockIdx.y) * kColChunk;
-    const int rows = int(min(int64_t(kColChunk), M - m0));
-    const uint16_t* p = x + m0 * N + n;
-    float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    // eight rows' loads in flight, summed in row order
-    for (int r0 = 0; r0 < rows; r0 += 8) {
-        uint4 v[8];
+    for (int c = blockIdx.y; c < chunks; c += gridDim.y) {
+        const int64_t m0 = int64_t(c) * kColChunk;
+        const int rows = int(min(int64_t(kColChunk), M - m0));
+        const uint16_t* p = x + m0 * N + n;
+        float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        // eight rows' loads in flight, summed in row order
+        for (int r0 = 0; r0 < rows; r0 += 8) {
+            uint4 v[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
-            if (r0 + u < rows) v[u] = *reinterpret_cast<const uint4*>(p + int64_t(r0 + u) * N);
+            for (int u = 0; u < 8; ++u)
+                if (r0 + u < rows) v[u] = *reinterpret_cast<const uint4*>(p + int64_t(r0 + u) * N);
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            if (r0 + u < rows) {
-                a[0] += bf16lo(v[u].x); a[1] += bf16hi(v[u].x);
-                a[2] += bf16lo(v[u].y); a[3] += bf16hi(v[u].y);
-                a[4] += bf16lo(v[u].z); a[5] += bf16hi(v[u].z);
-                a[6] += bf16lo(v[u].w); a[7] += bf16hi(v[u].w);
+            for (int u = 0; u < 8; ++u) {
+                if (r0 + u < rows) {
+                    a[0] += bf16lo(v[u].x); a[1] += bf16hi(v[u].x);
+                    a[2] += bf16lo(v[u].y); a[3] += bf16hi(v[u].y);
+                    a[4] += bf16lo(v[u].z); a[5] += bf16hi(v[u].z);
+                    a[6] += bf16lo(v[u].w); a[7] += bf16hi(v[u].w);
+                }
             }
         }
+        float* o = part + int64_t(c) * N + n;
+        *reinterpret_cast<float4*>(o) = make_float4(a[0], a[1], a[2], a[3]);
+        *reinterpret_cast<float4*>(o + 4) = make_float4(a[4], a[5], a[6], a[7]);
     }
-    float* o = part + int64_t(blockIdx.y) * N + n;
-    *reinterpret_cast<float4*>(o) = make_float4(a[0], a[1], a[2], a[3]);
-    *reinterpret_cast<float4*>(o + 4) = make_float4(a[4], a[5], a[6], a[7]);
 }
 
 // The chunk sums of 64 columns per block of 8 waves: wave w adds chunks w,
@@ -903,8 +907,8 @@ hipError_t column_sum_bf16(hipStream_t st, const void* x, void* out, int64_t M, 
                            float* part) {
     const int chunks = int((M + kColChunk - 1) / kColChunk);
     hipLaunchKernelGGL(colsum_part_kernel, dim3(unsigned((N + kColCols - 1) / kColCols),
-                                                unsigned(chunks)),
-                       dim3(256), 0, st, static_cast<const uint16_t*>(x), part, M, N);
+                                                unsigned(min(chunks, 65535))),
+                       dim3(256), 0, st, static_cast<const uint16_t*>(x), part, M, N, chunks);
     if (const hipError_t e = hipGetLastError(); e != hipSuccess) return e;
     hipLaunchKernelGGL(colsum_final_kernel, dim3(unsigned((N + 63) / 64)), dim3(512), 0, st, part,
                        static_cast<uint16_t*>(out), chunks, N);

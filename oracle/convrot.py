@@ -302,21 +302,27 @@ def column_sum(x_bf16: np.ndarray) -> np.ndarray:
     rounding.)  Returns bf16 bits."""
     x = bf16_to_f32(x_bf16)
     m, n = x.shape
-    chunks = []
-    for c0 in range(0, m, COL_CHUNK):
-        a = np.zeros(n, dtype=np.float32)
-        for r in range(c0, min(m, c0 + COL_CHUNK)):
-            a = (a + x[r]).astype(np.float32)
-        chunks.append(a)
-    lanes = []
-    for w in range(8):
-        a = np.zeros(n, dtype=np.float32)
-        for c in range(w, len(chunks), 8):
-            a = (a + chunks[c]).astype(np.float32)
-        lanes.append(a)
+    # Vectorised over chunks (and then over the eight lanes): every running
+    # sum starts at +0 and only ever adds, so it is never -0, and the +0 rows
+    # and chunks that pad the last chunk and the last group of eight leave it
+    # unchanged -- the same sums as the per-row loop.
+    nc = -(-m // COL_CHUNK)
+    xp = np.zeros((nc * COL_CHUNK, n), dtype=np.float32)
+    xp[:m] = x
+    xp = xp.reshape(nc, COL_CHUNK, n)
+    chunks = np.zeros((nc, n), dtype=np.float32)
+    for r in range(COL_CHUNK):
+        chunks = (chunks + xp[:, r, :]).astype(np.float32)
+    ng = -(-nc // 8)
+    cp = np.zeros((ng * 8, n), dtype=np.float32)
+    cp[:nc] = chunks
+    cp = cp.reshape(ng, 8, n)
+    lanes = np.zeros((8, n), dtype=np.float32)
+    for i in range(ng):
+        lanes = (lanes + cp[i]).astype(np.float32)
     tot = lanes[0]
-    for a in lanes[1:]:
-        tot = (tot + a).astype(np.float32)
+    for w in range(1, 8):
+        tot = (tot + lanes[w]).astype(np.float32)
     return f32_to_bf16(tot)
 
 

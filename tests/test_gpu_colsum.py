@@ -29,6 +29,17 @@ def test_column_sum_exact(dev, m, n):
     assert torch.all((got.float().cpu() - ref).abs() <= ref.abs() * 2.0 ** -7 + 1e-30)
 
 
+def test_column_sum_more_chunks_than_grid_rows(dev):
+    """More 32-row chunks than a launch's 65535 block rows: the partial-sum
+    kernel takes chunks c, c + 65535, ... per block row."""
+    m, n = 65535 * 32 + 100, 16
+    g = torch.Generator().manual_seed(77)
+    dy = (torch.randn(m, n, generator=g) * 1e-3).to(torch.bfloat16)
+    got = int8.column_sum(dy.to(dev))
+    want = O.column_sum(bits(dy))
+    assert np.array_equal(bits(got), want), mismatch(bits(got), want)
+
+
 def test_column_sum_dirty_workspace(dev):
     """The workspace needs no clearing: a call on garbage partials equals one
     on zeros."""
