@@ -1200,9 +1200,10 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_pp_kernel(
 //         and issues its loads for step s + S - 1
 // with one s_barrier between phases.  A team's step is complete (each wave
 // waits for its own loads, then the barrier) before the phase that reads it;
-// its stage is refilled only after the phase that consumed it.  Team 1 then
-// hands its accumulators to team 0 through LDS in two halves (exact int32
-// sums), and team 0 runs the epilogue.
+// its stage is refilled only after the phase that consumed it.  The teams'
+// partial sums then meet in LDS (exact int32 sums): with a dequant epilogue
+// each team finishes half of the tile's rows and both run the epilogue; K
+// slices hand team 1's sums to team 0, which stores the int32 slice.
 template <int S, bool KTAIL, bool WNN, class Epi, bool XT = false>
 __global__ __launch_bounds__(512, 1) void gemm_i8_splitk_kernel(
     const int8_t* __restrict__ X, int64_t ldx, const int8_t* __restrict__ W, int64_t ldw, int M,
