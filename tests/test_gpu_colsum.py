@@ -40,6 +40,33 @@ def test_column_sum_more_chunks_than_grid_rows(dev):
     assert np.array_equal(bits(got), want), mismatch(bits(got), want)
 
 
+def test_column_sum_specials(dev):
+    """NaN and infinities: a column holding a NaN, or both infinities, sums to
+    NaN; one infinity sums to it -- whatever the order, as torch's sum does."""
+    m, n = 100, 32
+    dy = (torch.randn(m, n, generator=torch.Generator().manual_seed(9)) * 1e-3).to(torch.bfloat16)
+    dy[7, 0] = float("nan")
+    dy[3, 1] = float("inf")
+    dy[90, 2] = float("-inf")
+    dy[5, 3] = float("inf")
+    dy[64, 3] = float("-inf")
+    dy[40, 4] = float("nan")
+    dy[41, 4] = float("inf")
+    gb = bits(int8.column_sum(dy.to(dev)))
+    got = torch.from_numpy(O.bf16_to_f32(gb).copy())
+    want = O.column_sum(bits(dy))
+    wnan = np.isnan(O.bf16_to_f32(want))
+    # NaN payloads and signs are the hardware's own; the rest bit for bit
+    assert np.array_equal(np.isnan(got.numpy()), wnan)
+    assert np.array_equal(gb[~wnan], want[~wnan])
+    ref = dy.sum(0).float()
+    assert torch.equal(torch.isnan(got), torch.isnan(ref))
+    assert torch.equal(torch.isinf(got), torch.isinf(ref))
+    assert torch.isnan(got[[0, 3, 4]]).all() and got[1] == float("inf") and got[2] == float("-inf")
+    fin = torch.isfinite(ref)
+    assert torch.all((got[fin] - ref[fin]).abs() <= ref[fin].abs() * 2.0 ** -7 + 1e-30)
+
+
 def test_column_sum_dirty_workspace(dev):
     """The workspace needs no clearing: a call on garbage partials equals one
     on zeros."""
