@@ -42,6 +42,17 @@ def test_group_size(lib):
     assert lib.xpuint8_convrot_groupsize() == 256
 
 
+def test_c_consumer_is_built_and_links():
+    """The plain C caller (tests/c_abi/linear_consumer.c) is built with the
+    library and its dynamic links resolve: run without arguments it prints
+    its usage before any HIP call."""
+    import subprocess
+    binp = os.path.join(ROOT, "tests", "c_abi", "linear_consumer")
+    assert os.path.exists(binp), "not built (run __graft_entry__.build())"
+    r = subprocess.run([binp], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 2 and "usage" in r.stderr, r.stderr
+
+
 P = ctypes.c_void_p(0x1000)   # never dereferenced: validation runs first
 Z = ctypes.c_void_p(0)
 
