@@ -86,6 +86,30 @@ def test_linear_gemm_tiled_matches_row_major(dev, m, n, k):
     assert np.array_equal(outs[0], want), mismatch(outs[0], want)
 
 
+@pytest.mark.parametrize("m,n,k", [(4096, 10240, 1280), (2100, 1296, 2048)])
+@pytest.mark.parametrize("bias_kind", ["fp32", "none"])
+def test_linear_gemm_tiled_bias_forms(dev, m, n, k, bias_kind):
+    """The tiled entry point with an fp32 bias and with none (persistent and
+    split-K kernels), against the oracle's dequant of the exact product."""
+    x = activation(m, k, seed=m + 11 * k)
+    w8, ws = int8.prepare_weight(weight(n, k, seed=n + 2 * k).to(dev))
+    q, s, qt, st = quantize_both(dev, x, m, k)
+    if bias_kind == "fp32":
+        b = (torch.randn(n, generator=torch.Generator().manual_seed(n)) * 0.01).float()
+        barg, bf = b.to(dev), b.numpy()
+    else:
+        barg, bf = None, None
+    lib = L._lib()
+    out = torch.full((m, n), -1, device=dev, dtype=torch.int16).view(torch.bfloat16)
+    rc = lib.xpuint8_linear_gemm_tiled_stream(L._stream(dev), L._ptr(qt), L._ptr(st), L._ptr(w8),
+                                              L._ptr(ws), None if barg is None else L._ptr(barg),
+                                              0, L._ptr(out), m, n, k)
+    assert rc == 0, lib.xpuint8_last_error()
+    want = O.dequant(O.int_mm(q.cpu().numpy(), w8.cpu().numpy()), s.cpu().numpy(),
+                     ws.cpu().numpy(), bf)
+    assert np.array_equal(bits(out), want), mismatch(bits(out), want)
+
+
 def test_linear_gemm_tiled_rejects_other_shapes(dev):
     lib = L._lib()
     p = torch.empty(16, device=dev, dtype=torch.int8)
