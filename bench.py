@@ -252,6 +252,35 @@ def measure_side_rows(torch, int8, lib, L, st, dev, K, W, SET, extra, hbm_line, 
     extra["config3_dequant"] = hbm_line(bytes_dq, timed(torch, deq, K, W, SET),
                                         timed(torch, lambda i: deq(0), K, W, SET), sets=ndq)
     del dq, acc
+
+    # the GEMM the reference itself calls (torch._int_mm, ops.py:634; hipBLASLt
+    # here) against this library's int32 GEMM, cold, on the same int8 operands:
+    # with the standalone dequant and quantize above, the reference's unfused
+    # step on this GPU
+    nim = n_sets(M * Kd + Kd * N + 4 * M * N)
+    im = [(torch.randint(-127, 128, (M, Kd), device=dev, generator=dev_gen(990 + i),
+                         dtype=torch.int8),
+           torch.randint(-127, 128, (Kd, N), device=dev, generator=dev_gen(1090 + i),
+                         dtype=torch.int8)) for i in range(nim)]
+    imw = [b.t().contiguous() for _, b in im]
+    imo = [torch.empty((M, N), device=dev, dtype=torch.int32) for _ in range(nim)]
+    ms_tim = timed(torch, lambda i: torch._int_mm(im[i % nim][0], im[i % nim][1]), K, W, SET)
+
+    def own_i32(i):
+        C(lib.xpuint8_int8_gemm_stream, L._ptr(im[i % nim][0]), L._ptr(imw[i % nim]),
+          L._ptr(imo[i % nim]), M, N, Kd)
+    ms_oim = timed(torch, own_i32, K, W, SET)
+    extra["config3_torch_int_mm"] = {
+        "torch_int_mm_ms_cold": round(ms_tim, 5),
+        "torch_int_mm_TOP/s_cold": round(ops3 / (ms_tim * 1e-3) / 1e12, 1),
+        "xpuint8_int32_gemm_ms_cold": round(ms_oim, 5),
+        "xpuint8_int32_gemm_TOP/s_cold": round(ops3 / (ms_oim * 1e-3) / 1e12, 1),
+        "sets": nim}
+    if "config3_quantize" in extra:
+        extra["config3_torch_int_mm"]["unfused_step_ms_cold"] = round(
+            extra["config3_quantize"]["ms_cold"] + ms_tim + extra["config3_dequant"]["ms_cold"], 5)
+    log(f"[bench] torch._int_mm {ms_tim:.4f} ms cold, this library's int32 GEMM {ms_oim:.4f} ms")
+    del im, imw, imo
     Nq, Nqkv = 3072, 9216
     bytes_sl = 6 * M * Nq + 4 * M + 8 * Nq
     nsl = n_sets(bytes_sl)
