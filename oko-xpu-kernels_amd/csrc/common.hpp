@@ -332,6 +332,35 @@ __device__ __forceinline__ uint32_t pack4(uint32_t a, uint32_t b, uint32_t c, ui
     return __builtin_amdgcn_perm(cd, ab, 0x05040100u);
 }
 
+// The two divisions a quantizer makes per row, as short exact sequences in
+// place of the general correctly rounded division (~10 VALU operations each):
+//
+// div127_rn(x) == x / 127.0f (IEEE) for every x >= 0, +inf included: the
+// product by r = RN(1/127) is within an ulp of the quotient, so its remainder
+// x - 127q is exact in one fma and one correction step with r rounds to the
+// IEEE quotient (the method for a divisor known in advance; a quotient by 127
+// is never within 2^-32 of a rounding boundary, far beyond the step's 2^-47).
+// +inf takes the plain product (the remainder would be NaN).
+//
+// rcp_rn(x) == 1.0f / x (IEEE) for x in [2^-110, 2^122] and for +inf / NaN:
+// one Newton step with fma on v_rcp_f32's approximation.  The range holds
+// every row scale the quantizers form (>= bf16(1e-30) / 127 and <= FLT_MAX /
+// 127); both identities are checked over every float of their range on the
+// device (tests/c_abi/rounding_check.hip).
+__device__ __forceinline__ float div127_rn(float x) {
+    constexpr float r = 1.0f / 127.0f;
+    const float q = x * r;
+    const float e = __builtin_fmaf(-q, 127.0f, x);
+    const float c = __builtin_fmaf(e, r, q);
+    return x <= 3.40282347e38f ? c : q;
+}
+__device__ __forceinline__ float rcp_rn(float x) {
+    const float y = __builtin_amdgcn_rcpf(x);
+    const float e = __builtin_fmaf(-x, y, 1.0f);
+    const float z = __builtin_fmaf(e, y, y);
+    return x <= 3.40282347e38f ? z : y;
+}
+
 // rint(x / s) with x / s the correctly rounded IEEE quotient, for |x/s| <= 127.5:
 // the reciprocal product decides unless it lies within 2^-14 of a half-integer
 // (it differs from the IEEE quotient by at most a few ulp, i.e. < 2^-15 at

@@ -404,9 +404,9 @@ enum QMode : int {
 __device__ __forceinline__ float row_scale(int mode, float rowmax) {
     if (mode == kPrepare) {
         // bf16(1e-30f) = 0x0DA2 << 16
-        return fmaxf(rowmax, __uint_as_float(0x0DA20000u)) / 127.0f;
+        return div127_rn(fmaxf(rowmax, __uint_as_float(0x0DA20000u)));
     }
-    return fmaxf(rowmax / 127.0f, 1e-30f);
+    return fmaxf(div127_rn(rowmax), 1e-30f);
 }
 
 // Quantize 16 values: the values themselves unless ROT, in which case the
@@ -576,7 +576,7 @@ __global__ __launch_bounds__(1024) void rowquant_seg_kernel(Loader load, int8_t*
     if (!live) return;
     const float rowmax = __uint_as_float(row_max[r]);
     const float sc = row_scale(MODE, finish_max<MODE>(rowmax));
-    const float inv = 1.0f / sc;
+    const float inv = rcp_rn(sc);
     if (sg == 0 && sl == 0) scale[row0 + r] = sc;
     int8_t* const qrow = q + row0 * K;
     // the transform leaves register lane_w_rot(sl) of the group in the lane
@@ -623,7 +623,7 @@ __global__ __launch_bounds__(256) void rowquant_2pass_kernel(Loader load, int8_t
     }
     const float rowmax = finish_max<MODE>(wave_max(m));
     const float sc = row_scale(MODE, rowmax);
-    const float inv = 1.0f / sc;
+    const float inv = rcp_rn(sc);
     if (lane == 0) scale[row] = sc;
     for (int s = 0; s < slots; ++s) {
         float v[1][16];
