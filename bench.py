@@ -489,6 +489,7 @@ def main():
     import torch
     from xpu_kernels import int8
     from xpu_kernels.int8 import _lib as L
+    from xpu_kernels.int8 import ops
     if not int8.available():
         raise SystemExit(f"libxpuint8 unavailable: {L._ERR}")
     dev = torch.device("cuda", 0)
@@ -552,6 +553,10 @@ def main():
         sets3.append((dev_act(M, Kd, 200 + i), wi8, wis, dev_weight(1, N, 300 + i, 0.01)[0]))
     log(f"[bench] config 3 linear {M}x{Kd}x{N}: {W} warm-up + {K} timed steps, "
         f"cold over {n3} input sets")
+    # prepare_weight gave each weight its packed copy (the MFMA block layout,
+    # read by the GEMM instead of the row-major codes; same bits): int8.linear
+    # takes it, as it does for any caller of prepare_weight
+    assert all(ops._packed_for(s[1]) is not None for s in sets3)
     if args.only_gemm or args.only_rowquant or args.only_c45:
         ms = ms_warm = float("nan")
     else:
@@ -579,14 +584,22 @@ def main():
 
     def gemm(i):
         xq, xs, wi8, wis, bi, out = gsets[i % ng]
+        lib.xpuint8_linear_gemm_packed_stream(st, L._ptr(xq), L._ptr(xs),
+                                              L._ptr(ops._packed_for(wi8)), L._ptr(wis),
+                                              L._ptr(bi), 1, L._ptr(out), M, N, Kd)
+
+    def gemm_rowmajor(i):
+        xq, xs, wi8, wis, bi, out = gsets[i % ng]
         lib.xpuint8_linear_gemm_tiled_stream(st, L._ptr(xq), L._ptr(xs), L._ptr(wi8), L._ptr(wis),
                                              L._ptr(bi), 1, L._ptr(out), M, N, Kd)
-    ms_gemm = ms_gemm_warm = float("nan")
+    ms_gemm = ms_gemm_warm = ms_gemm_rm = float("nan")
     if not (args.only_rowquant or args.only_c45):
         ms_gemm = timed(torch, gemm, K, W, SET)
+        ms_gemm_rm = timed(torch, gemm_rowmajor, K, W, SET)
     if args.only_gemm:
         print(json.dumps({"only_gemm": True, "gemm_ms_cold": round(ms_gemm, 5),
                           "TOP/s": round(ops3 / (ms_gemm * 1e-3) / 1e12, 1),
+                          "gemm_rowmajor_weight_ms_cold": round(ms_gemm_rm, 5),
                           "steps": K, "warmup": W, "sets": ng}), flush=True)
         return
     if not (args.only_rowquant or args.only_c45):
@@ -611,7 +624,17 @@ def main():
     extra["config3_TOP/s_warm"] = round(ops3 / (ms_warm * 1e-3) / 1e12, 2)
     extra["config3_gemm"] = {"ms_cold": round(ms_gemm, 5), "ms_warm": round(ms_gemm_warm, 5),
                              "TOP/s_cold": round(gemm_tops, 1),
-                             "TOP/s_warm": round(ops3 / (ms_gemm_warm * 1e-3) / 1e12, 1)}
+                             "TOP/s_warm": round(ops3 / (ms_gemm_warm * 1e-3) / 1e12, 1),
+                             "weight": "packed (MFMA block layout)",
+                             "rowmajor_weight_ms_cold": round(ms_gemm_rm, 5)}
+    if not (args.only_rowquant or args.only_c45):
+        # the same step with the weights as the reference stores them
+        # (row-major codes, no packed copy: clones are new storages)
+        sets3r = [(xi, wi8.clone(), wis, bi) for (xi, wi8, wis, bi) in sets3]
+        ms_rm = timed(torch, lambda i: int8.linear(*sets3r[i % n3]), K, W, SET)
+        extra["config3_rowmajor_weight"] = {"step_ms_cold": round(ms_rm, 5),
+                                            "TOP/s_cold": round(ops3 / (ms_rm * 1e-3) / 1e12, 1)}
+        del sets3r
     extra["config3_quantize"] = hbm_line(bytes_q3, ms_q3, ms_q3_warm)
     del gsets
 
@@ -827,9 +850,9 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(gemm_tops, 2), "peak": PEAK_INT8_TOPS,
                      "unit": "TOP/s", "frac": round(gemm_tops / PEAK_INT8_TOPS, 4),
                      "traffic": measured_traffic(),
-                     "kernel": "gemm_i8_pp_kernel (persistent 256x320 ping-pong, x in the MFMA block "
-                               "layout) with dequant epilogue (2*M*N*K int ops per launch, cold "
-                               "operands)"},
+                     "kernel": "gemm_i8_pp_kernel (persistent 256x320 ping-pong, x and the "
+                               "weight's packed copy in the MFMA block layout) with dequant "
+                               "epilogue (2*M*N*K int ops per launch, cold operands)"},
         "extra": extra,
     }
     if not args.no_cpu:

@@ -232,6 +232,50 @@ int xpuint8_ffn_stream(const void *stream, const void *x, const int8_t *up_w8,
  * point above, with no counterpart in the reference. */
 int64_t xpuint8_ffn_workspace_size(int64_t M, int64_t inner, int64_t K, int32_t activation);
 
+/* ---- the packed weight (no counterpart in the reference) ----
+ * A prepared weight w8 int8 [N,K] (row-major, as prepare_weight returns it)
+ * copied into the MFMA block layout of xpuint8_convrot_quantize_tiled_stream
+ * (16-row x 64-byte blocks, each one contiguous 1 KB), the bytes past K zero.
+ * The GEMMs that stream the weight through LDS then load whole cache lines
+ * (one 1 KB block per load) instead of 16 half lines; the results are the
+ * same bits.  The packed copy is derived data: a caller that changes w8
+ * packs it again.  N % 16 == 0, K % 16 == 0. */
+
+/* The bytes of the packed copy of an [N,K] weight (N * K rounded up to whole
+ * blocks), or -1 for an unsupported shape.  No device needed. */
+int64_t xpuint8_packed_weight_bytes(int64_t N, int64_t K);
+
+/* packed = w8 [N,K] in the MFMA block layout (xpuint8_packed_weight_bytes(N, K)
+ * bytes, 16-byte aligned; w8 16-byte aligned). */
+int xpuint8_pack_weight_stream(const void *stream, const int8_t *w8, int8_t *packed, int64_t N,
+                               int64_t K);
+
+/* xpuint8_linear_stream, bit for bit, reading w8_packed (w8 packed by
+ * xpuint8_pack_weight_stream) in the GEMMs that take the block layout and w8
+ * in the others; w8_packed may be null (then it is xpuint8_linear_stream).
+ * The workspace is xpuint8_linear_workspace_size(M, N, K). */
+int xpuint8_linear_packed_stream(const void *stream, const void *x, const int8_t *w8,
+                                 const int8_t *w8_packed, const float *w_scale, const void *bias,
+                                 int32_t bias_bf16, void *out, int64_t M, int64_t N, int64_t K,
+                                 void *work, int64_t work_bytes);
+
+/* xpuint8_linear_gemm_tiled_stream, bit for bit, with the weight given only
+ * packed; the same shapes (others return an error). */
+int xpuint8_linear_gemm_packed_stream(const void *stream, const int8_t *xq, const float *x_scale,
+                                      const int8_t *w8_packed, const float *w_scale,
+                                      const void *bias, int32_t bias_bf16, void *out, int64_t M,
+                                      int64_t N, int64_t K);
+
+/* xpuint8_ffn_stream, bit for bit, with either weight's packed copy (or null)
+ * read where its GEMM takes the block layout.  The workspace is
+ * xpuint8_ffn_workspace_size(M, inner, K, activation). */
+int xpuint8_ffn_packed_stream(const void *stream, const void *x, const int8_t *up_w8,
+                              const int8_t *up_packed, const float *up_scale,
+                              const int8_t *down_w8, const int8_t *down_packed,
+                              const float *down_scale, const void *bias, int32_t bias_bf16,
+                              void *out, int64_t M, int64_t inner, int64_t K, int32_t activation,
+                              void *work, int64_t work_bytes);
+
 /* linear_dx_int8's GEMM: dx[m,k] = bf16(float(sum_n q[m,n] w8[n,k]) * a[m]),
  * the NN product with the row-scale epilogue.  `work` holds w8^T (K*N bytes).
  * Replaces torch._int_mm(q, w8) + dequant(acc, a, ones) at

@@ -241,9 +241,12 @@ size_t linear_work_bytes(int64_t M, int64_t N, int64_t K) {
 }
 
 // quantize + GEMM + dequant of xpuint8_linear_stream on checked arguments.
+// wp (optional): pack_weight's copy of w8, read instead of w8 by the kernels
+// that take the block layout (the split-K and persistent ones).
 int linear_run(hipStream_t st, const void* x, const int8_t* w8, const float* w_scale,
                const void* bias, int32_t bias_bf16, void* out, int64_t M, int64_t N, int64_t K,
-               void* work) {
+               void* work, const int8_t* wp = nullptr) {
+    const int8_t* wb = wp ? wp : w8;
     int8_t* q = static_cast<int8_t*>(work);
     float* xs = reinterpret_cast<float*>(static_cast<char*>(work) + linear_work_q_bytes(M, K));
     const float* b32 = bias_bf16 ? nullptr : static_cast<const float*>(bias);
@@ -264,15 +267,15 @@ int linear_run(hipStream_t st, const void* x, const int8_t* w8, const float* w_s
     // the MFMA block layout; the other shapes a row-major q
     if (splitk_applies(int(M), int(N), int(K)) && rowquant_can_tile(int(K))) {
         XPU_TRY(launched(convrot_quantize_tiled(st, x, q, xs, M, int(K)), "linear (quantize)"));
-        return launched(gemm_dequant_xt(st, q, w8, K, out, N, xs, w_scale, b32, b16, int(M),
-                                        int(N), int(K)),
+        return launched(gemm_dequant_xt(st, q, wb, K, out, N, xs, w_scale, b32, b16, int(M),
+                                        int(N), int(K), wp != nullptr),
                         "linear (gemm)");
     }
     // the persistent kernel reads q in the MFMA block layout too
     if (pp_applies(int(M), int(N), int(K), false) && rowquant_can_tile(int(K))) {
         XPU_TRY(launched(convrot_quantize_tiled(st, x, q, xs, M, int(K)), "linear (quantize)"));
-        return launched(gemm_dequant_pp_xt(st, q, w8, K, out, N, xs, w_scale, b32, b16, int(M),
-                                           int(N), int(K)),
+        return launched(gemm_dequant_pp_xt(st, q, wb, K, out, N, xs, w_scale, b32, b16, int(M),
+                                           int(N), int(K), wp != nullptr),
                         "linear (gemm)");
     }
     XPU_TRY(launched(convrot_quantize(st, x, q, xs, M, int(K), 0), "linear (quantize)"));
@@ -304,6 +307,62 @@ int ffn_check(int64_t M, int64_t inner, int64_t K, int32_t activation) {
     XPU_TRY(check_epilogue(M, K));
     XPU_TRY(check_gemm(M, act_paired(activation) ? 2 * inner : inner, K));
     return check_gemm(M, K, inner);
+}
+
+// The FFN of xpuint8_ffn_stream on checked arguments; up_wp / down_wp
+// (optional) are pack_weight's copies of the two weights.
+int ffn_run(hipStream_t st, const void* x, const int8_t* up_w8, const int8_t* up_wp,
+            const float* up_scale, const int8_t* down_w8, const int8_t* down_wp,
+            const float* down_scale, const void* bias, int32_t bias_bf16, void* out, int64_t M,
+            int64_t inner, int64_t K, int32_t activation, void* work) {
+    char* v = static_cast<char*>(work);
+    char* region = v + ffn_work_region_offset(M, inner);
+    int8_t* xq = reinterpret_cast<int8_t*>(region);
+    float* xs = reinterpret_cast<float*>(region + linear_work_q_bytes(M, K));
+    // the persistent up-projection reads xq in the MFMA block layout
+    if (pp_applies(int(M), int(inner), int(K), act_paired(activation)) &&
+        rowquant_can_tile(int(K))) {
+        XPU_TRY(launched(convrot_quantize_tiled(st, x, xq, xs, M, int(K)), "ffn (quantize)"));
+        XPU_TRY(launched(gemm_act_pp_xt(st, xq, up_wp ? up_wp : up_w8, K, v, inner, xs, up_scale,
+                                        int(M), int(inner), int(K), activation, up_wp != nullptr),
+                         "ffn (up projection)"));
+    } else {
+        XPU_TRY(launched(convrot_quantize(st, x, xq, xs, M, int(K), 0), "ffn (quantize)"));
+        XPU_TRY(launched(gemm_act(st, xq, K, up_w8, K, v, inner, xs, up_scale, int(M),
+                                  int(inner), int(K), activation),
+                         "ffn (up projection)"));
+    }
+    return linear_run(st, v, down_w8, down_scale, bias, bias_bf16, out, M, K, inner, region,
+                      down_wp);
+}
+
+// The checks shared by the one-call linear entry points.
+int linear_check(const void* x, const int8_t* w8, const float* w_scale, const void* bias,
+                 int32_t bias_bf16, const void* out, int64_t M, int64_t N, int64_t K,
+                 const void* work, int64_t work_bytes) {
+    XPU_TRY(check_rows(M, K));
+    XPU_TRY(check_epilogue(M, N));
+    XPU_TRY(check_gemm(M, N, K));
+    XPU_NONNULL(x); XPU_NONNULL(w8); XPU_NONNULL(w_scale); XPU_NONNULL(out); XPU_NONNULL(work);
+    XPU_ALIGNED_OPT(bias);
+    if (bias_bf16 != 0 && bias_bf16 != 1) return fail(2, "bias_bf16 must be 0 or 1");
+    if (work_bytes < int64_t(linear_work_bytes(M, N, K)))
+        return fail(2, "work must hold xpuint8_linear_workspace_size(M, N, K) bytes");
+    return 0;
+}
+
+int ffn_args_check(const void* x, const int8_t* up_w8, const float* up_scale,
+                   const int8_t* down_w8, const float* down_scale, const void* bias,
+                   int32_t bias_bf16, const void* out, int64_t M, int64_t inner, int64_t K,
+                   int32_t activation, const void* work, int64_t work_bytes) {
+    XPU_TRY(ffn_check(M, inner, K, activation));
+    XPU_NONNULL(x); XPU_NONNULL(up_w8); XPU_NONNULL(up_scale); XPU_NONNULL(down_w8);
+    XPU_NONNULL(down_scale); XPU_NONNULL(out); XPU_NONNULL(work);
+    XPU_ALIGNED_OPT(bias);
+    if (bias_bf16 != 0 && bias_bf16 != 1) return fail(2, "bias_bf16 must be 0 or 1");
+    if (work_bytes < int64_t(ffn_work_bytes(M, inner, K)))
+        return fail(2, "work must hold xpuint8_ffn_workspace_size(M, inner, K, activation) bytes");
+    return 0;
 }
 
 int act_ok(int32_t act) {
@@ -554,16 +613,61 @@ int64_t xpuint8_linear_workspace_size(int64_t M, int64_t N, int64_t K) {
 int xpuint8_linear_stream(const void* stream, const void* x, const int8_t* w8,
                           const float* w_scale, const void* bias, int32_t bias_bf16, void* out,
                           int64_t M, int64_t N, int64_t K, void* work, int64_t work_bytes) {
+    XPU_TRY(linear_check(x, w8, w_scale, bias, bias_bf16, out, M, N, K, work, work_bytes));
+    XPU_TRY(ensure_device());
+    return linear_run(as_stream(stream), x, w8, w_scale, bias, bias_bf16, out, M, N, K, work);
+}
+
+int64_t xpuint8_packed_weight_bytes(int64_t N, int64_t K) {
+    if (N <= 0 || K <= 0 || N % 16 != 0 || K % 16 != 0 || N > kMaxDim || K > kMaxK) return -1;
+    return tiled_bytes(N, K);
+}
+
+int xpuint8_pack_weight_stream(const void* stream, const int8_t* w8, int8_t* packed, int64_t N,
+                               int64_t K) {
+    if (N <= 0 || K <= 0 || N % 16 != 0 || K % 16 != 0)
+        return fail(2, "pack_weight: N and K must be positive multiples of 16");
+    if (N > kMaxDim || K > kMaxK) return fail(4, "pack_weight: K must be <= 131072 and N < 2^31");
+    XPU_NONNULL(w8); XPU_NONNULL(packed);
+    XPU_TRY(ensure_device());
+    return launched(pack_weight(as_stream(stream), w8, packed, N, int(K)), "pack_weight");
+}
+
+int xpuint8_linear_packed_stream(const void* stream, const void* x, const int8_t* w8,
+                                 const int8_t* w8_packed, const float* w_scale, const void* bias,
+                                 int32_t bias_bf16, void* out, int64_t M, int64_t N, int64_t K,
+                                 void* work, int64_t work_bytes) {
+    XPU_TRY(linear_check(x, w8, w_scale, bias, bias_bf16, out, M, N, K, work, work_bytes));
+    XPU_ALIGNED_OPT(w8_packed);
+    XPU_TRY(ensure_device());
+    return linear_run(as_stream(stream), x, w8, w_scale, bias, bias_bf16, out, M, N, K, work,
+                      w8_packed);
+}
+
+int xpuint8_linear_gemm_packed_stream(const void* stream, const int8_t* xq, const float* x_scale,
+                                      const int8_t* w8_packed, const float* w_scale,
+                                      const void* bias, int32_t bias_bf16, void* out, int64_t M,
+                                      int64_t N, int64_t K) {
     XPU_TRY(check_rows(M, K));
     XPU_TRY(check_epilogue(M, N));
     XPU_TRY(check_gemm(M, N, K));
-    XPU_NONNULL(x); XPU_NONNULL(w8); XPU_NONNULL(w_scale); XPU_NONNULL(out); XPU_NONNULL(work);
+    XPU_NONNULL(xq); XPU_NONNULL(x_scale); XPU_NONNULL(w8_packed); XPU_NONNULL(w_scale);
+    XPU_NONNULL(out);
     XPU_ALIGNED_OPT(bias);
     if (bias_bf16 != 0 && bias_bf16 != 1) return fail(2, "bias_bf16 must be 0 or 1");
-    if (work_bytes < int64_t(linear_work_bytes(M, N, K)))
-        return fail(2, "work must hold xpuint8_linear_workspace_size(M, N, K) bytes");
     XPU_TRY(ensure_device());
-    return linear_run(as_stream(stream), x, w8, w_scale, bias, bias_bf16, out, M, N, K, work);
+    const float* b32 = bias_bf16 ? nullptr : static_cast<const float*>(bias);
+    const uint16_t* b16 = bias_bf16 ? static_cast<const uint16_t*>(bias) : nullptr;
+    hipStream_t st = as_stream(stream);
+    if (pp_applies(int(M), int(N), int(K), false))
+        return launched(gemm_dequant_pp_xt(st, xq, w8_packed, 0, out, N, x_scale, w_scale, b32,
+                                           b16, int(M), int(N), int(K), true),
+                        "linear_gemm_packed");
+    if (splitk_applies(int(M), int(N), int(K)) && gemm_slices(int(M), int(N), int(K)) == 0)
+        return launched(gemm_dequant_xt(st, xq, w8_packed, 0, out, N, x_scale, w_scale, b32, b16,
+                                        int(M), int(N), int(K), true),
+                        "linear_gemm_packed");
+    return fail(2, "linear_gemm_packed: this shape does not read the block layouts");
 }
 
 int64_t xpuint8_ffn_workspace_size(int64_t M, int64_t inner, int64_t K, int32_t activation) {
@@ -575,33 +679,26 @@ int xpuint8_ffn_stream(const void* stream, const void* x, const int8_t* up_w8,
                        const float* up_scale, const int8_t* down_w8, const float* down_scale,
                        const void* bias, int32_t bias_bf16, void* out, int64_t M, int64_t inner,
                        int64_t K, int32_t activation, void* work, int64_t work_bytes) {
-    XPU_TRY(ffn_check(M, inner, K, activation));
-    XPU_NONNULL(x); XPU_NONNULL(up_w8); XPU_NONNULL(up_scale); XPU_NONNULL(down_w8);
-    XPU_NONNULL(down_scale); XPU_NONNULL(out); XPU_NONNULL(work);
-    XPU_ALIGNED_OPT(bias);
-    if (bias_bf16 != 0 && bias_bf16 != 1) return fail(2, "bias_bf16 must be 0 or 1");
-    if (work_bytes < int64_t(ffn_work_bytes(M, inner, K)))
-        return fail(2, "work must hold xpuint8_ffn_workspace_size(M, inner, K, activation) bytes");
+    XPU_TRY(ffn_args_check(x, up_w8, up_scale, down_w8, down_scale, bias, bias_bf16, out, M,
+                           inner, K, activation, work, work_bytes));
     XPU_TRY(ensure_device());
-    hipStream_t st = as_stream(stream);
-    char* v = static_cast<char*>(work);
-    char* region = v + ffn_work_region_offset(M, inner);
-    int8_t* xq = reinterpret_cast<int8_t*>(region);
-    float* xs = reinterpret_cast<float*>(region + linear_work_q_bytes(M, K));
-    // the persistent up-projection reads xq in the MFMA block layout
-    if (pp_applies(int(M), int(inner), int(K), act_paired(activation)) &&
-        rowquant_can_tile(int(K))) {
-        XPU_TRY(launched(convrot_quantize_tiled(st, x, xq, xs, M, int(K)), "ffn (quantize)"));
-        XPU_TRY(launched(gemm_act_pp_xt(st, xq, up_w8, K, v, inner, xs, up_scale, int(M),
-                                        int(inner), int(K), activation),
-                         "ffn (up projection)"));
-    } else {
-        XPU_TRY(launched(convrot_quantize(st, x, xq, xs, M, int(K), 0), "ffn (quantize)"));
-        XPU_TRY(launched(gemm_act(st, xq, K, up_w8, K, v, inner, xs, up_scale, int(M),
-                                  int(inner), int(K), activation),
-                         "ffn (up projection)"));
-    }
-    return linear_run(st, v, down_w8, down_scale, bias, bias_bf16, out, M, K, inner, region);
+    return ffn_run(as_stream(stream), x, up_w8, nullptr, up_scale, down_w8, nullptr, down_scale,
+                   bias, bias_bf16, out, M, inner, K, activation, work);
+}
+
+int xpuint8_ffn_packed_stream(const void* stream, const void* x, const int8_t* up_w8,
+                              const int8_t* up_packed, const float* up_scale,
+                              const int8_t* down_w8, const int8_t* down_packed,
+                              const float* down_scale, const void* bias, int32_t bias_bf16,
+                              void* out, int64_t M, int64_t inner, int64_t K, int32_t activation,
+                              void* work, int64_t work_bytes) {
+    XPU_TRY(ffn_args_check(x, up_w8, up_scale, down_w8, down_scale, bias, bias_bf16, out, M,
+                           inner, K, activation, work, work_bytes));
+    XPU_ALIGNED_OPT(up_packed);
+    XPU_ALIGNED_OPT(down_packed);
+    XPU_TRY(ensure_device());
+    return ffn_run(as_stream(stream), x, up_w8, up_packed, up_scale, down_w8, down_packed,
+                   down_scale, bias, bias_bf16, out, M, inner, K, activation, work);
 }
 
 int xpuint8_linear_gemm_residual_stream(const void* stream, const int8_t* xq,

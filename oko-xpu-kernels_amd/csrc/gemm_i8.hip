@@ -844,8 +844,10 @@ hipError_t launch_cfg(hipStream_t st, const int8_t* X, int64_t ldx, const int8_t
 // output), so each X block of a step is one contiguous 1 KB load instead of
 // 16 row segments of 64 bytes: 61.1 -> 58.2 us at C3 (cold, timing-only
 // builds of the load pattern), the direct-to-LDS path being bound by the
-// number of cache lines an instruction touches.
-template <int BM, int BN, int WGM, int WGN, int S, bool KTAIL, class Epi, bool XT = false>
+// number of cache lines an instruction touches.  WT: the weight too
+// (pack_weight's copy), 58.1 -> 53.0 us at C3.
+template <int BM, int BN, int WGM, int WGN, int S, bool KTAIL, class Epi, bool XT = false,
+          bool WT = false>
 __global__ __launch_bounds__(512, 1) void gemm_i8_pp_kernel(
     const int8_t* __restrict__ X, int64_t ldx, const int8_t* __restrict__ W, int64_t ldw, int M,
     int N, int K, int tiles_m, int tiles_n, Epi epi) {
@@ -935,6 +937,16 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_pp_kernel(
                     base[i] = xbase;
                     off[i] = (min(m0 + 16 * j + lr, M - 1) - m0) * int(ldx) + lc;
                 }
+            } else if constexpr (WT) {
+                // a block of the packed weight: rows n0 + 16 jb.. (the last
+                // block for blocks past N), or for pairs the value (even jw)
+                // or gate (odd jw) rows of pair jw / 2
+                const int jw = j - XB;
+                const int jb = PAIRED ? jw >> 1 : jw;
+                const int nb = min(n0 / 16 + jb, (N - 1) / 16);
+                const int pb = (PAIRED && (jw & 1)) ? pair_offset(epi) / 16 : 0;
+                base[i] = W + int64_t(pb + nb) * KT * 1024;
+                off[i] = ln * 16;
             } else if constexpr (PAIRED) {
                 const int jw = j - XB;
                 base[i] = (jw & 1) ? gbase : wbase;
@@ -959,9 +971,10 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_pp_kernel(
         for (int i = 0; i < PER; ++i) {
             if (i == PER - 1 && REM != 0 && g != 0) continue;
             const int8_t* p;
-            if (XT && wave + NW * i < XB) {
-                // a tiled X block: K step kstep is the row group's kstep-th
-                // KB; bytes past K in it meet zeros of W
+            if ((XT && wave + NW * i < XB) || (WT && wave + NW * i >= XB)) {
+                // a tiled block: K step kstep is the row group's kstep-th
+                // KB; bytes past K in a tiled X block meet zeros of W (the
+                // packed weight's are zeros)
                 p = base[i] + uint64_t(uint32_t(off[i] + kstep * 1024));
             } else {
                 p = base[i] + uint64_t(uint32_t(off[i] + k0));
@@ -1204,7 +1217,7 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_pp_kernel(
 // partial sums then meet in LDS (exact int32 sums): with a dequant epilogue
 // each team finishes half of the tile's rows and both run the epilogue; K
 // slices hand team 1's sums to team 0, which stores the int32 slice.
-template <int S, bool KTAIL, bool WNN, class Epi, bool XT = false>
+template <int S, bool KTAIL, bool WNN, class Epi, bool XT = false, bool WT = false>
 __global__ __launch_bounds__(512, 1) void gemm_i8_splitk_kernel(
     const int8_t* __restrict__ X, int64_t ldx, const int8_t* __restrict__ W, int64_t ldw, int M,
     int N, int K, int tiles_m, int tiles_n, Epi epi) {
@@ -1216,6 +1229,7 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_splitk_kernel(
     constexpr bool SLICE = IsSliceEpi<Epi>::value;
     static_assert(!Epi::kPaired && (Epi::kStaged || SLICE), "dequant or slice epilogues only");
     static_assert(!SLICE || !XT, "K slices of a row-major X");
+    static_assert(!WT || (!WNN && !SLICE), "the packed weight: whole-K NT products");
     static_assert(2 * RING >= 4 * TN * (TM / 2) * 1024, "half of a team's accumulators fit");
     // K slice blockIdx.y of a split across blocks: K is the slice's length and
     // the operands' rows keep their full strides
@@ -1292,6 +1306,11 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_splitk_kernel(
             krow[i] = 32 * rb + kr;
             base[i] = wbase;
             off[i] = krow[i] * int(ldw) + min(32 * cg + 16 * half, N - n0 - 16);
+        } else if constexpr (WT) {
+            // the packed weight's block n0/16 + (j - XB) (the last one for
+            // blocks past N), one contiguous 1 KB per step
+            base[i] = W + int64_t(min(n0 / 16 + (j - XB), (N - 1) / 16)) * KT * 1024;
+            off[i] = 16 * lane;
         } else {
             base[i] = wbase;
             off[i] = (min(n0 + 16 * (j - XB) + lr, N - 1) - n0) * int(ldw) + lc;
@@ -1310,7 +1329,7 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_splitk_kernel(
             if (WNN && j >= XB) {
                 p = base[i] + uint64_t(uint32_t(off[i]) + uint32_t(k0) * uint32_t(ldw));
                 if (KTAIL && k0 + krow[i] >= K) p = g_zero16;
-            } else if (XT && j < XB) {
+            } else if ((XT && j < XB) || (WT && j >= XB)) {
                 // bytes past K in the last step are multiplied by W's zeros
                 p = base[i] + uint64_t(off[i]) + uint64_t(kt0 + s) * 1024;
             } else {
@@ -1515,17 +1534,19 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_splitk_kernel(
     }
 }
 
-template <bool WNN = false, class Epi, bool XT = false>
+template <bool WNN = false, class Epi, bool XT = false, bool WT = false>
 hipError_t launch_splitk(hipStream_t st, const int8_t* X, int64_t ldx, const int8_t* W,
                          int64_t ldw, int M, int N, int K, const Epi& epi) {
     constexpr int S = 4;                        // 2 x 4 x 18 KB of LDS
     const int tm = (M + 127) / 128, tn = (N + 159) / 160;
     if (K % 64 == 0)
-        hipLaunchKernelGGL((gemm_i8_splitk_kernel<S, false, WNN, Epi, XT>), dim3(unsigned(tm * tn)),
-                           dim3(512), 0, st, X, ldx, W, ldw, M, N, K, tm, tn, epi);
+        hipLaunchKernelGGL((gemm_i8_splitk_kernel<S, false, WNN, Epi, XT, WT>),
+                           dim3(unsigned(tm * tn)), dim3(512), 0, st, X, ldx, W, ldw, M, N, K, tm,
+                           tn, epi);
     else
-        hipLaunchKernelGGL((gemm_i8_splitk_kernel<S, true, WNN, Epi, XT>), dim3(unsigned(tm * tn)),
-                           dim3(512), 0, st, X, ldx, W, ldw, M, N, K, tm, tn, epi);
+        hipLaunchKernelGGL((gemm_i8_splitk_kernel<S, true, WNN, Epi, XT, WT>),
+                           dim3(unsigned(tm * tn)), dim3(512), 0, st, X, ldx, W, ldw, M, N, K, tm,
+                           tn, epi);
     return hipGetLastError();
 }
 
@@ -1734,17 +1755,17 @@ constexpr int kSkinnyPairedM = 256;
 
 // The persistent ping-pong kernel over 256 x 320 tiles, one block per CU (X
 // row-major with row stride ldx, or XT: in the MFMA block layout).
-template <bool XT, class Epi>
+template <bool XT, bool WT = false, class Epi>
 hipError_t launch_pp(hipStream_t st, const int8_t* X, int64_t ldx, const int8_t* W, int64_t ldw,
                      int M, int N, int K, const Epi& epi) {
     constexpr int WGM = Epi::kPaired ? 4 : 2, WGN = 8 / WGM;
     const int tm = (M + 255) / 256, tn = Epi::kPaired ? (N + 159) / 160 : (N + 319) / 320;
     const dim3 grid(unsigned(std::min<int64_t>(int64_t(tm) * tn, device_cus())));
     if (K % 64 == 0)
-        hipLaunchKernelGGL((gemm_i8_pp_kernel<256, 320, WGM, WGN, 4, false, Epi, XT>), grid,
+        hipLaunchKernelGGL((gemm_i8_pp_kernel<256, 320, WGM, WGN, 4, false, Epi, XT, WT>), grid,
                            dim3(512), 0, st, X, ldx, W, ldw, M, N, K, tm, tn, epi);
     else
-        hipLaunchKernelGGL((gemm_i8_pp_kernel<256, 320, WGM, WGN, 4, true, Epi, XT>), grid,
+        hipLaunchKernelGGL((gemm_i8_pp_kernel<256, 320, WGM, WGN, 4, true, Epi, XT, WT>), grid,
                            dim3(512), 0, st, X, ldx, W, ldw, M, N, K, tm, tn, epi);
     return hipGetLastError();
 }
@@ -2066,28 +2087,38 @@ hipError_t gemm_dequant_nn(hipStream_t st, const int8_t* A, int64_t lda, const i
 
 hipError_t gemm_dequant_xt(hipStream_t st, const int8_t* At, const int8_t* B, int64_t ldb,
                            void* out, int64_t ldo, const float* xs, const float* ws,
-                           const float* bias, const uint16_t* bias16, int M, int N, int K) {
-    return launch_splitk<false, EpiDequant, true>(
-        st, At, 0, B, ldb, M, N, K,
-        EpiDequant{static_cast<uint16_t*>(out), ldo, xs, ws, bias, bias16});
+                           const float* bias, const uint16_t* bias16, int M, int N, int K,
+                           bool packed) {
+    const EpiDequant epi{static_cast<uint16_t*>(out), ldo, xs, ws, bias, bias16};
+    if (packed) return launch_splitk<false, EpiDequant, true, true>(st, At, 0, B, 0, M, N, K, epi);
+    return launch_splitk<false, EpiDequant, true>(st, At, 0, B, ldb, M, N, K, epi);
 }
 
 hipError_t gemm_dequant_pp_xt(hipStream_t st, const int8_t* At, const int8_t* B, int64_t ldb,
                               void* out, int64_t ldo, const float* xs, const float* ws,
-                              const float* bias, const uint16_t* bias16, int M, int N, int K) {
-    return launch_pp<true>(st, At, 0, B, ldb, M, N, K,
-                           EpiDequant{static_cast<uint16_t*>(out), ldo, xs, ws, bias, bias16});
+                              const float* bias, const uint16_t* bias16, int M, int N, int K,
+                              bool packed) {
+    const EpiDequant epi{static_cast<uint16_t*>(out), ldo, xs, ws, bias, bias16};
+    if (packed) return launch_pp<true, true>(st, At, 0, B, 0, M, N, K, epi);
+    return launch_pp<true>(st, At, 0, B, ldb, M, N, K, epi);
+}
+
+template <int ACT>
+static hipError_t act_pp_xt(hipStream_t st, const int8_t* At, const int8_t* B, int64_t ldb,
+                            const EpiAct<ACT>& epi, int M, int N, int K, bool packed) {
+    if (packed) return launch_pp<true, true>(st, At, 0, B, 0, M, N, K, epi);
+    return launch_pp<true>(st, At, 0, B, ldb, M, N, K, epi);
 }
 
 hipError_t gemm_act_pp_xt(hipStream_t st, const int8_t* At, const int8_t* B, int64_t ldb,
                           void* out, int64_t ldo, const float* xs, const float* ws, int M, int N,
-                          int K, int act) {
+                          int K, int act, bool packed) {
     uint16_t* o = static_cast<uint16_t*>(out);
     const uint16_t* tab = activation_tables();
     switch (act) {
-        case 3: return launch_pp<true>(st, At, 0, B, ldb, M, N, K, EpiAct<3>{o, ldo, xs, ws, N, tab});
-        case 4: return launch_pp<true>(st, At, 0, B, ldb, M, N, K, EpiAct<4>{o, ldo, xs, ws, N, tab});
-        case 5: return launch_pp<true>(st, At, 0, B, ldb, M, N, K, EpiAct<5>{o, ldo, xs, ws, N, tab});
+        case 3: return act_pp_xt(st, At, B, ldb, EpiAct<3>{o, ldo, xs, ws, N, tab}, M, N, K, packed);
+        case 4: return act_pp_xt(st, At, B, ldb, EpiAct<4>{o, ldo, xs, ws, N, tab}, M, N, K, packed);
+        case 5: return act_pp_xt(st, At, B, ldb, EpiAct<5>{o, ldo, xs, ws, N, tab}, M, N, K, packed);
         default: return hipErrorInvalidValue;
     }
 }
@@ -2152,6 +2183,33 @@ hipError_t dequant_slices(hipStream_t st, const int32_t* acc, int64_t acc_ld, in
 hipError_t transpose_i8(hipStream_t st, const int8_t* in, int8_t* out, int64_t R, int64_t C) {
     const dim3 grid(unsigned((C + 127) / 128), unsigned((R + 127) / 128));
     hipLaunchKernelGGL(transpose_i8_kernel, grid, dim3(256), 0, st, in, out, R, C);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------ packed weight
+// w [N, K] (row-major, K % 16 == 0) in the MFMA block layout (tiled_offset),
+// zeros past K and past N: thread t writes the layout's 16-byte chunk t,
+// position p of row r of its block, which holds the row's chunk p ^ ((r >> 1) & 3)
+__global__ __launch_bounds__(256) void pack_weight_kernel(const int8_t* __restrict__ w,
+                                                          int8_t* __restrict__ out, int64_t N,
+                                                          int K, int KB, int64_t chunks) {
+    const int64_t t = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (t >= chunks) return;
+    const int64_t blk = t >> 6;
+    const int l = int(t & 63), r = l >> 2, c = (l & 3) ^ ((r >> 1) & 3);
+    const int64_t nb = blk / KB;
+    const int k = int(blk - nb * KB) * 64 + 16 * c;
+    const int64_t n = 16 * nb + r;
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    if (n < N && k < K) v = *reinterpret_cast<const uint4*>(w + n * K + k);
+    reinterpret_cast<uint4*>(out)[t] = v;
+}
+
+hipError_t pack_weight(hipStream_t st, const int8_t* w, int8_t* out, int64_t N, int K) {
+    const int KB = (K + 63) / 64;
+    const int64_t chunks = tiled_bytes(N, K) / 16;
+    hipLaunchKernelGGL(pack_weight_kernel, dim3(unsigned((chunks + 255) / 256)), dim3(256), 0, st,
+                       w, out, N, K, KB, chunks);
     return hipGetLastError();
 }
 

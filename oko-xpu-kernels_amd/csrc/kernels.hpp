@@ -64,10 +64,12 @@ hipError_t gemm_dequant_nn(hipStream_t st, const int8_t* A, int64_t lda, const i
 bool splitk_applies(int M, int N, int K);
 bool splitk_nn_applies(int M, int N, int K, int64_t ldb);
 // the split-K dequant GEMMs with A in the MFMA block layout (tiled_offset);
-// callers check splitk_applies first
+// callers check splitk_applies first.  packed: B is pack_weight's copy of the
+// weight (the block layout too; ldb unused)
 hipError_t gemm_dequant_xt(hipStream_t st, const int8_t* At, const int8_t* B, int64_t ldb,
                            void* out, int64_t ldo, const float* xs, const float* ws,
-                           const float* bias, const uint16_t* bias16, int M, int N, int K);
+                           const float* bias, const uint16_t* bias16, int M, int N, int K,
+                           bool packed = false);
 hipError_t gemm_dequant_nn_xt(hipStream_t st, const int8_t* At, const int8_t* Bkn, int64_t ldb,
                               void* out, int64_t ldo, const float* xs, int M, int N, int K);
 // whether the persistent ping-pong kernel takes the dequant GEMM (paired:
@@ -76,10 +78,15 @@ hipError_t gemm_dequant_nn_xt(hipStream_t st, const int8_t* At, const int8_t* Bk
 bool pp_applies(int M, int N, int K, bool paired);
 hipError_t gemm_dequant_pp_xt(hipStream_t st, const int8_t* At, const int8_t* B, int64_t ldb,
                               void* out, int64_t ldo, const float* xs, const float* ws,
-                              const float* bias, const uint16_t* bias16, int M, int N, int K);
+                              const float* bias, const uint16_t* bias16, int M, int N, int K,
+                              bool packed = false);
 hipError_t gemm_act_pp_xt(hipStream_t st, const int8_t* At, const int8_t* B, int64_t ldb,
                           void* out, int64_t ldo, const float* xs, const float* ws, int M, int N,
-                          int K, int act);
+                          int K, int act, bool packed = false);
+// w [N, K] int8 (row-major, K % 16 == 0) in the MFMA block layout, the bytes
+// past K zero: the packed weight the GEMMs above read with packed = true
+// (tiled_bytes(N, K) bytes at out)
+hipError_t pack_weight(hipStream_t st, const int8_t* w, int8_t* out, int64_t N, int K);
 // the same with the residual update out = bf16(res + d * rscale[n]) (bf16 res, rscale)
 hipError_t gemm_dequant_residual(hipStream_t st, const int8_t* A, int64_t lda, const int8_t* B,
                                  int64_t ldb, void* out, int64_t ldo, const float* xs,

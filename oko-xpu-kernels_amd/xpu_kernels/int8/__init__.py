@@ -39,6 +39,7 @@ from .ops import (
     linear_dw,
     linear_dx,
     linear_dx_int8,
+    pack_weight,
     prepare_weight,
     prepare_weight_fused,
     quantize,
@@ -55,6 +56,6 @@ __all__ = [
     "dequant", "dequant_act_quantize", "dequant_slice", "dequant_weight",
     "dequant_weight_torch", "device_name", "expand_scale", "ffn", "ffn_situ", "int8_linear",
     "int_mm", "linear", "linear_acc", "linear_dw", "linear_dx", "linear_dx_int8", "load",
-    "prepare_weight", "prepare_weight_fused", "quantize", "quantize_act", "quantize_row",
+    "pack_weight", "prepare_weight", "prepare_weight_fused", "quantize", "quantize_act", "quantize_row",
     "quantize_row_torch", "rotate", "selftest", "unsupported_reason",
 ]

@@ -42,6 +42,90 @@ def _opt(t):
     return _NULL if t is None else _ptr(t)
 
 
+# ------------------------------------------------------------ packed weights
+# A prepared weight can carry a packed copy: the same int8 codes in the MFMA
+# block layout (xpuint8_pack_weight_stream), which the GEMMs that stream the
+# weight through LDS load as whole cache lines, with the same results.  The
+# copy is keyed by the weight's storage, so that aliases (``detach()``, an
+# Int8Linear buffer) find it; it is used only while the weight's in-place
+# version counter holds the value it was packed at, and it is dropped when
+# the storage is.  Writes the version counter does not see (through
+# ``.data``, DLPack or raw pointers) need a new :func:`pack_weight`.
+_PACKED = {}   # storage data_ptr -> (weakref to the storage, version, shape, packed)
+
+
+def _pack_key(w8):
+    """The registry key of a weight that can carry a packed copy, else None:
+    a CUDA int8 [N, K] tensor (N, K multiples of 16) that starts its storage,
+    is contiguous and 16-byte aligned, and has a version counter (not an
+    inference tensor)."""
+    if not isinstance(w8, torch.Tensor) or w8.dtype != torch.int8 or w8.dim() != 2:
+        return None
+    if not w8.is_cuda or w8.is_inference() or w8.storage_offset() != 0:
+        return None
+    n, k = w8.shape
+    if n == 0 or n % 16 or k == 0 or k % 16 or not w8.is_contiguous() or w8.data_ptr() % 16:
+        return None
+    return w8.untyped_storage().data_ptr()
+
+
+def _drop_packed(key, ref):
+    e = _PACKED.get(key)
+    if e is not None and e[0] is ref:
+        del _PACKED[key]
+
+
+def pack_weight(w8):
+    """Give the prepared weight ``w8`` (int8 [N, K]) a packed copy, read by
+    :func:`linear`, :func:`int8_linear` and :func:`ffn` in place of ``w8``
+    (bit-identical results, faster weight loads).  :func:`prepare_weight`
+    calls it; call it again after writing ``w8`` in a way its version
+    counter does not record.  Returns True if the copy is attached; a weight
+    that cannot be tracked (see ``_pack_key``) gets none and is read as it is.
+    Not during a device-graph capture (the copy would be captured and
+    recomputed on every replay)."""
+    key = _pack_key(w8)
+    if key is None:
+        return False
+    if is_capturing():
+        raise RuntimeError("pack_weight() allocates and writes the packed copy of a weight; "
+                           "inside a device-graph capture it would be recomputed on every "
+                           "replay. Call it before capturing.")
+    import weakref
+    lib = _lib()
+    n, k = w8.shape
+    need = lib.xpuint8_packed_weight_bytes(n, k)
+    if need < 0:
+        return False
+    packed = torch.empty(int(need), device=w8.device, dtype=torch.int8)
+    rc = lib.xpuint8_pack_weight_stream(_stream(w8.device), _ptr(w8), _ptr(packed), n, k)
+    if rc != 0:
+        _err(lib, "pack_weight")
+    st = w8.untyped_storage()
+    old = _PACKED.get(key)
+    if old is not None and old[0]() is st:
+        ref = old[0]
+    else:
+        ref = weakref.ref(st)
+        weakref.finalize(st, _drop_packed, key, ref)
+    _PACKED[key] = (ref, w8._version, (n, k), packed)
+    return True
+
+
+def _packed_for(w8):
+    """The packed copy attached to ``w8`` if it is still valid, else None."""
+    if not _PACKED:
+        return None
+    key = _pack_key(w8)
+    e = _PACKED.get(key) if key is not None else None
+    if e is None:
+        return None
+    ref, version, shape, packed = e
+    if ref() is not w8.untyped_storage() or tuple(w8.shape) != shape or w8._version != version:
+        return None
+    return packed
+
+
 def rotate(x):
     """ConvRot rotation only: bf16 [.., K] in, bf16 [.., K] out (ops.py:26-37)."""
     lib = _lib()
@@ -89,13 +173,15 @@ def quantize_act(x, activation: str):
     return q.reshape(*shape[:-1], k), scale.reshape(shape[:-1])
 
 
-def prepare_weight(w, group: int = 256):
+def prepare_weight(w, group: int = 256, *, pack: bool = True):
     """Prepare an INT8 weight for :func:`linear` (ops.py:83-100).
 
     ``w`` is bf16 or fp32 [N, K] in the unrotated orientation.  Returns
     ``(int8 [N, K], fp32 [N])``.  One kernel, bit-identical to the reference's
     torch chain: rotate to bf16, the bf16 row absmax floored at bf16(1e-30),
-    ``s = amax / 127`` and ``round(wr / s)`` with an IEEE division.
+    ``s = amax / 127`` and ``round(wr / s)`` with an IEEE division.  With
+    ``pack`` (outside a device-graph capture) the codes also get a packed copy
+    (:func:`pack_weight`), another N*K bytes of device memory.
     """
     if w.shape[1] % group:
         raise ValueError(f"K={w.shape[1]} is not a multiple of the group size {group}")
@@ -107,6 +193,8 @@ def prepare_weight(w, group: int = 256):
     rc = lib.xpuint8_prepare_weight_stream(_stream(w.device), _ptr(w2), _ptr(q), _ptr(scale), n, k)
     if rc != 0:
         _err(lib, "prepare_weight")
+    if pack and not is_capturing():
+        pack_weight(q)
     return q, scale
 
 
@@ -564,7 +652,7 @@ def linear(x, w8, w_scale, bias=None, act: Optional[str] = None, residual=None,
         # workspace laid out for the GEMM that reads it
         ws = expand_scale(w_scale, n, x.device)
         b, b16 = _bias_arg(bias, n, x.device)
-        out = _linear_bf16(lib, x2, w8c, ws, b, b16, m, n, k)
+        out = _linear_bf16(lib, x2, w8c, ws, b, b16, m, n, k, _packed_for(w8c))
         return _residual_tail(out, residual, residual_scale, input_dtype, x.shape, m, n)
     if act is None:
         xq, xs = quantize(x2)
@@ -594,14 +682,22 @@ def linear(x, w8, w_scale, bias=None, act: Optional[str] = None, residual=None,
     return _residual_tail(out, residual, residual_scale, input_dtype, x.shape, m, n)
 
 
-def _linear_bf16(lib, x2, w8c, ws, b, b16, m, n, k):
+def _linear_bf16(lib, x2, w8c, ws, b, b16, m, n, k, packed=None):
     """quantize + GEMM + dequant of a bf16 [m, k] through one library call
-    (xpuint8_linear_stream) with its workspace."""
+    (xpuint8_linear_stream, or xpuint8_linear_packed_stream with the weight's
+    packed copy) with its workspace."""
     need = lib.xpuint8_linear_workspace_size(m, n, k)
     if need < 0:
         _err(lib, "linear")
     work = torch.empty(int(need), device=x2.device, dtype=torch.uint8)
     out = torch.empty((m, n), device=x2.device, dtype=torch.bfloat16)
+    if packed is not None:
+        rc = lib.xpuint8_linear_packed_stream(_stream(x2.device), _ptr(x2), _ptr(w8c),
+                                              _ptr(packed), _ptr(ws), _opt(b), b16, _ptr(out), m,
+                                              n, k, _ptr(work), int(need))
+        if rc != 0:
+            _err(lib, "linear")
+        return out
     rc = lib.xpuint8_linear_stream(_stream(x2.device), _ptr(x2), _ptr(w8c), _ptr(ws), _opt(b),
                                    b16, _ptr(out), m, n, k, _ptr(work), int(need))
     if rc != 0:
@@ -716,9 +812,16 @@ def ffn(x, up_w8, up_scale, down_w8, down_scale, down_bias=None, act="situ"):
     # the four (five) kernels in one library call, the intermediates in `work`
     work = torch.empty(int(need), device=device, dtype=torch.uint8)
     out = torch.empty((m, k), device=device, dtype=torch.bfloat16)
-    rc = lib.xpuint8_ffn_stream(_stream(device), _ptr(x2), _ptr(uw8), _ptr(us), _ptr(dw8),
-                                _ptr(ds), _opt(b), b16, _ptr(out), m, inner, k, code,
-                                _ptr(work), int(need))
+    up_p, down_p = _packed_for(uw8), _packed_for(dw8)
+    if up_p is not None or down_p is not None:
+        rc = lib.xpuint8_ffn_packed_stream(_stream(device), _ptr(x2), _ptr(uw8), _opt(up_p),
+                                           _ptr(us), _ptr(dw8), _opt(down_p), _ptr(ds), _opt(b),
+                                           b16, _ptr(out), m, inner, k, code, _ptr(work),
+                                           int(need))
+    else:
+        rc = lib.xpuint8_ffn_stream(_stream(device), _ptr(x2), _ptr(uw8), _ptr(us), _ptr(dw8),
+                                    _ptr(ds), _opt(b), b16, _ptr(out), m, inner, k, code,
+                                    _ptr(work), int(need))
     if rc != 0:
         _err(lib, "ffn")
     out = out.reshape(*x.shape[:-1], k)
@@ -789,7 +892,7 @@ class _TrainableInt8LinearFn(torch.autograd.Function):
 class Int8Linear(torch.nn.Module):
     """Drop-in ``nn.Linear`` replacement with prepared weights (ops.py:831-902)."""
 
-    def __init__(self, w8, w_scale, bias=None, *, backward="dense"):
+    def __init__(self, w8, w_scale, bias=None, *, backward="dense", pack=True):
         super().__init__()
         self.register_buffer("w8", w8.detach())
         self.register_buffer("w_scale", w_scale.detach().to(torch.float32))
@@ -798,13 +901,19 @@ class Int8Linear(torch.nn.Module):
         if backward not in ("dense", "int8"):
             raise ValueError(f"unknown backward mode {backward!r}; use 'dense' or 'int8'")
         self.backward = backward
+        # keep a packed copy of the weight (pack_weight), made again when the
+        # weight moves or is written; False reads w8 as it is
+        self.pack = pack
 
     @classmethod
-    def from_linear(cls, mod, *, backward="dense"):
-        q, scale = prepare_weight(mod.weight.detach())
-        return cls(q, scale, getattr(mod, "bias", None), backward=backward)
+    def from_linear(cls, mod, *, backward="dense", pack=True):
+        q, scale = prepare_weight(mod.weight.detach(), pack=pack)
+        return cls(q, scale, getattr(mod, "bias", None), backward=backward, pack=pack)
 
     def forward(self, x):
+        if (self.pack and _pack_key(self.w8) is not None and _packed_for(self.w8) is None
+                and not is_capturing()):
+            pack_weight(self.w8)
         return int8_linear(x, self.w8, self.w_scale, self.bias, mode=self.backward)
 
     def dense_weight(self, refresh=False):

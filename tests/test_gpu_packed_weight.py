@@ -1,0 +1,207 @@
+"""The packed weight (``pack_weight``; ``xpuint8_pack_weight_stream``): its
+bytes against a torch restatement of the MFMA block layout, and every GEMM
+that reads it -- the persistent kernel (config 3's shape and a ragged batch),
+the split-K kernel (the N = 1280 shapes, a ragged one), both projections of
+the FFN -- bit for bit the row-major weight's result and the oracle's; shapes
+whose GEMMs read the weight row-major (K slices, the skinny kernel) through
+the packed entry point; and the rules that decide when the copy is used (an
+in-place write, an alias, an offset view, a module's weight moved or written,
+a storage that is freed)."""
+
+import gc
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from gpu_util import activation, bits, mismatch, npy, weight
+from xpu_kernels import int8
+from xpu_kernels.int8 import _lib as L
+from xpu_kernels.int8 import ops
+
+pytestmark = pytest.mark.gpu
+
+
+def block_layout(w8):
+    """w8 int8 [N, K] (N % 16 == 0, K % 16 == 0) in the MFMA block layout:
+    16-row x 64-byte blocks, block (n/16, k/64) at ((n/16) * ceil(K/64) +
+    k/64) * 1024, row r at 64r and at position p the row's 16-byte chunk
+    p ^ ((r >> 1) & 3); zeros past K."""
+    w = w8.cpu()
+    n, k = w.shape
+    kp = (k + 63) // 64 * 64
+    if kp != k:
+        w = torch.cat([w, torch.zeros(n, kp - k, dtype=torch.int8)], dim=1)
+    b = w.reshape(n // 16, 16, kp // 64, 4, 16).permute(0, 2, 1, 3, 4)   # nb, kb, r, c, byte
+    r = torch.arange(16).view(16, 1)
+    p = torch.arange(4).view(1, 4)
+    src = (p ^ ((r >> 1) & 3)).view(1, 1, 16, 4, 1).expand(n // 16, kp // 64, 16, 4, 16)
+    return torch.gather(b, 3, src).reshape(-1)
+
+
+@pytest.mark.parametrize("n,k", [(10240, 1280), (1280, 5120), (48, 1296), (16, 16), (32, 272)])
+def test_pack_layout_exact(dev, n, k):
+    g = torch.Generator().manual_seed(n + k)
+    w8 = torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8)
+    lib = L._lib()
+    need = lib.xpuint8_packed_weight_bytes(n, k)
+    assert need == (n // 16) * ((k + 63) // 64) * 1024
+    packed = torch.full((need,), 99, device=dev, dtype=torch.int8)
+    wd = w8.to(dev)
+    assert lib.xpuint8_pack_weight_stream(L._stream(dev), L._ptr(wd), L._ptr(packed), n, k) == 0, \
+        lib.xpuint8_last_error()
+    assert torch.equal(packed.cpu(), block_layout(w8))
+
+
+def test_pack_rejects_bad_shapes(dev):
+    lib = L._lib()
+    assert lib.xpuint8_packed_weight_bytes(24, 64) == -1
+    assert lib.xpuint8_packed_weight_bytes(16, 40) == -1
+    w = torch.zeros(32, 64, device=dev, dtype=torch.int8)
+    assert lib.xpuint8_pack_weight_stream(L._stream(dev), L._ptr(w), L._ptr(w), 24, 64) != 0
+    assert b"multiples of 16" in lib.xpuint8_last_error()
+
+
+def _both(dev, n, k, seed):
+    """The same weight prepared with and without its packed copy."""
+    w = weight(n, k, seed=seed).to(dev)
+    w8p, ws = int8.prepare_weight(w)
+    w8r, ws_r = int8.prepare_weight(w, pack=False)
+    assert torch.equal(w8p, w8r) and torch.equal(ws, ws_r)
+    assert ops._packed_for(w8p) is not None and ops._packed_for(w8r) is None
+    return w8p, w8r, ws
+
+
+# (M, N, K): the persistent kernel (config 3; a batch that is not a multiple
+# of 256), the split-K kernel (the SDXL N = 1280 shapes; ragged rows and a
+# last column tile of 16), K slices (M = 200, 512) and the skinny kernel (M = 16).
+LINEAR_SHAPES = [(4096, 10240, 1280), (3000, 10240, 1280), (4096, 1280, 5120),
+                 (4096, 1280, 2048), (4096, 1280, 1280), (2100, 1296, 2048), (200, 1280, 4096),
+                 (512, 4096, 4096), (16, 4096, 4096)]
+
+
+@pytest.mark.parametrize("m,n,k", LINEAR_SHAPES)
+def test_linear_packed_equals_rowmajor(dev, m, n, k):
+    w8p, w8r, ws = _both(dev, n, k, seed=n + 11)
+    x = activation(m, k, seed=m + k).to(dev)
+    bias = weight(1, n, seed=5, std=0.01)[0].to(dev)
+    yp = int8.linear(x, w8p, ws, bias)
+    yr = int8.linear(x, w8r, ws, bias)
+    assert np.array_equal(bits(yp), bits(yr)), mismatch(bits(yp), bits(yr))
+
+
+@pytest.mark.parametrize("m,n,k", [(4096, 10240, 1280), (4096, 1280, 1280), (1100, 1296, 2048)])
+def test_linear_packed_exact(dev, m, n, k):
+    w8p, _, ws = _both(dev, n, k, seed=n + 13)
+    x = activation(m, k, seed=2 * m + k)
+    bias = weight(1, n, seed=6, std=0.01)[0]
+    y = int8.linear(x.to(dev), w8p, ws, bias.to(dev))
+    want = O.linear(bits(x), npy(w8p), npy(ws), O.bf16_to_f32(bits(bias)))
+    assert np.array_equal(bits(y), want), mismatch(bits(y), want)
+
+
+def test_linear_gemm_packed_entry(dev):
+    """xpuint8_linear_gemm_packed_stream against xpuint8_linear_gemm_tiled_stream
+    (the block-layout x, row-major weight) at config 3 and a split-K shape."""
+    lib = L._lib()
+    for m, n, k in [(4096, 10240, 1280), (4096, 1280, 5120)]:
+        w8p, _, ws = _both(dev, n, k, seed=n + 17)
+        x = activation(m, k, seed=m + 3).to(dev)
+        tb = ((m + 15) // 16) * ((k + 63) // 64) * 1024
+        xq = torch.empty(tb, device=dev, dtype=torch.int8)
+        xs = torch.empty(m, device=dev, dtype=torch.float32)
+        st = L._stream(dev)
+        assert lib.xpuint8_convrot_quantize_tiled_stream(st, L._ptr(x), L._ptr(xq), L._ptr(xs),
+                                                         m, k) == 0
+        b = weight(1, n, seed=8, std=0.01)[0].to(dev)
+        o1 = torch.empty((m, n), device=dev, dtype=torch.bfloat16)
+        o2 = torch.empty((m, n), device=dev, dtype=torch.bfloat16)
+        assert lib.xpuint8_linear_gemm_tiled_stream(st, L._ptr(xq), L._ptr(xs), L._ptr(w8p),
+                                                    L._ptr(ws), L._ptr(b), 1, L._ptr(o1),
+                                                    m, n, k) == 0
+        packed = ops._packed_for(w8p)
+        assert lib.xpuint8_linear_gemm_packed_stream(st, L._ptr(xq), L._ptr(xs), L._ptr(packed),
+                                                     L._ptr(ws), L._ptr(b), 1, L._ptr(o2),
+                                                     m, n, k) == 0, lib.xpuint8_last_error()
+        assert np.array_equal(bits(o1), bits(o2)), mismatch(bits(o1), bits(o2))
+    # a shape whose GEMM reads neither block layout is refused
+    xq = torch.zeros(16 * 4096, device=dev, dtype=torch.int8)
+    xs = torch.ones(16, device=dev)
+    o = torch.empty((16, 4096), device=dev, dtype=torch.bfloat16)
+    w8p, _, ws = _both(dev, 4096, 4096, seed=1)
+    assert lib.xpuint8_linear_gemm_packed_stream(L._stream(dev), L._ptr(xq), L._ptr(xs),
+                                                 L._ptr(ops._packed_for(w8p)), L._ptr(ws), None,
+                                                 0, L._ptr(o), 16, 4096, 4096) != 0
+
+
+# (M, K, inner, act): config 4 (GEGLU), a ragged batch, GELU-erf (an
+# unpaired up-projection), situ at a batch small enough for K slices below
+@pytest.mark.parametrize("m,k,inner,act", [(4096, 1280, 5120, "geglu_erf"),
+                                           (2100, 1280, 5120, "geglu_erf"),
+                                           (4096, 1280, 5120, "gelu_erf"),
+                                           (256, 1280, 5120, "situ")])
+def test_ffn_packed_equals_rowmajor(dev, m, k, inner, act):
+    up_rows = 2 * inner if act in ("geglu_erf", "situ") else inner
+    up_p, up_r, us = _both(dev, up_rows, k, seed=up_rows + 1)
+    dn_p, dn_r, ds = _both(dev, k, inner, seed=inner + 2)
+    x = activation(m, k, seed=m + 7).to(dev)
+    b = weight(1, k, seed=9, std=0.01)[0].to(dev)
+    yp = int8.ffn(x, up_p, us, dn_p, ds, b, act=act)
+    yr = int8.ffn(x, up_r, us, dn_r, ds, b, act=act)
+    assert np.array_equal(bits(yp), bits(yr)), mismatch(bits(yp), bits(yr))
+    # one weight packed, the other not
+    ym = int8.ffn(x, up_r, us, dn_p, ds, b, act=act)
+    assert np.array_equal(bits(ym), bits(yr)), mismatch(bits(ym), bits(yr))
+
+
+def test_packed_copy_follows_inplace_writes(dev):
+    n, k, m = 10240, 1280, 4096
+    w8, ws = int8.prepare_weight(weight(n, k, seed=21).to(dev))
+    x = activation(m, k, seed=22).to(dev)
+    w8[100:116, :64] = 5                        # in place: the copy is stale from here
+    assert ops._packed_for(w8) is None
+    y_stale_safe = int8.linear(x, w8, ws)       # reads w8 itself
+    w8r = w8.clone()
+    y_ref = int8.linear(x, w8r, ws)
+    assert np.array_equal(bits(y_stale_safe), bits(y_ref))
+    assert int8.pack_weight(w8) and ops._packed_for(w8) is not None
+    y_new = int8.linear(x, w8, ws)
+    assert np.array_equal(bits(y_new), bits(y_ref)), mismatch(bits(y_new), bits(y_ref))
+
+
+def test_packed_copy_aliases_and_views(dev):
+    n, k = 4096, 1280
+    w8, ws = int8.prepare_weight(weight(2 * n, k, seed=23).to(dev))
+    assert ops._packed_for(w8.detach()) is not None         # an alias finds it
+    assert ops._packed_for(w8[n:]) is None                  # offset view: not the packed rows
+    assert ops._packed_for(w8[:n]) is None                  # another shape over the storage
+    x = activation(4096, k, seed=24).to(dev)
+    y = int8.linear(x, w8[n:], ws[n:])
+    y_ref = int8.linear(x, w8[n:].clone(), ws[n:])
+    assert np.array_equal(bits(y), bits(y_ref))
+    key = w8.untyped_storage().data_ptr()
+    assert key in ops._PACKED
+    del w8, y
+    gc.collect()
+    assert key not in ops._PACKED                            # freed with the storage
+
+
+def test_int8linear_packs_its_weight(dev):
+    n, k = 10240, 1280
+    w = weight(n, k, seed=25).to(dev)
+    w8r, ws = int8.prepare_weight(w, pack=False)
+    mod = int8.Int8Linear(w8r, ws, weight(1, n, seed=26, std=0.01)[0].to(dev))
+    x = activation(4096, k, seed=27).to(dev)
+    y1 = mod(x)                                              # packs on first use
+    assert ops._packed_for(mod.w8) is not None
+    y0 = int8.linear(x, w8r.clone(), ws, mod.bias)
+    assert np.array_equal(bits(y1), bits(y0))
+    with torch.no_grad():
+        mod.w8[0, :16] = -3                                  # in place: packed again on use
+    y2 = mod(x)
+    y2_ref = int8.linear(x, mod.w8.clone(), ws, mod.bias)
+    assert np.array_equal(bits(y2), bits(y2_ref))
+    off = int8.Int8Linear(w8r.clone(), ws, pack=False)
+    off(x)
+    assert ops._packed_for(off.w8) is None
