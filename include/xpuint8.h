@@ -276,6 +276,25 @@ int xpuint8_ffn_packed_stream(const void *stream, const void *x, const int8_t *u
                               void *out, int64_t M, int64_t inner, int64_t K, int32_t activation,
                               void *work, int64_t work_bytes);
 
+/* The weight's second packed form, for linear_dx_int8's product q @ w8 (the
+ * contraction over w8's rows): w8 [N,K] in the NN stage order of that GEMM,
+ * per 64 rows and 32 columns two 1 KB blocks of 32 rows x 32 bytes (block
+ * ((s * K/32 + c) * 2 + h) * 1024 for rows 64s + 32h.. and columns 32c..; in
+ * it, 16-byte chunk l holds row l/2, column half (l & 1) ^ ((l >> 5) & 1)),
+ * zeros past N.  xpuint8_packed_weight_nn_bytes(N, K) = ceil(N/64) * 64 * K,
+ * or -1 (N % 16 == 0, K % 32 == 0 required).  No device needed for the size. */
+int64_t xpuint8_packed_weight_nn_bytes(int64_t N, int64_t K);
+int xpuint8_pack_weight_nn_stream(const void *stream, const int8_t *w8, int8_t *packed, int64_t N,
+                                  int64_t K);
+
+/* xpuint8_linear_dx_int8_stream, bit for bit, reading w8_packed_nn (w8 packed
+ * by xpuint8_pack_weight_nn_stream; null reads w8) where the split-K GEMM
+ * takes the product. */
+int xpuint8_linear_dx_int8_packed_stream(const void *stream, const void *dy, const float *w_scale,
+                                         const int8_t *w8, const int8_t *w8_packed_nn, void *dx,
+                                         int64_t M, int64_t N, int64_t K, void *work,
+                                         int64_t work_bytes);
+
 /* linear_dx_int8's GEMM: dx[m,k] = bf16(float(sum_n q[m,n] w8[n,k]) * a[m]),
  * the NN product with the row-scale epilogue.  `work` holds w8^T (K*N bytes).
  * Replaces torch._int_mm(q, w8) + dequant(acc, a, ones) at

@@ -172,8 +172,9 @@ int check_dx(int64_t M, int64_t N, int64_t K) {
 
 // quantize_row (column-scaled) -> w8^T -> GEMM with the row-scale epilogue ->
 // inverse rotation, all on one stream, through the workspace at `work`.
+// wnn (optional): pack_weight_nn's copy of w8, read by the split-K GEMM.
 int dx_chain(hipStream_t st, const void* dy, const float* w_scale, const int8_t* w8, void* dx,
-             int64_t M, int64_t N, int64_t K, char* work) {
+             int64_t M, int64_t N, int64_t K, char* work, const int8_t* wnn = nullptr) {
     const DxWork L = dx_work_layout(M, N, K);
     int8_t* q = reinterpret_cast<int8_t*>(work + L.q);
     float* a = reinterpret_cast<float*>(work + L.a);
@@ -185,7 +186,8 @@ int dx_chain(hipStream_t st, const void* dy, const float* w_scale, const int8_t*
     if (splitk_nn_applies(int(M), int(K), int(N), K) && rowquant_can_tile(int(N))) {
         XPU_TRY(launched(quantize_row(st, dy, w_scale, q, a, M, int(N), true),
                          "linear_dx_int8 (quantize_row)"));
-        XPU_TRY(launched(gemm_dequant_nn_xt(st, q, w8, K, pre, K, a, int(M), int(K), int(N)),
+        XPU_TRY(launched(gemm_dequant_nn_xt(st, q, wnn ? wnn : w8, K, pre, K, a, int(M), int(K),
+                                            int(N), wnn != nullptr),
                          "linear_dx_int8 (gemm)"));
         return launched(rotate_bf16(st, pre, dx, M, int(K)), "linear_dx_int8 (rotate)");
     }
@@ -780,6 +782,35 @@ int xpuint8_linear_dx_int8_stream(const void* stream, const void* dy, const floa
         return fail(2, "work must hold xpuint8_linear_dx_int8_workspace_size(M, N, K) bytes");
     XPU_TRY(ensure_device());
     return dx_chain(as_stream(stream), dy, w_scale, w8, dx, M, N, K, static_cast<char*>(work));
+}
+
+int64_t xpuint8_packed_weight_nn_bytes(int64_t N, int64_t K) {
+    if (N <= 0 || K <= 0 || N % 16 != 0 || K % 32 != 0 || N > kMaxK || K > kMaxDim) return -1;
+    return packed_nn_bytes(N, K);
+}
+
+int xpuint8_pack_weight_nn_stream(const void* stream, const int8_t* w8, int8_t* packed, int64_t N,
+                                  int64_t K) {
+    if (N <= 0 || K <= 0 || N % 16 != 0 || K % 32 != 0)
+        return fail(2, "pack_weight_nn: N must be a positive multiple of 16 and K of 32");
+    if (N > kMaxK || K > kMaxDim) return fail(4, "pack_weight_nn: N must be <= 131072 and K < 2^31");
+    XPU_NONNULL(w8); XPU_NONNULL(packed);
+    XPU_TRY(ensure_device());
+    return launched(pack_weight_nn(as_stream(stream), w8, packed, N, int(K)), "pack_weight_nn");
+}
+
+int xpuint8_linear_dx_int8_packed_stream(const void* stream, const void* dy, const float* w_scale,
+                                         const int8_t* w8, const int8_t* w8_packed_nn, void* dx,
+                                         int64_t M, int64_t N, int64_t K, void* work,
+                                         int64_t work_bytes) {
+    XPU_TRY(check_dx(M, N, K));
+    XPU_NONNULL(dy); XPU_NONNULL(w_scale); XPU_NONNULL(w8); XPU_NONNULL(dx); XPU_NONNULL(work);
+    XPU_ALIGNED_OPT(w8_packed_nn);
+    if (work_bytes < int64_t(dx_work_layout(M, N, K).total))
+        return fail(2, "work must hold xpuint8_linear_dx_int8_workspace_size(M, N, K) bytes");
+    XPU_TRY(ensure_device());
+    return dx_chain(as_stream(stream), dy, w_scale, w8, dx, M, N, K, static_cast<char*>(work),
+                    w8_packed_nn);
 }
 
 int xpuint8_linear_dx_int8_noalloc_stream(const void* stream, const void* dy,

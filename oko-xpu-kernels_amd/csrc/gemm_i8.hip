@@ -1229,7 +1229,7 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_splitk_kernel(
     constexpr bool SLICE = IsSliceEpi<Epi>::value;
     static_assert(!Epi::kPaired && (Epi::kStaged || SLICE), "dequant or slice epilogues only");
     static_assert(!SLICE || !XT, "K slices of a row-major X");
-    static_assert(!WT || (!WNN && !SLICE), "the packed weight: whole-K NT products");
+    static_assert(!WT || !SLICE, "the packed weights: whole-K products");
     static_assert(2 * RING >= 4 * TN * (TM / 2) * 1024, "half of a team's accumulators fit");
     // K slice blockIdx.y of a split across blocks: K is the slice's length and
     // the operands' rows keep their full strides
@@ -1282,7 +1282,10 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_splitk_kernel(
     // 32rb.. and columns 32cg..; row r of a block is 32 bytes at 32r, its two
     // 16-byte halves swapped when r & 16 (so that the transposing fragment
     // reads of rows r and r + 16 fall on different banks).  DMA lane l fills
-    // row l/2, stored half l%2.
+    // row l/2, stored half l%2.  With WT the weight comes packed in that
+    // stage order (pack_weight_nn: block (s, n/32, rb) the 1 KB at
+    // ((s * N/32 + n/32) * 2 + rb) * 1024, zeros past K), one contiguous load
+    // per block instead of 32 quarter lines; N % 32 == 0.
     const int8_t* const wbase = WNN ? W + n0 : W + int64_t(n0) * ldw;
     const int8_t* base[PER];
     int off[PER];
@@ -1304,8 +1307,13 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_splitk_kernel(
             const int jj = j - XB, rb = jj / 5, cg = jj - 5 * rb;
             const int kr = lane >> 1, half = (lane & 1) ^ ((kr >> 4) & 1);
             krow[i] = 32 * rb + kr;
-            base[i] = wbase;
-            off[i] = krow[i] * int(ldw) + min(32 * cg + 16 * half, N - n0 - 16);
+            if constexpr (WT) {
+                base[i] = W + int64_t(min(n0 / 32 + cg, N / 32 - 1) * 2 + rb) * 1024;
+                off[i] = 16 * lane;
+            } else {
+                base[i] = wbase;
+                off[i] = krow[i] * int(ldw) + min(32 * cg + 16 * half, N - n0 - 16);
+            }
         } else if constexpr (WT) {
             // the packed weight's block n0/16 + (j - XB) (the last one for
             // blocks past N), one contiguous 1 KB per step
@@ -1326,7 +1334,10 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_splitk_kernel(
             if (i == PER - 1 && !full_share) break;
             const int j = wt + 4 * i;
             const int8_t* p;
-            if (WNN && j >= XB) {
+            if (WNN && WT && j >= XB) {
+                // a packed step is N / 32 x 2 blocks (N * 64 bytes)
+                p = base[i] + uint64_t(off[i]) + uint64_t(kt0 + s) * uint64_t(N) * 64;
+            } else if (WNN && j >= XB) {
                 p = base[i] + uint64_t(uint32_t(off[i]) + uint32_t(k0) * uint32_t(ldw));
                 if (KTAIL && k0 + krow[i] >= K) p = g_zero16;
             } else if ((XT && j < XB) || (WT && j >= XB)) {
@@ -2124,10 +2135,11 @@ hipError_t gemm_act_pp_xt(hipStream_t st, const int8_t* At, const int8_t* B, int
 }
 
 hipError_t gemm_dequant_nn_xt(hipStream_t st, const int8_t* At, const int8_t* Bkn, int64_t ldb,
-                              void* out, int64_t ldo, const float* xs, int M, int N, int K) {
-    return launch_splitk<true, EpiDequant, true>(
-        st, At, 0, Bkn, ldb, M, N, K,
-        EpiDequant{static_cast<uint16_t*>(out), ldo, xs, nullptr, nullptr, nullptr});
+                              void* out, int64_t ldo, const float* xs, int M, int N, int K,
+                              bool packed) {
+    const EpiDequant epi{static_cast<uint16_t*>(out), ldo, xs, nullptr, nullptr, nullptr};
+    if (packed) return launch_splitk<true, EpiDequant, true, true>(st, At, 0, Bkn, 0, M, N, K, epi);
+    return launch_splitk<true, EpiDequant, true>(st, At, 0, Bkn, ldb, M, N, K, epi);
 }
 
 hipError_t gemm_dequant_residual(hipStream_t st, const int8_t* A, int64_t lda, const int8_t* B,
@@ -2210,6 +2222,38 @@ hipError_t pack_weight(hipStream_t st, const int8_t* w, int8_t* out, int64_t N, 
     const int64_t chunks = tiled_bytes(N, K) / 16;
     hipLaunchKernelGGL(pack_weight_kernel, dim3(unsigned((chunks + 255) / 256)), dim3(256), 0, st,
                        w, out, N, K, KB, chunks);
+    return hipGetLastError();
+}
+
+// w [R, C] (row-major: R contraction rows, C = the product's columns, C % 32
+// == 0) in the NN stage order of the split-K kernel: per 64-row step s, per
+// 32-column group cb, per 32-row half rb the 1 KB block ((s * C/32 + cb) * 2 +
+// rb) * 1024, in which 16-byte chunk l holds row l/2 of the half, column half
+// (l & 1) ^ ((l >> 5) & 1) of the group; zeros past R
+__global__ __launch_bounds__(256) void pack_weight_nn_kernel(const int8_t* __restrict__ w,
+                                                             int8_t* __restrict__ out, int64_t R,
+                                                             int C, int64_t chunks) {
+    const int64_t t = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (t >= chunks) return;
+    const int64_t blk = t >> 6;
+    const int l = int(t & 63), kr = l >> 1, h = (l & 1) ^ ((kr >> 4) & 1);
+    const int groups = C / 32;
+    const int rb = int(blk & 1);
+    const int64_t sg = blk >> 1;
+    const int64_t step = sg / groups;
+    const int cb = int(sg - step * groups);
+    const int64_t r = 64 * step + 32 * rb + kr;
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    if (r < R) v = *reinterpret_cast<const uint4*>(w + r * C + 32 * cb + 16 * h);
+    reinterpret_cast<uint4*>(out)[t] = v;
+}
+
+int64_t packed_nn_bytes(int64_t R, int64_t C) { return ((R + 63) / 64) * 64 * C; }
+
+hipError_t pack_weight_nn(hipStream_t st, const int8_t* w, int8_t* out, int64_t R, int C) {
+    const int64_t chunks = packed_nn_bytes(R, C) / 16;
+    hipLaunchKernelGGL(pack_weight_nn_kernel, dim3(unsigned((chunks + 255) / 256)), dim3(256), 0,
+                       st, w, out, R, C, chunks);
     return hipGetLastError();
 }
 

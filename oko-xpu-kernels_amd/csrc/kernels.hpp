@@ -71,7 +71,8 @@ hipError_t gemm_dequant_xt(hipStream_t st, const int8_t* At, const int8_t* B, in
                            const float* bias, const uint16_t* bias16, int M, int N, int K,
                            bool packed = false);
 hipError_t gemm_dequant_nn_xt(hipStream_t st, const int8_t* At, const int8_t* Bkn, int64_t ldb,
-                              void* out, int64_t ldo, const float* xs, int M, int N, int K);
+                              void* out, int64_t ldo, const float* xs, int M, int N, int K,
+                              bool packed = false);
 // whether the persistent ping-pong kernel takes the dequant GEMM (paired:
 // the FFN's up-projection) of this shape, and those GEMMs with A in the MFMA
 // block layout on that kernel
@@ -87,6 +88,11 @@ hipError_t gemm_act_pp_xt(hipStream_t st, const int8_t* At, const int8_t* B, int
 // past K zero: the packed weight the GEMMs above read with packed = true
 // (tiled_bytes(N, K) bytes at out)
 hipError_t pack_weight(hipStream_t st, const int8_t* w, int8_t* out, int64_t N, int K);
+// w [R, C] int8 (row-major, C % 32 == 0) in the split-K kernel's NN stage
+// order, the rows past R zero (packed_nn_bytes(R, C) bytes): the NN products'
+// packed right operand (gemm_dequant_nn_xt with packed = true)
+int64_t packed_nn_bytes(int64_t R, int64_t C);
+hipError_t pack_weight_nn(hipStream_t st, const int8_t* w, int8_t* out, int64_t R, int C);
 // the same with the residual update out = bf16(res + d * rscale[n]) (bf16 res, rscale)
 hipError_t gemm_dequant_residual(hipStream_t st, const int8_t* A, int64_t lda, const int8_t* B,
                                  int64_t ldb, void* out, int64_t ldo, const float* xs,

@@ -51,7 +51,9 @@ def _opt(t):
 # version counter holds the value it was packed at, and it is dropped when
 # the storage is.  Writes the version counter does not see (through
 # ``.data``, DLPack or raw pointers) need a new :func:`pack_weight`.
-_PACKED = {}   # storage data_ptr -> (weakref to the storage, version, shape, packed)
+# storage data_ptr -> [weakref to the storage, version, shape, packed, packed_nn]
+# (packed_nn: the form linear_dx_int8's product reads, made at its first use)
+_PACKED = {}
 
 
 def _pack_key(w8):
@@ -108,22 +110,49 @@ def pack_weight(w8):
     else:
         ref = weakref.ref(st)
         weakref.finalize(st, _drop_packed, key, ref)
-    _PACKED[key] = (ref, w8._version, (n, k), packed)
+    _PACKED[key] = [ref, w8._version, (n, k), packed, None]
     return True
 
 
-def _packed_for(w8):
-    """The packed copy attached to ``w8`` if it is still valid, else None."""
+def _packed_entry(w8):
+    """The registry entry of ``w8`` if its packed copy is still valid, else None."""
     if not _PACKED:
         return None
     key = _pack_key(w8)
     e = _PACKED.get(key) if key is not None else None
     if e is None:
         return None
-    ref, version, shape, packed = e
+    ref, version, shape = e[0], e[1], e[2]
     if ref() is not w8.untyped_storage() or tuple(w8.shape) != shape or w8._version != version:
         return None
-    return packed
+    return e
+
+
+def _packed_for(w8):
+    """The packed copy attached to ``w8`` if it is still valid, else None."""
+    e = _packed_entry(w8)
+    return None if e is None else e[3]
+
+
+def _packed_nn_for(w8):
+    """The second packed form of a weight with a valid packed copy (the order
+    in which linear_dx_int8's split-K product reads w8 [N, K] as its right
+    operand), made at the first call outside a graph capture; else None."""
+    e = _packed_entry(w8)
+    if e is None:
+        return None
+    if e[4] is None and not is_capturing():
+        lib = _lib()
+        n, k = e[2]
+        need = lib.xpuint8_packed_weight_nn_bytes(n, k)
+        if need < 0:
+            return None
+        nn = torch.empty(int(need), device=w8.device, dtype=torch.int8)
+        rc = lib.xpuint8_pack_weight_nn_stream(_stream(w8.device), _ptr(w8), _ptr(nn), n, k)
+        if rc != 0:
+            _err(lib, "pack_weight")
+        e[4] = nn
+    return e[4]
 
 
 def rotate(x):
@@ -416,8 +445,14 @@ def linear_dx_int8(dy, w8, w_scale):
         _err(lib, "linear_dx_int8")
     work = torch.empty((nbytes,), device=dy.device, dtype=torch.int8)
     dx = torch.empty((m, k), device=dy.device, dtype=torch.bfloat16)
-    rc = lib.xpuint8_linear_dx_int8_stream(_stream(dy.device), _ptr(d2), _ptr(ws), _ptr(w8c),
-                                           _ptr(dx), m, n, k, _ptr(work), nbytes)
+    nn = _packed_nn_for(w8c)
+    if nn is not None:
+        rc = lib.xpuint8_linear_dx_int8_packed_stream(_stream(dy.device), _ptr(d2), _ptr(ws),
+                                                      _ptr(w8c), _ptr(nn), _ptr(dx), m, n, k,
+                                                      _ptr(work), nbytes)
+    else:
+        rc = lib.xpuint8_linear_dx_int8_stream(_stream(dy.device), _ptr(d2), _ptr(ws),
+                                               _ptr(w8c), _ptr(dx), m, n, k, _ptr(work), nbytes)
     if rc != 0:
         _err(lib, "linear_dx_int8")
     return dx.reshape(*dy.shape[:-1], k)

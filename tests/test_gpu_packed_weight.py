@@ -205,3 +205,82 @@ def test_int8linear_packs_its_weight(dev):
     off = int8.Int8Linear(w8r.clone(), ws, pack=False)
     off(x)
     assert ops._packed_for(off.w8) is None
+
+
+def nn_layout(w8):
+    """w8 int8 [R, C] (C % 32 == 0) in the NN stage order of the split-K
+    GEMM: per 64-row step s, 32-column group c and 32-row half h the 1 KB
+    block ((s * C/32 + c) * 2 + h) * 1024, its 16-byte chunk l holding row l/2
+    of the half and column half (l & 1) ^ ((l >> 5) & 1) of the group; zeros
+    past R."""
+    w = w8.cpu().numpy()
+    r, c = w.shape
+    rp = (r + 63) // 64 * 64
+    wp = np.zeros((rp, c), np.int8)
+    wp[:r] = w
+    # [s, h, row in half, c group, column half, 16 bytes]
+    v = wp.reshape(rp // 64, 2, 32, c // 32, 2, 16)
+    l = np.arange(64)
+    row, half = l >> 1, (l & 1) ^ ((l >> 5) & 1)
+    blocks = v[:, :, row, :, half, :]                 # [l, s, h, cg, 16] (advanced index first)
+    return torch.from_numpy(np.ascontiguousarray(blocks.transpose(1, 3, 2, 0, 4)).reshape(-1))
+
+
+@pytest.mark.parametrize("r,c", [(5120, 1280), (2064, 1280), (48, 64)])
+def test_pack_nn_layout_exact(dev, r, c):
+    g = torch.Generator().manual_seed(r * 3 + c)
+    w8 = torch.randint(-127, 128, (r, c), generator=g, dtype=torch.int8)
+    lib = L._lib()
+    need = lib.xpuint8_packed_weight_nn_bytes(r, c)
+    assert need == (r + 63) // 64 * 64 * c
+    packed = torch.full((need,), 99, device=dev, dtype=torch.int8)
+    wd = w8.to(dev)
+    assert lib.xpuint8_pack_weight_nn_stream(L._stream(dev), L._ptr(wd), L._ptr(packed), r, c) \
+        == 0, lib.xpuint8_last_error()
+    assert torch.equal(packed.cpu(), nn_layout(w8))
+    assert lib.xpuint8_packed_weight_nn_bytes(64, 48) == -1
+
+
+# (M, N, K) of dx = dy [M, N] against w8 [N, K]: config 5, a ragged batch, a
+# contraction whose last 64-row step is partly past N (2064 = 32 * 64 + 16),
+# and a batch small enough for the K-slice kernels (the packed form unused)
+@pytest.mark.parametrize("m,n,k", [(4096, 5120, 1280), (3000, 5120, 1280), (4096, 2064, 1280),
+                                   (256, 5120, 1280)])
+def test_dx_int8_packed_equals_rowmajor(dev, m, n, k):
+    w8p, w8r, ws = _both(dev, n, k, seed=n + 31)
+    g = torch.Generator().manual_seed(m + n)
+    dy = (torch.randn(m, n, generator=g) * 1e-3).to(torch.bfloat16).to(dev)
+    dp = int8.linear_dx_int8(dy, w8p, ws)
+    dr = int8.linear_dx_int8(dy, w8r, ws)
+    assert np.array_equal(bits(dp), bits(dr)), mismatch(bits(dp), bits(dr))
+    if m >= 4096 and n == 5120:
+        assert ops._packed_entry(w8p)[4] is not None       # the NN form was made and used
+
+
+def test_dx_int8_packed_exact(dev):
+    m, n, k = 1536, 2064, 1280
+    w8p, _, ws = _both(dev, n, k, seed=41)
+    g = torch.Generator().manual_seed(42)
+    dy = (torch.randn(m, n, generator=g) * 1e-3).to(torch.bfloat16)
+    d = int8.linear_dx_int8(dy.to(dev), w8p, ws)
+    want = O.linear_dx_int8(bits(dy), npy(w8p), npy(ws))
+    assert np.array_equal(bits(d), want), mismatch(bits(d), want)
+
+
+def test_int8_linear_backward_packed(dev):
+    """The training step through autograd (int8 backward) with and without the
+    packed forms: forward output and dx bit for bit."""
+    m, n, k = 4096, 5120, 1280
+    w8p, w8r, ws = _both(dev, n, k, seed=43)
+    b = weight(1, n, seed=44, std=0.01)[0].to(dev)
+    x = activation(m, k, seed=45).to(dev)
+    dy = (torch.randn(m, n, generator=torch.Generator().manual_seed(46)) * 1e-3) \
+        .to(torch.bfloat16).to(dev)
+    grads = []
+    for w8 in (w8p, w8r):
+        xx = x.clone().requires_grad_(True)
+        y = int8.int8_linear(xx, w8, ws, b, mode="int8")
+        y.backward(dy)
+        grads.append((bits(y), bits(xx.grad)))
+    assert np.array_equal(grads[0][0], grads[1][0])
+    assert np.array_equal(grads[0][1], grads[1][1]), mismatch(grads[0][1], grads[1][1])
