@@ -660,7 +660,10 @@ def linear(x, w8, w_scale, bias=None, act: Optional[str] = None, residual=None,
     Two kernels: rotate+quantize of ``x`` (with ``act`` fused into its load),
     then the MFMA GEMM with the dequant (+bias) epilogue fused into its store;
     a product too small to fill the GPU is split in K across blocks, and a
-    third kernel adds the slices' int32 sums and applies the dequant.
+    third kernel adds the slices' int32 sums and applies the dequant.  When
+    ``w8`` carries a valid packed copy (:func:`prepare_weight`,
+    :func:`pack_weight`) the GEMMs that take the block layout read it instead,
+    with the same results.
     ``residual``/``residual_scale`` apply ``residual + residual_scale * out``;
     ``return_acc`` returns ``(int32 [M, N], fp32 [M], fp32 [N])`` instead.
     """
