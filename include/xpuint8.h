@@ -259,6 +259,33 @@ int xpuint8_linear_packed_stream(const void *stream, const void *x, const int8_t
                                  int32_t bias_bf16, void *out, int64_t M, int64_t N, int64_t K,
                                  void *work, int64_t work_bytes);
 
+/* The whole of linear(x, w8, ws, bias, residual=, residual_scale=) in one call:
+ * xpuint8_convrot_quantize_stream(x) then xpuint8_linear_gemm_residual_stream,
+ * bit for bit, with the quantized activation in `work`
+ * (xpuint8_linear_workspace_size(M, N, K) bytes) laid out for the GEMM that
+ * reads it (the MFMA block layout where the persistent or the split-K kernel
+ * takes the shape), and w8_packed (optional) read there in place of w8.
+ * Replaces quantize + torch._int_mm + dequant + addcmul at
+ * python/xpu_kernels/int8/ops.py:631-644; no counterpart as one call. */
+int xpuint8_linear_residual_packed_stream(const void *stream, const void *x, const int8_t *w8,
+                                          const int8_t *w8_packed, const float *w_scale,
+                                          const void *bias, int32_t bias_bf16,
+                                          const void *residual, const void *residual_scale,
+                                          void *out, int64_t M, int64_t N, int64_t K, void *work,
+                                          int64_t work_bytes);
+
+/* linear_acc in one call: (q, x_scale) = xpuint8_convrot_quantize_stream(x),
+ * acc[M,N] = q @ w8^T (int32, exact), bit for bit, the codes in `work`
+ * (xpuint8_linear_workspace_size(M, N, K) bytes suffice) laid out for the
+ * GEMM (the MFMA block layout where the persistent kernel takes the shape),
+ * and w8_packed (optional) read there in place of w8.  x_scale fp32 [M] is
+ * an output.  Replaces quantize + torch._int_mm at
+ * python/xpu_kernels/int8/ops.py:571-588; no counterpart as one call. */
+int xpuint8_linear_acc_packed_stream(const void *stream, const void *x, const int8_t *w8,
+                                     const int8_t *w8_packed, int32_t *acc, float *x_scale,
+                                     int64_t M, int64_t N, int64_t K, void *work,
+                                     int64_t work_bytes);
+
 /* xpuint8_linear_gemm_tiled_stream, bit for bit, with the weight given only
  * packed; the same shapes (others return an error). */
 int xpuint8_linear_gemm_packed_stream(const void *stream, const int8_t *xq, const float *x_scale,

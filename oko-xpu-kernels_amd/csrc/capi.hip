@@ -646,6 +646,62 @@ int xpuint8_linear_packed_stream(const void* stream, const void* x, const int8_t
                       w8_packed);
 }
 
+int xpuint8_linear_residual_packed_stream(const void* stream, const void* x, const int8_t* w8,
+                                          const int8_t* w8_packed, const float* w_scale,
+                                          const void* bias, int32_t bias_bf16,
+                                          const void* residual, const void* residual_scale,
+                                          void* out, int64_t M, int64_t N, int64_t K, void* work,
+                                          int64_t work_bytes) {
+    XPU_TRY(linear_check(x, w8, w_scale, bias, bias_bf16, out, M, N, K, work, work_bytes));
+    XPU_NONNULL(residual); XPU_NONNULL(residual_scale);
+    XPU_ALIGNED_OPT(w8_packed);
+    XPU_TRY(ensure_device());
+    hipStream_t st = as_stream(stream);
+    int8_t* q = static_cast<int8_t*>(work);
+    float* xs = reinterpret_cast<float*>(static_cast<char*>(work) + linear_work_q_bytes(M, K));
+    const float* b32 = bias_bf16 ? nullptr : static_cast<const float*>(bias);
+    const uint16_t* b16 = bias_bf16 ? static_cast<const uint16_t*>(bias) : nullptr;
+    // the kernels that read x in the MFMA block layout (and the packed weight)
+    if (rowquant_can_tile(int(K)) &&
+        (pp_applies(int(M), int(N), int(K), false) ||
+         (splitk_applies(int(M), int(N), int(K)) && gemm_slices(int(M), int(N), int(K)) == 0))) {
+        XPU_TRY(launched(convrot_quantize_tiled(st, x, q, xs, M, int(K)),
+                         "linear_residual (quantize)"));
+        return launched(gemm_dequant_residual_xt(st, q, w8_packed ? w8_packed : w8, K, out, N, xs,
+                                                 w_scale, b32, b16, residual, N, residual_scale,
+                                                 int(M), int(N), int(K), w8_packed != nullptr),
+                        "linear_residual (gemm)");
+    }
+    XPU_TRY(launched(convrot_quantize(st, x, q, xs, M, int(K), 0), "linear_residual (quantize)"));
+    return launched(gemm_dequant_residual(st, q, K, w8, K, out, N, xs, w_scale, b32, b16, residual,
+                                          N, residual_scale, int(M), int(N), int(K)),
+                    "linear_residual (gemm)");
+}
+
+int xpuint8_linear_acc_packed_stream(const void* stream, const void* x, const int8_t* w8,
+                                     const int8_t* w8_packed, int32_t* acc, float* x_scale,
+                                     int64_t M, int64_t N, int64_t K, void* work,
+                                     int64_t work_bytes) {
+    XPU_TRY(check_rows(M, K));
+    XPU_TRY(check_gemm(M, N, K));
+    XPU_NONNULL(x); XPU_NONNULL(w8); XPU_NONNULL(acc); XPU_NONNULL(x_scale); XPU_NONNULL(work);
+    XPU_ALIGNED_OPT(w8_packed);
+    if (work_bytes < int64_t(linear_work_q_bytes(M, K)))
+        return fail(2, "work must hold xpuint8_linear_workspace_size(M, N, K) bytes");
+    XPU_TRY(ensure_device());
+    hipStream_t st = as_stream(stream);
+    int8_t* q = static_cast<int8_t*>(work);
+    if (rowquant_can_tile(int(K)) && pp_applies(int(M), int(N), int(K), false)) {
+        XPU_TRY(launched(convrot_quantize_tiled(st, x, q, x_scale, M, int(K)),
+                         "linear_acc (quantize)"));
+        return launched(gemm_i32_pp_xt(st, q, w8_packed ? w8_packed : w8, K, acc, N, int(M),
+                                       int(N), int(K), w8_packed != nullptr),
+                        "linear_acc (gemm)");
+    }
+    XPU_TRY(launched(convrot_quantize(st, x, q, x_scale, M, int(K), 0), "linear_acc (quantize)"));
+    return launched(gemm_i32(st, q, K, w8, K, acc, N, int(M), int(N), int(K)), "linear_acc (gemm)");
+}
+
 int xpuint8_linear_gemm_packed_stream(const void* stream, const int8_t* xq, const float* x_scale,
                                       const int8_t* w8_packed, const float* w_scale,
                                       const void* bias, int32_t bias_bf16, void* out, int64_t M,

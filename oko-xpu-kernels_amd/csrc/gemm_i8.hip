@@ -2156,6 +2156,35 @@ hipError_t gemm_dequant_residual(hipStream_t st, const int8_t* A, int64_t lda, c
     return launch_gemm(st, A, lda, B, ldb, M, N, K, e);
 }
 
+hipError_t gemm_dequant_residual_xt(hipStream_t st, const int8_t* At, const int8_t* B,
+                                    int64_t ldb, void* out, int64_t ldo, const float* xs,
+                                    const float* ws, const float* bias, const uint16_t* bias16,
+                                    const void* res, int64_t ldr, const void* rscale, int M, int N,
+                                    int K, bool packed) {
+    EpiDequantRes e;
+    static_cast<EpiDequant&>(e) =
+        EpiDequant{static_cast<uint16_t*>(out), ldo, xs, ws, bias, bias16};
+    e.res = static_cast<const uint16_t*>(res);
+    e.ldr = ldr;
+    e.rscale = static_cast<const uint16_t*>(rscale);
+    if (pp_applies(M, N, K, false)) {
+        if (packed) return launch_pp<true, true>(st, At, 0, B, 0, M, N, K, e);
+        return launch_pp<true>(st, At, 0, B, ldb, M, N, K, e);
+    }
+    if (splitk_applies(M, N, K)) {
+        if (packed) return launch_splitk<false, EpiDequantRes, true, true>(st, At, 0, B, 0, M, N, K, e);
+        return launch_splitk<false, EpiDequantRes, true>(st, At, 0, B, ldb, M, N, K, e);
+    }
+    return hipErrorInvalidValue;
+}
+
+hipError_t gemm_i32_pp_xt(hipStream_t st, const int8_t* At, const int8_t* B, int64_t ldb,
+                          int32_t* C, int64_t ldc, int M, int N, int K, bool packed) {
+    const EpiI32 epi{C, ldc};
+    if (packed) return launch_pp<true, true>(st, At, 0, B, 0, M, N, K, epi);
+    return launch_pp<true>(st, At, 0, B, ldb, M, N, K, epi);
+}
+
 hipError_t gemm_act(hipStream_t st, const int8_t* A, int64_t lda, const int8_t* B, int64_t ldb,
                     void* out, int64_t ldo, const float* xs, const float* ws, int M, int N, int K,
                     int act) {

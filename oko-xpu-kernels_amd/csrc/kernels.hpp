@@ -99,6 +99,17 @@ hipError_t gemm_dequant_residual(hipStream_t st, const int8_t* A, int64_t lda, c
                                  const float* ws, const float* bias, const uint16_t* bias16,
                                  const void* res, int64_t ldr, const void* rscale, int M, int N,
                                  int K);
+// the same two GEMMs with A in the MFMA block layout (packed: B is pack_weight's
+// copy): the residual epilogue on the persistent or the split-K kernel (callers
+// check pp_applies / splitk_applies; other shapes are refused), and the int32
+// product on the persistent kernel (callers check pp_applies)
+hipError_t gemm_dequant_residual_xt(hipStream_t st, const int8_t* At, const int8_t* B,
+                                    int64_t ldb, void* out, int64_t ldo, const float* xs,
+                                    const float* ws, const float* bias, const uint16_t* bias16,
+                                    const void* res, int64_t ldr, const void* rscale, int M, int N,
+                                    int K, bool packed);
+hipError_t gemm_i32_pp_xt(hipStream_t st, const int8_t* At, const int8_t* B, int64_t ldb,
+                          int32_t* C, int64_t ldc, int M, int N, int K, bool packed);
 // out[m, n] = act(bf16(acc(n) * ws[n] * xs[m]), bf16(acc(N + n) * ws[N + n] * xs[m])) for the
 // paired activations 3 (situ) and 4 (GEGLU), whose B has 2N rows; act 5 (GELU) takes N rows
 hipError_t gemm_act(hipStream_t st, const int8_t* A, int64_t lda, const int8_t* B, int64_t ldb,

@@ -80,6 +80,9 @@ def _signatures():
         "xpuint8_pack_weight_stream": ([vp] * 3 + [i64] * 2, c_int),
         "xpuint8_linear_packed_stream": ([vp] * 6 + [i32, vp] + [i64] * 3 + [vp, i64], c_int),
         "xpuint8_linear_gemm_packed_stream": ([vp] * 6 + [i32, vp] + [i64] * 3, c_int),
+        "xpuint8_linear_residual_packed_stream": ([vp] * 6 + [i32] + [vp] * 3 + [i64] * 3
+                                                  + [vp, i64], c_int),
+        "xpuint8_linear_acc_packed_stream": ([vp] * 6 + [i64] * 3 + [vp, i64], c_int),
         "xpuint8_ffn_packed_stream": ([vp] * 9 + [i32, vp] + [i64] * 3 + [i32, vp, i64], c_int),
         "xpuint8_packed_weight_nn_bytes": ([i64] * 2, i64),
         "xpuint8_pack_weight_nn_stream": ([vp] * 3 + [i64] * 2, c_int),

@@ -641,6 +641,9 @@ def dequant_act_quantize(acc, x_scale, w_scale, activation="situ"):
 def linear_acc(x, w8, w_scale, act: Optional[str] = None):
     """The GEMM without the output dequant: ``(int32 [M, N], fp32 [M])``
     (ops.py:571-588)."""
+    if act is None and _acc_one_call(x, w8):
+        x2 = _c(x.reshape(-1, x.shape[-1]))
+        return _linear_acc_bf16(_lib(), x2, _c(w8), x2.shape[0], w8.shape[0], w8.shape[1])
     if act is None:
         xq, xs = quantize(x)
     else:
@@ -651,6 +654,50 @@ def linear_acc(x, w8, w_scale, act: Optional[str] = None):
         raise ValueError(f"K mismatch: activation {xq.shape[-1]} vs weight {w8.shape[1]}")
     acc = int_mm(xq.reshape(-1, xq.shape[-1]), w8.contiguous().t())
     return acc, xs.reshape(-1)
+
+
+def _acc_one_call(x, w8):
+    """Whether quantize + int32 GEMM can run as one library call: a bf16 CUDA
+    activation and an int8 [N, K] weight of the shape contract."""
+    return (isinstance(x, torch.Tensor) and x.is_cuda and x.dtype == torch.bfloat16
+            and x.dim() >= 1 and isinstance(w8, torch.Tensor) and w8.dtype == torch.int8
+            and w8.dim() == 2 and w8.device == x.device and x.shape[-1] == w8.shape[1]
+            and w8.shape[1] % 256 == 0 and w8.shape[0] % 16 == 0 and x.numel() > 0)
+
+
+def _linear_acc_bf16(lib, x2, w8c, m, n, k):
+    """quantize + int32 GEMM of a bf16 [m, k] through one library call
+    (xpuint8_linear_acc_packed_stream, with the weight's packed copy if it
+    has one): ``(int32 [m, n], fp32 [m])``."""
+    need = lib.xpuint8_linear_workspace_size(m, n, k)
+    if need < 0:
+        _err(lib, "linear_acc")
+    work = torch.empty(int(need), device=x2.device, dtype=torch.uint8)
+    acc = torch.empty((m, n), device=x2.device, dtype=torch.int32)
+    xs = torch.empty((m,), device=x2.device, dtype=torch.float32)
+    rc = lib.xpuint8_linear_acc_packed_stream(_stream(x2.device), _ptr(x2), _ptr(w8c),
+                                              _opt(_packed_for(w8c)), _ptr(acc), _ptr(xs), m, n,
+                                              k, _ptr(work), int(need))
+    if rc != 0:
+        _err(lib, "linear_acc")
+    return acc, xs
+
+
+def _linear_residual_bf16(lib, x2, w8c, ws, b, b16, res, rs, m, n, k):
+    """quantize + GEMM + dequant + residual update of a bf16 [m, k] through one
+    library call (xpuint8_linear_residual_packed_stream, with the weight's
+    packed copy if it has one)."""
+    need = lib.xpuint8_linear_workspace_size(m, n, k)
+    if need < 0:
+        _err(lib, "linear")
+    work = torch.empty(int(need), device=x2.device, dtype=torch.uint8)
+    out = torch.empty((m, n), device=x2.device, dtype=torch.bfloat16)
+    rc = lib.xpuint8_linear_residual_packed_stream(
+        _stream(x2.device), _ptr(x2), _ptr(w8c), _opt(_packed_for(w8c)), _ptr(ws), _opt(b), b16,
+        _ptr(res), _ptr(rs), _ptr(out), m, n, k, _ptr(work), int(need))
+    if rc != 0:
+        _err(lib, "linear")
+    return out
 
 
 def linear(x, w8, w_scale, bias=None, act: Optional[str] = None, residual=None,
@@ -692,6 +739,16 @@ def linear(x, w8, w_scale, bias=None, act: Optional[str] = None, residual=None,
         b, b16 = _bias_arg(bias, n, x.device)
         out = _linear_bf16(lib, x2, w8c, ws, b, b16, m, n, k, _packed_for(w8c))
         return _residual_tail(out, residual, residual_scale, input_dtype, x.shape, m, n)
+    if act is None and rs is not None:
+        # the residual update in the GEMM's store, quantize and GEMM in one call
+        ws = expand_scale(w_scale, n, x.device)
+        b, b16 = _bias_arg(bias, n, x.device)
+        res = _c(residual.reshape(m, n).to(torch.bfloat16))
+        out = _linear_residual_bf16(lib, x2, w8c, ws, b, b16, res, rs, m, n, k)
+        return out.reshape(*x.shape[:-1], n)
+    if act is None and return_acc:
+        acc, xs = _linear_acc_bf16(lib, x2, w8c, m, n, k)
+        return acc, xs, expand_scale(w_scale, n, acc.device)
     if act is None:
         xq, xs = quantize(x2)
     else:

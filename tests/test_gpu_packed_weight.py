@@ -284,3 +284,44 @@ def test_int8_linear_backward_packed(dev):
         grads.append((bits(y), bits(xx.grad)))
     assert np.array_equal(grads[0][0], grads[1][0])
     assert np.array_equal(grads[0][1], grads[1][1]), mismatch(grads[0][1], grads[1][1])
+
+
+# linear with the residual update and linear_acc, each one library call that
+# quantizes into the layout its GEMM reads: the persistent kernel (config 3;
+# a ragged batch), the split-K kernel, and a batch whose GEMM reads the
+# activation row-major (K slices)
+ONE_CALL_SHAPES = [(4096, 10240, 1280), (3000, 10240, 1280), (4096, 1280, 5120), (200, 1280, 4096)]
+
+
+@pytest.mark.parametrize("m,n,k", ONE_CALL_SHAPES)
+def test_linear_residual_one_call(dev, m, n, k):
+    w8p, w8r, ws = _both(dev, n, k, seed=n + 51)
+    x = activation(m, k, seed=m + 52)
+    bias = weight(1, n, seed=53, std=0.01)[0]
+    g = torch.Generator().manual_seed(m + n)
+    res = torch.randn(m, n, generator=g).to(torch.bfloat16)
+    rscale = (torch.rand(n, generator=g) * 2 - 0.5).to(torch.bfloat16)
+    args = dict(residual=res.to(dev), residual_scale=rscale.to(dev))
+    yp = int8.linear(x.to(dev), w8p, ws, bias.to(dev), **args)
+    yr = int8.linear(x.to(dev), w8r, ws, bias.to(dev), **args)
+    assert np.array_equal(bits(yp), bits(yr)), mismatch(bits(yp), bits(yr))
+    if m * n <= 4096 * 10240 and k <= 1280:
+        d = O.linear(bits(x), npy(w8p), npy(ws), O.bf16_to_f32(bits(bias)))
+        f = O.bf16_to_f32
+        want = O.f32_to_bf16(f(bits(res)) + f(d) * f(bits(rscale))[None, :])
+        assert np.array_equal(bits(yp), want), mismatch(bits(yp), want)
+
+
+@pytest.mark.parametrize("m,n,k", ONE_CALL_SHAPES)
+def test_linear_acc_one_call(dev, m, n, k):
+    w8p, w8r, ws = _both(dev, n, k, seed=n + 61)
+    x = activation(m, k, seed=m + 62)
+    accp, xsp = int8.linear_acc(x.to(dev), w8p, ws)
+    accr, xsr = int8.linear_acc(x.to(dev), w8r, ws)
+    assert torch.equal(accp, accr) and torch.equal(xsp, xsr)
+    acc2, xs2, ws2 = int8.linear(x.to(dev), w8p, ws, return_acc=True)
+    assert torch.equal(acc2, accp) and torch.equal(xs2, xsp) and torch.equal(ws2, ws)
+    q, s = O.convrot_quantize(bits(x))
+    assert np.array_equal(npy(xsp), s)
+    if k <= 1280:
+        assert np.array_equal(npy(accp), O.int_mm(q, npy(w8p)))
