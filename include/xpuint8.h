@@ -314,6 +314,21 @@ int64_t xpuint8_packed_weight_nn_bytes(int64_t N, int64_t K);
 int xpuint8_pack_weight_nn_stream(const void *stream, const int8_t *w8, int8_t *packed, int64_t N,
                                   int64_t K);
 
+/* The backward of int8_linear(mode="int8") in one call: dbias = the column
+ * sums of dy (xpuint8_column_sum_stream, bit for bit; bf16, or with
+ * dbias_fp32 = 1 the fp32 each bf16 sum widens to, which is what the bias
+ * of an fp32 parameter receives; dbias may be null) and dx =
+ * xpuint8_linear_dx_int8_stream(dy, w_scale, w8), bit for bit, reading
+ * w8_packed_nn (optional) as xpuint8_linear_dx_int8_packed_stream does.
+ * `work` holds xpuint8_linear_backward_int8_workspace_size(M, N, K) bytes.
+ * Replaces the bias-gradient sum and linear_dx_int8 of
+ * python/xpu_kernels/int8/ops.py:270-289; no counterpart as one call. */
+int64_t xpuint8_linear_backward_int8_workspace_size(int64_t M, int64_t N, int64_t K);
+int xpuint8_linear_backward_int8_stream(const void *stream, const void *dy, const float *w_scale,
+                                        const int8_t *w8, const int8_t *w8_packed_nn, void *dx,
+                                        void *dbias, int32_t dbias_fp32, int64_t M, int64_t N,
+                                        int64_t K, void *work, int64_t work_bytes);
+
 /* xpuint8_linear_dx_int8_stream, bit for bit, reading w8_packed_nn (w8 packed
  * by xpuint8_pack_weight_nn_stream; null reads w8) where the split-K GEMM
  * takes the product. */

@@ -869,6 +869,34 @@ int xpuint8_linear_dx_int8_packed_stream(const void* stream, const void* dy, con
                     w8_packed_nn);
 }
 
+int64_t xpuint8_linear_backward_int8_workspace_size(int64_t M, int64_t N, int64_t K) {
+    if (check_dx(M, N, K) != 0) return -1;
+    const size_t dx = (dx_work_layout(M, N, K).total + 255) & ~size_t(255);
+    return int64_t(dx + size_t(colsum_work_bytes(M, N)));
+}
+
+int xpuint8_linear_backward_int8_stream(const void* stream, const void* dy, const float* w_scale,
+                                        const int8_t* w8, const int8_t* w8_packed_nn, void* dx,
+                                        void* dbias, int32_t dbias_fp32, int64_t M, int64_t N,
+                                        int64_t K, void* work, int64_t work_bytes) {
+    XPU_TRY(check_dx(M, N, K));
+    XPU_NONNULL(dy); XPU_NONNULL(w_scale); XPU_NONNULL(w8); XPU_NONNULL(dx); XPU_NONNULL(work);
+    XPU_ALIGNED_OPT(w8_packed_nn);
+    XPU_ALIGNED_OPT(dbias);
+    if (dbias_fp32 != 0 && dbias_fp32 != 1) return fail(2, "dbias_fp32 must be 0 or 1");
+    const size_t dxw = (dx_work_layout(M, N, K).total + 255) & ~size_t(255);
+    if (work_bytes < int64_t(dxw + size_t(colsum_work_bytes(M, N))))
+        return fail(2, "work must hold xpuint8_linear_backward_int8_workspace_size(M, N, K) bytes");
+    XPU_TRY(ensure_device());
+    hipStream_t st = as_stream(stream);
+    char* w = static_cast<char*>(work);
+    if (dbias)
+        XPU_TRY(launched(column_sum_bf16(st, dy, dbias, M, int(N), reinterpret_cast<float*>(w + dxw),
+                                         dbias_fp32 != 0),
+                         "linear_backward_int8 (column sum)"));
+    return dx_chain(st, dy, w_scale, w8, dx, M, N, K, w, w8_packed_nn);
+}
+
 int xpuint8_linear_dx_int8_noalloc_stream(const void* stream, const void* dy,
                                           const float* w_scale, const int8_t* w8, void* dx,
                                           int64_t M, int64_t N, int64_t K) {

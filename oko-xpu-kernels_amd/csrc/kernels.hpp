@@ -43,10 +43,11 @@ hipError_t convrot_quantize_tiled(hipStream_t st, const void* x, int8_t* q, floa
                                   int64_t M, int K);
 
 // bf16 column sums out[n] = bf16(sum_m x[m, n]) (N % 8 == 0) through fp32
-// partials in part (colsum_work_bytes(M, N) bytes)
+// partials in part (colsum_work_bytes(M, N) bytes); out_f32 writes each
+// bf16-rounded sum as the fp32 it widens to
 int64_t colsum_work_bytes(int64_t M, int64_t N);
 hipError_t column_sum_bf16(hipStream_t st, const void* x, void* out, int64_t M, int N,
-                           float* part);
+                           float* part, bool out_f32 = false);
 
 // gemm_i8.hip
 hipError_t gemm_i32(hipStream_t st, const int8_t* A, int64_t lda, const int8_t* B, int64_t ldb,

@@ -805,9 +805,11 @@ __global__ __launch_bounds__(256) void colsum_part_kernel(const uint16_t* __rest
 // The chunk sums of 64 columns per block of 8 waves: wave w adds chunks w,
 // w + 8, w + 16, ... in that order (all its loads issued first), then the
 // eight wave sums are added in wave order.
+// out_f32: the bf16-rounded sum written as the fp32 it widens to (exact), for a
+// gradient whose parameter is fp32
 __global__ __launch_bounds__(512) void colsum_final_kernel(const float* __restrict__ part,
-                                                           uint16_t* __restrict__ out, int chunks,
-                                                           int N) {
+                                                           void* __restrict__ out, int chunks,
+                                                           int N, int out_f32) {
     __shared__ float t[8][64];
     const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
     const int n = blockIdx.x * 64 + l;
@@ -830,7 +832,9 @@ __global__ __launch_bounds__(512) void colsum_final_kernel(const float* __restri
         float s = t[0][l];
 #pragma unroll
         for (int i = 1; i < 8; ++i) s += t[i][l];
-        out[n] = uint16_t(f32_to_bf16_bits(s));
+        const uint32_t b = f32_to_bf16_bits(s);
+        if (out_f32) static_cast<uint32_t*>(out)[n] = b << 16;
+        else static_cast<uint16_t*>(out)[n] = uint16_t(b);
     }
 }
 
@@ -904,14 +908,14 @@ int64_t colsum_work_bytes(int64_t M, int64_t N) {
 }
 
 hipError_t column_sum_bf16(hipStream_t st, const void* x, void* out, int64_t M, int N,
-                           float* part) {
+                           float* part, bool out_f32) {
     const int chunks = int((M + kColChunk - 1) / kColChunk);
     hipLaunchKernelGGL(colsum_part_kernel, dim3(unsigned((N + kColCols - 1) / kColCols),
                                                 unsigned(min(chunks, 65535))),
                        dim3(256), 0, st, static_cast<const uint16_t*>(x), part, M, N, chunks);
     if (const hipError_t e = hipGetLastError(); e != hipSuccess) return e;
     hipLaunchKernelGGL(colsum_final_kernel, dim3(unsigned((N + 63) / 64)), dim3(512), 0, st, part,
-                       static_cast<uint16_t*>(out), chunks, N);
+                       out, chunks, N, out_f32 ? 1 : 0);
     return hipGetLastError();
 }
 

@@ -354,6 +354,45 @@ def column_sum(dy):
     return dy.sum(dim=0)
 
 
+def _backward_one_call(dy, w8):
+    """Whether the int8-mode backward can run as one library call: a 2-D bf16
+    CUDA ``dy`` [M, N] against an int8 [N, K] weight of the shape contract
+    (the cases where column_sum and linear_dx_int8 both take the kernels)."""
+    return (isinstance(dy, torch.Tensor) and dy.is_cuda and dy.dtype == torch.bfloat16
+            and dy.dim() == 2 and dy.shape[0] > 0 and w8.dtype == torch.int8
+            and w8.dim() == 2 and w8.device == dy.device and dy.shape[1] == w8.shape[0]
+            and w8.shape[0] % 16 == 0 and w8.shape[1] % 256 == 0)
+
+
+def _linear_backward_int8(dy, w8, w_scale, want_dbias, bias_dtype):
+    """dx = linear_dx_int8(dy, w8, w_scale) and, if wanted, the bias gradient
+    column_sum(dy) in one library call (xpuint8_linear_backward_int8_stream),
+    bit for bit.  The bias gradient comes out in the bias's dtype when that is
+    fp32 (each bf16 sum widened, exactly what autograd's cast would give) or
+    bf16; otherwise bf16, which autograd casts as before."""
+    lib = _lib()
+    m, n = int(dy.shape[0]), int(dy.shape[1])
+    k = int(w8.shape[1])
+    d2 = _c(dy)
+    ws = expand_scale(w_scale, n, dy.device)
+    w8c = _c(w8)
+    nbytes = lib.xpuint8_linear_backward_int8_workspace_size(m, n, k)
+    if nbytes < 0:
+        _err(lib, "linear_dx_int8")
+    work = torch.empty((nbytes,), device=dy.device, dtype=torch.int8)
+    dx = torch.empty((m, k), device=dy.device, dtype=torch.bfloat16)
+    dbias, f32 = None, 0
+    if want_dbias:
+        f32 = 1 if bias_dtype == torch.float32 else 0
+        dbias = torch.empty((n,), device=dy.device, dtype=torch.float32 if f32 else torch.bfloat16)
+    rc = lib.xpuint8_linear_backward_int8_stream(
+        _stream(dy.device), _ptr(d2), _ptr(ws), _ptr(w8c), _opt(_packed_nn_for(w8c)), _ptr(dx),
+        _opt(dbias), f32, m, n, k, _ptr(work), nbytes)
+    if rc != 0:
+        _err(lib, "linear_dx_int8")
+    return dx, dbias
+
+
 class _Int8LinearFn(torch.autograd.Function):
     """The INT8 linear as an autograd op (ops.py:241-289): forward is
     :func:`linear`; backward is dbias plus dx through :func:`linear_dx_int8`
@@ -365,11 +404,16 @@ class _Int8LinearFn(torch.autograd.Function):
         ctx.save_for_backward(w8, w_scale)
         ctx.mode = mode
         ctx.input_dtype = x.dtype
+        ctx.bias_dtype = None if bias is None else bias.dtype
         return linear(x, w8, w_scale, bias)
 
     @staticmethod
     def backward(ctx, dy):
         w8, w_scale = ctx.saved_tensors
+        if ctx.mode == "int8" and _backward_one_call(dy, w8):
+            dx, dbias = _linear_backward_int8(dy, w8, w_scale, ctx.needs_input_grad[3],
+                                              ctx.bias_dtype)
+            return dx.to(ctx.input_dtype), None, None, dbias, None
         dbias = column_sum(dy) if ctx.needs_input_grad[3] else None
         dy = dy.to(torch.bfloat16)
         if ctx.mode == "int8":

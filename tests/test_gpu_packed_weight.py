@@ -325,3 +325,32 @@ def test_linear_acc_one_call(dev, m, n, k):
     assert np.array_equal(npy(xsp), s)
     if k <= 1280:
         assert np.array_equal(npy(accp), O.int_mm(q, npy(w8p)))
+
+
+@pytest.mark.parametrize("bias_dtype", [torch.float32, torch.bfloat16, torch.float16, None])
+@pytest.mark.parametrize("packed", [True, False])
+def test_int8_backward_one_call(dev, bias_dtype, packed):
+    """The int8-mode backward (dx and the bias gradient in one library call)
+    against linear_dx_int8 and column_sum called separately, bit for bit; the
+    bias gradient in the bias's dtype, as autograd's cast of the bf16 sum
+    gives it."""
+    m, n, k = 4096, 5120, 1280
+    w8p, w8r, ws = _both(dev, n, k, seed=71)
+    w8 = w8p if packed else w8r
+    x = activation(m, k, seed=72).to(dev).requires_grad_(True)
+    dy = (torch.randn(m, n, generator=torch.Generator().manual_seed(73)) * 1e-3) \
+        .to(torch.bfloat16).to(dev)
+    bias = None
+    if bias_dtype is not None:
+        bias = (weight(1, n, seed=74, std=0.01)[0]).to(dev, bias_dtype).requires_grad_(True)
+    y = int8.int8_linear(x, w8, ws, bias, mode="int8")
+    y.backward(dy)
+    dx_ref = int8.linear_dx_int8(dy, w8r, ws)
+    assert np.array_equal(bits(x.grad), bits(dx_ref)), mismatch(bits(x.grad), bits(dx_ref))
+    if bias is not None:
+        db_ref = ops.column_sum(dy).to(bias_dtype)
+        assert bias.grad.dtype == bias_dtype
+        assert torch.equal(bias.grad.view(torch.int32 if bias_dtype == torch.float32 else
+                                          torch.int16),
+                           db_ref.view(torch.int32 if bias_dtype == torch.float32 else
+                                       torch.int16))
