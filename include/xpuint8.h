@@ -329,6 +329,21 @@ int xpuint8_linear_backward_int8_stream(const void *stream, const void *dy, cons
                                         void *dbias, int32_t dbias_fp32, int64_t M, int64_t N,
                                         int64_t K, void *work, int64_t work_bytes);
 
+/* The backward of int8_linear(mode="dense") in one call: dbias as in
+ * xpuint8_linear_backward_int8_stream, and dx = dy @ dequant_weight(w8,
+ * w_scale) (xpuint8_dequant_weight_stream then xpuint8_linear_dx_stream, bit
+ * for bit), the dequantized weight in `work`
+ * (xpuint8_linear_backward_dense_workspace_size(M, N, K) bytes: 2*N*K for it,
+ * the column sums' partials, and a small batch's split contraction).  K % 256
+ * == 0, N % 16 == 0.  Replaces the bias-gradient sum, dequant_weight and
+ * linear_dx of python/xpu_kernels/int8/ops.py:270-289; no counterpart as one
+ * call. */
+int64_t xpuint8_linear_backward_dense_workspace_size(int64_t M, int64_t N, int64_t K);
+int xpuint8_linear_backward_dense_stream(const void *stream, const void *dy, const int8_t *w8,
+                                         const float *w_scale, void *dx, void *dbias,
+                                         int32_t dbias_fp32, int64_t M, int64_t N, int64_t K,
+                                         void *work, int64_t work_bytes);
+
 /* xpuint8_linear_dx_int8_stream, bit for bit, reading w8_packed_nn (w8 packed
  * by xpuint8_pack_weight_nn_stream; null reads w8) where the split-K GEMM
  * takes the product. */

@@ -954,6 +954,58 @@ int xpuint8_linear_dx_stream(const void* stream, const void* dy, const void* w, 
                     "linear_dx");
 }
 
+// The workspace of xpuint8_linear_backward_dense_stream: the dequantized
+// weight bf16 [N, K], the column sums' partials, and (for a contraction split
+// across blocks) the bf16 GEMM's fp32 partials, each on a 256-byte boundary.
+struct DenseBwdWork {
+    size_t wd, colsum, part, total;
+};
+static DenseBwdWork dense_bwd_layout(int64_t M, int64_t N, int64_t K) {
+    auto up = [](int64_t b) { return (size_t(b) + 255) & ~size_t(255); };
+    DenseBwdWork w;
+    w.wd = 0;
+    w.colsum = up(2 * N * K);
+    w.part = w.colsum + up(colsum_work_bytes(M, N));
+    const int nsl = bf16_nn_slices(int(M), int(N), int(K));
+    w.total = w.part + (nsl > 0 ? size_t(nsl) * size_t(M) * size_t(K) * 4 : 0);
+    return w;
+}
+
+int64_t xpuint8_linear_backward_dense_workspace_size(int64_t M, int64_t N, int64_t K) {
+    if (check_rows(N, K) != 0 || check_linear_dx(M, N, K) != 0) return -1;
+    return int64_t(dense_bwd_layout(M, N, K).total);
+}
+
+int xpuint8_linear_backward_dense_stream(const void* stream, const void* dy, const int8_t* w8,
+                                         const float* w_scale, void* dx, void* dbias,
+                                         int32_t dbias_fp32, int64_t M, int64_t N, int64_t K,
+                                         void* work, int64_t work_bytes) {
+    XPU_TRY(check_rows(N, K));                  // the weight's rotation: K % 256
+    XPU_TRY(check_linear_dx(M, N, K));
+    XPU_NONNULL(dy); XPU_NONNULL(w8); XPU_NONNULL(w_scale); XPU_NONNULL(dx); XPU_NONNULL(work);
+    XPU_ALIGNED_OPT(dbias);
+    if (dbias_fp32 != 0 && dbias_fp32 != 1) return fail(2, "dbias_fp32 must be 0 or 1");
+    const DenseBwdWork L = dense_bwd_layout(M, N, K);
+    if (work_bytes < int64_t(L.total))
+        return fail(2, "work must hold xpuint8_linear_backward_dense_workspace_size(M, N, K) bytes");
+    XPU_TRY(ensure_device());
+    hipStream_t st = as_stream(stream);
+    char* w = static_cast<char*>(work);
+    if (dbias)
+        XPU_TRY(launched(column_sum_bf16(st, dy, dbias, M, int(N),
+                                         reinterpret_cast<float*>(w + L.colsum), dbias_fp32 != 0),
+                         "linear_backward_dense (column sum)"));
+    void* wd = w + L.wd;
+    XPU_TRY(launched(dequant_weight(st, w8, w_scale, wd, N, int(K)),
+                     "linear_backward_dense (dequant_weight)"));
+    if (const int nsl = bf16_nn_slices(int(M), int(N), int(K)))
+        return launched(gemm_bf16_nn_slices(st, dy, N, wd, K, dx, K, int(M), int(N), int(K),
+                                            reinterpret_cast<float*>(w + L.part), nsl),
+                        "linear_backward_dense (gemm)");
+    return launched(gemm_bf16_nn(st, dy, N, wd, K, dx, K, int(M), int(N), int(K)),
+                    "linear_backward_dense (gemm)");
+}
+
 // ------------------------------------------------------------- rms + rope
 int xpuint8_rms_rope_dequant_stream(const void* stream, const int32_t* acc, int64_t acc_stride_b,
                                     int64_t acc_stride_s, int64_t acc_stride_h,

@@ -89,6 +89,8 @@ def _signatures():
         "xpuint8_linear_dx_int8_packed_stream": ([vp] * 6 + [i64] * 3 + [vp, i64], c_int),
         "xpuint8_linear_backward_int8_workspace_size": ([i64] * 3, i64),
         "xpuint8_linear_backward_int8_stream": ([vp] * 7 + [i32] + [i64] * 3 + [vp, i64], c_int),
+        "xpuint8_linear_backward_dense_workspace_size": ([i64] * 3, i64),
+        "xpuint8_linear_backward_dense_stream": ([vp] * 6 + [i32] + [i64] * 3 + [vp, i64], c_int),
         "xpuint8_dx_gemm_stream": ([vp] * 5 + [i64] * 3 + [vp], c_int),
         "xpuint8_linear_dx_int8_stream": ([vp] * 5 + [i64] * 3 + [vp, i64], c_int),
         "xpuint8_column_sum_stream": ([vp] * 3 + [i64] * 2 + [vp, i64], c_int),

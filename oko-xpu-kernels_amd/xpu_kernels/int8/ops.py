@@ -364,32 +364,43 @@ def _backward_one_call(dy, w8):
             and w8.shape[0] % 16 == 0 and w8.shape[1] % 256 == 0)
 
 
-def _linear_backward_int8(dy, w8, w_scale, want_dbias, bias_dtype):
-    """dx = linear_dx_int8(dy, w8, w_scale) and, if wanted, the bias gradient
-    column_sum(dy) in one library call (xpuint8_linear_backward_int8_stream),
-    bit for bit.  The bias gradient comes out in the bias's dtype when that is
-    fp32 (each bf16 sum widened, exactly what autograd's cast would give) or
-    bf16; otherwise bf16, which autograd casts as before."""
+def _linear_backward(dy, w8, w_scale, want_dbias, bias_dtype, mode):
+    """The backward of _Int8LinearFn in one library call, bit for bit: dx =
+    linear_dx_int8(dy, w8, w_scale) (mode "int8",
+    xpuint8_linear_backward_int8_stream) or linear_dx(dy, dequant_weight(w8,
+    w_scale)) (mode "dense", xpuint8_linear_backward_dense_stream), and, if
+    wanted, the bias gradient column_sum(dy).  The bias gradient comes out in
+    the bias's dtype when that is fp32 (each bf16 sum widened, exactly what
+    autograd's cast would give) or bf16; otherwise bf16, which autograd casts
+    as before."""
     lib = _lib()
     m, n = int(dy.shape[0]), int(dy.shape[1])
     k = int(w8.shape[1])
     d2 = _c(dy)
     ws = expand_scale(w_scale, n, dy.device)
     w8c = _c(w8)
-    nbytes = lib.xpuint8_linear_backward_int8_workspace_size(m, n, k)
+    size = (lib.xpuint8_linear_backward_int8_workspace_size if mode == "int8"
+            else lib.xpuint8_linear_backward_dense_workspace_size)
+    what = "linear_dx_int8" if mode == "int8" else "linear_dx"
+    nbytes = size(m, n, k)
     if nbytes < 0:
-        _err(lib, "linear_dx_int8")
+        _err(lib, what)
     work = torch.empty((nbytes,), device=dy.device, dtype=torch.int8)
     dx = torch.empty((m, k), device=dy.device, dtype=torch.bfloat16)
     dbias, f32 = None, 0
     if want_dbias:
         f32 = 1 if bias_dtype == torch.float32 else 0
         dbias = torch.empty((n,), device=dy.device, dtype=torch.float32 if f32 else torch.bfloat16)
-    rc = lib.xpuint8_linear_backward_int8_stream(
-        _stream(dy.device), _ptr(d2), _ptr(ws), _ptr(w8c), _opt(_packed_nn_for(w8c)), _ptr(dx),
-        _opt(dbias), f32, m, n, k, _ptr(work), nbytes)
+    if mode == "int8":
+        rc = lib.xpuint8_linear_backward_int8_stream(
+            _stream(dy.device), _ptr(d2), _ptr(ws), _ptr(w8c), _opt(_packed_nn_for(w8c)),
+            _ptr(dx), _opt(dbias), f32, m, n, k, _ptr(work), nbytes)
+    else:
+        rc = lib.xpuint8_linear_backward_dense_stream(
+            _stream(dy.device), _ptr(d2), _ptr(w8c), _ptr(ws), _ptr(dx), _opt(dbias), f32, m, n,
+            k, _ptr(work), nbytes)
     if rc != 0:
-        _err(lib, "linear_dx_int8")
+        _err(lib, what)
     return dx, dbias
 
 
@@ -410,9 +421,10 @@ class _Int8LinearFn(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dy):
         w8, w_scale = ctx.saved_tensors
-        if ctx.mode == "int8" and _backward_one_call(dy, w8):
-            dx, dbias = _linear_backward_int8(dy, w8, w_scale, ctx.needs_input_grad[3],
-                                              ctx.bias_dtype)
+        if ctx.mode in ("int8", "dense") and _backward_one_call(dy, w8) and \
+                w_scale.numel() in (1, w8.shape[0]):
+            dx, dbias = _linear_backward(dy, w8, w_scale, ctx.needs_input_grad[3],
+                                         ctx.bias_dtype, ctx.mode)
             return dx.to(ctx.input_dtype), None, None, dbias, None
         dbias = column_sum(dy) if ctx.needs_input_grad[3] else None
         dy = dy.to(torch.bfloat16)

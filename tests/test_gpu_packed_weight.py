@@ -329,12 +329,14 @@ def test_linear_acc_one_call(dev, m, n, k):
 
 @pytest.mark.parametrize("bias_dtype", [torch.float32, torch.bfloat16, torch.float16, None])
 @pytest.mark.parametrize("packed", [True, False])
-def test_int8_backward_one_call(dev, bias_dtype, packed):
-    """The int8-mode backward (dx and the bias gradient in one library call)
-    against linear_dx_int8 and column_sum called separately, bit for bit; the
-    bias gradient in the bias's dtype, as autograd's cast of the bf16 sum
-    gives it."""
-    m, n, k = 4096, 5120, 1280
+@pytest.mark.parametrize("mode,m", [("int8", 4096), ("dense", 4096), ("dense", 100)])
+def test_backward_one_call(dev, bias_dtype, packed, mode, m):
+    """The backward of int8_linear (dx and the bias gradient in one library
+    call) against linear_dx_int8 -- or linear_dx of dequant_weight -- and
+    column_sum called separately, bit for bit; the bias gradient in the
+    bias's dtype, as autograd's cast of the bf16 sum gives it.  M = 100 splits
+    the dense product's contraction across blocks."""
+    n, k = 5120, 1280
     w8p, w8r, ws = _both(dev, n, k, seed=71)
     w8 = w8p if packed else w8r
     x = activation(m, k, seed=72).to(dev).requires_grad_(True)
@@ -343,9 +345,12 @@ def test_int8_backward_one_call(dev, bias_dtype, packed):
     bias = None
     if bias_dtype is not None:
         bias = (weight(1, n, seed=74, std=0.01)[0]).to(dev, bias_dtype).requires_grad_(True)
-    y = int8.int8_linear(x, w8, ws, bias, mode="int8")
+    y = int8.int8_linear(x, w8, ws, bias, mode=mode)
     y.backward(dy)
-    dx_ref = int8.linear_dx_int8(dy, w8r, ws)
+    if mode == "int8":
+        dx_ref = int8.linear_dx_int8(dy, w8r, ws)
+    else:
+        dx_ref = int8.linear_dx(dy, int8.dequant_weight(w8r, ws))
     assert np.array_equal(bits(x.grad), bits(dx_ref)), mismatch(bits(x.grad), bits(dx_ref))
     if bias is not None:
         db_ref = ops.column_sum(dy).to(bias_dtype)
