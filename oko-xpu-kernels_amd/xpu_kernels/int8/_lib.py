@@ -188,15 +188,17 @@ _RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 
 
 def _stream(device):
-    """The HIP stream behind torch's current stream on ``device``."""
+    """The HIP stream behind torch's current stream on ``device``, as the
+    integer handle (ctypes passes it as the ``c_void_p`` argument)."""
     if _RAW_STREAM is not None:
         index = device.index if device.index is not None else torch.cuda.current_device()
-        return ctypes.c_void_p(_RAW_STREAM(index))
-    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+        return _RAW_STREAM(index)
+    return torch.cuda.current_stream(device).cuda_stream
 
 
 def _ptr(t):
-    return ctypes.c_void_p(t.data_ptr())
+    """A tensor's device address as an integer (a ``c_void_p`` argument)."""
+    return t.data_ptr()
 
 
 def _fp32(t):

@@ -17,7 +17,6 @@ bf16 GPU tensor (an fp32 training model) or a dimension is not a multiple of
 
 from __future__ import annotations
 
-import ctypes
 from typing import Optional
 
 import torch
@@ -35,7 +34,7 @@ from ._lib import (
     load,
 )
 
-_NULL = ctypes.c_void_p(0)
+_NULL = None                 # a null c_void_p argument
 
 
 def _opt(t):
