@@ -403,12 +403,15 @@ def measure_side_rows(torch, int8, lib, L, st, dev, K, W, SET, extra, hbm_line, 
         log(f"[bench] int8_linear step ({mode} backward): {ms_st:.4f} ms")
 
 
-def measure_small_batch(torch, int8, lib, L, st, dev, K, W, SET, extra, dev_act, dev_weight):
+def measure_small_batch(torch, int8, lib, L, st, dev, K, W, SET, extra, dev_act, dev_weight,
+                        ops):
     """Small batches (batched decode) at config 4's widths, weights cold
     (rotating sets of > 640 MB): the whole FFN (x [M,1280] -> GEGLU [M,5120]
-    -> [M,1280], bf16 bias) as one ``xpuint8_ffn_stream`` call and the linear
-    of its down-projection shape (K=5120, N=1280) as one
-    ``xpuint8_linear_stream`` call, both on preallocated buffers, and the
+    -> [M,1280], bf16 bias) as one ``xpuint8_ffn_packed_stream`` call and the
+    linear of its down-projection shape (K=5120, N=1280) as one
+    ``xpuint8_linear_packed_stream`` call (the weights' packed copies, as
+    ``prepare_weight`` makes them), both on preallocated buffers, the FFN
+    reading the row-major weights (``xpuint8_ffn_stream``), and the
     ``int8.ffn`` API call (host work included) beside them, at M = 1, 64, 128,
     200.
     At these sizes the weights are most of the traffic (19.66 MB per FFN,
@@ -417,6 +420,8 @@ def measure_small_batch(torch, int8, lib, L, st, dev, K, W, SET, extra, dev_act,
     nf = n_sets(3 * f * k)
     ffw = [int8.prepare_weight(dev_weight(2 * f, k, 2000 + i)) + int8.prepare_weight(
         dev_weight(k, f, 2100 + i)) for i in range(nf)]
+    ffp = [(ops._packed_for(up8), ops._packed_for(dn8)) for up8, _, dn8, _ in ffw]
+    assert all(a is not None and b is not None for a, b in ffp)
     bias = dev_weight(1, k, 2200, 0.01)[0]
     res = {}
     for m in (1, 64, 128, 200):
@@ -427,12 +432,27 @@ def measure_small_batch(torch, int8, lib, L, st, dev, K, W, SET, extra, dev_act,
 
         def ffn(i):
             up8, ups, dn8, dns = ffw[i % nf]
+            up_p, dn_p = ffp[i % nf]
+            rc = lib.xpuint8_ffn_packed_stream(st, L._ptr(x), L._ptr(up8), L._ptr(up_p),
+                                               L._ptr(ups), L._ptr(dn8), L._ptr(dn_p),
+                                               L._ptr(dns), L._ptr(bias), 1, L._ptr(y), m, f, k,
+                                               4, L._ptr(work), need)
+            if rc != 0:
+                raise RuntimeError(lib.xpuint8_last_error().decode())
+
+        def ffn_rowmajor(i):
+            up8, ups, dn8, dns = ffw[i % nf]
             rc = lib.xpuint8_ffn_stream(st, L._ptr(x), L._ptr(up8), L._ptr(ups), L._ptr(dn8),
                                         L._ptr(dns), L._ptr(bias), 1, L._ptr(y), m, f, k, 4,
                                         L._ptr(work), need)
             if rc != 0:
                 raise RuntimeError(lib.xpuint8_last_error().decode())
+        ffn(0)
+        y_p = y.clone()
+        ffn_rowmajor(0)
+        assert torch.equal(y_p, y), f"small-batch FFN M={m}: packed and row-major differ"
         ms_ffn = timed(torch, ffn, K, W, SET)
+        ms_ffn_rm = timed(torch, ffn_rowmajor, K, W, SET)
         ms_api = timed(torch, lambda i: int8.ffn(x, *ffw[i % nf], bias, act="geglu_erf"),
                        K, W, SET)
         xd = dev_act(m, f, 2400 + m)
@@ -442,14 +462,16 @@ def measure_small_batch(torch, int8, lib, L, st, dev, K, W, SET, extra, dev_act,
 
         def down(i):
             dn8, dns = ffw[i % nf][2:]
-            rc = lib.xpuint8_linear_stream(st, L._ptr(xd), L._ptr(dn8), L._ptr(dns),
-                                           L._ptr(bias), 1, L._ptr(yd), m, k, f,
-                                           L._ptr(workl), needl)
+            rc = lib.xpuint8_linear_packed_stream(st, L._ptr(xd), L._ptr(dn8),
+                                                  L._ptr(ffp[i % nf][1]), L._ptr(dns),
+                                                  L._ptr(bias), 1, L._ptr(yd), m, k, f,
+                                                  L._ptr(workl), needl)
             if rc != 0:
                 raise RuntimeError(lib.xpuint8_last_error().decode())
         ms_lin = timed(torch, down, K, W, SET)
         res[f"M{m}"] = {"ffn_ms_cold": round(ms_ffn, 5),
                         "ffn_weights_GB/s": round(3 * f * k / (ms_ffn * 1e-3) / 1e9, 1),
+                        "ffn_rowmajor_weights_ms_cold": round(ms_ffn_rm, 5),
                         "ffn_api_ms_cold": round(ms_api, 5),
                         "linear_k5120_n1280_ms_cold": round(ms_lin, 5),
                         "linear_weights_GB/s": round(f * k / (ms_lin * 1e-3) / 1e9, 1)}
@@ -544,7 +566,8 @@ def main():
     w8, ws = int8.prepare_weight(weight(torch, N, Kd).to(dev))
     bias = weight(torch, 1, N, seed=2, std=0.01)[0].to(dev)
     if args.only_small:
-        measure_small_batch(torch, int8, lib, L, st, dev, K, W, SET, extra, dev_act, dev_weight)
+        measure_small_batch(torch, int8, lib, L, st, dev, K, W, SET, extra, dev_act, dev_weight,
+                            ops)
         print(json.dumps({"only_small": True, "steps": K, "warmup": W, "extra": extra}),
               flush=True)
         return
@@ -773,13 +796,34 @@ def main():
         sk += [int8.prepare_weight(dev_weight(4096, 4096, 700 + i)) for i in range(1, nsk)]
         q16, s16 = int8.quantize(xs16)
         o16 = [torch.empty((16, 4096), device=dev, dtype=torch.bfloat16) for _ in range(nsk)]
+        # what linear runs on a prepared (packed) weight: q in the MFMA block
+        # layout, the weight's packed copy
+        q16t = torch.empty(4096 * 16, device=dev, dtype=torch.int8)
+        s16t = torch.empty(16, device=dev, dtype=torch.float32)
+        assert lib.xpuint8_convrot_quantize_tiled_stream(st, L._ptr(xs16), L._ptr(q16t),
+                                                         L._ptr(s16t), 16, 4096) == 0
+        assert torch.equal(s16t, s16)
+        sk_p = [ops._packed_for(w_i) for w_i, _ in sk]
+        assert all(p is not None for p in sk_p)
 
         def skinny(i):
+            j = i % nsk
+            lib.xpuint8_linear_gemm_packed_stream(st, L._ptr(q16t), L._ptr(s16t), L._ptr(sk_p[j]),
+                                                  L._ptr(sk[j][1]), None, 0, L._ptr(o16[j]), 16,
+                                                  4096, 4096)
+
+        def skinny_rowmajor(i):
             w_i, s_i = sk[i % nsk]
             lib.xpuint8_linear_gemm_stream(st, L._ptr(q16), L._ptr(s16), L._ptr(w_i), L._ptr(s_i),
                                            None, 0, L._ptr(o16[i % nsk]), 16, 4096, 4096)
+        skinny(0)
+        o_p = o16[0].clone()
+        skinny_rowmajor(0)
+        assert torch.equal(o_p, o16[0]), "skinny: packed and row-major differ"
         ms_sk = timed(torch, skinny, K, W, SET)
         ms_sk_warm = timed(torch, lambda i: skinny(0), K, W, SET)
+        ms_sk_rm = timed(torch, skinny_rowmajor, K, W, SET)
+        ms_sk_rm_warm = timed(torch, lambda i: skinny_rowmajor(0), K, W, SET)
         ms_sk_api = timed(torch, lambda i: int8.linear(xs16, *sk[0]), K, W, SET)
         # the same API call captured once in a HIP graph and replayed: what a
         # serving loop pays per call without the Python host cost
@@ -795,8 +839,10 @@ def main():
         ms_sk_graph = timed(torch, lambda i: graph.replay(), K, W, SET)
         extra["config5_skinny_m16"] = hbm_line(bytes_sk, ms_sk, ms_sk_warm, sets=nsk,
                                                api_ms=round(ms_sk_api, 5),
-                                               api_graph_replay_ms=round(ms_sk_graph, 5))
-        del sk, graph
+                                               api_graph_replay_ms=round(ms_sk_graph, 5),
+                                               rowmajor_ms_cold=round(ms_sk_rm, 5),
+                                               rowmajor_ms_warm=round(ms_sk_rm_warm, 5))
+        del sk, sk_p, graph
         log(f"[bench] config 5: dx {ms_dx_c:.4f} / {ms_dx:.4f} ms, dW {ms_dw_c:.4f} / {ms_dw:.4f} ms, "
             f"dense dx {ms_dxd_c:.4f} / {ms_dxd:.4f} ms (cold / warm), "
             f"quantize_row {ms_rq:.4f} / {ms_rq_warm:.4f} ms, skinny {ms_sk:.4f} / "
@@ -834,7 +880,8 @@ def main():
             return
         measure_side_rows(torch, int8, lib, L, st, dev, K, W, SET, extra, hbm_line, dev_gen,
                           dev_act, dev_weight, x, w8, ws, bias)
-        measure_small_batch(torch, int8, lib, L, st, dev, K, W, SET, extra, dev_act, dev_weight)
+        measure_small_batch(torch, int8, lib, L, st, dev, K, W, SET, extra, dev_act, dev_weight,
+                            ops)
 
     line = {
         "metric": "int8_linear TOPS (M=4096,K=1280,N=10240); rotate+quant HBM GB/s",

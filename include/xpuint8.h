@@ -287,7 +287,8 @@ int xpuint8_linear_acc_packed_stream(const void *stream, const void *x, const in
                                      int64_t work_bytes);
 
 /* xpuint8_linear_gemm_tiled_stream, bit for bit, with the weight given only
- * packed; the same shapes (others return an error). */
+ * packed; its shapes and those of the skinny kernel (M <= 64 with no split
+ * in K: N >= 2048, or M <= 32) -- others return an error. */
 int xpuint8_linear_gemm_packed_stream(const void *stream, const int8_t *xq, const float *x_scale,
                                       const int8_t *w8_packed, const float *w_scale,
                                       const void *bias, int32_t bias_bf16, void *out, int64_t M,

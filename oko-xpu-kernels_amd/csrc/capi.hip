@@ -244,7 +244,7 @@ size_t linear_work_bytes(int64_t M, int64_t N, int64_t K) {
 
 // quantize + GEMM + dequant of xpuint8_linear_stream on checked arguments.
 // wp (optional): pack_weight's copy of w8, read instead of w8 by the kernels
-// that take the block layout (the split-K and persistent ones).
+// that take the block layout (the split-K, persistent and skinny ones).
 int linear_run(hipStream_t st, const void* x, const int8_t* w8, const float* w_scale,
                const void* bias, int32_t bias_bf16, void* out, int64_t M, int64_t N, int64_t K,
                void* work, const int8_t* wp = nullptr) {
@@ -280,9 +280,16 @@ int linear_run(hipStream_t st, const void* x, const int8_t* w8, const float* w_s
                                            int(N), int(K), wp != nullptr),
                         "linear (gemm)");
     }
+    // and the skinny one, given the packed weight
+    if (wp && skinny_applies(int(M), false) && rowquant_can_tile(int(K))) {
+        XPU_TRY(launched(convrot_quantize_tiled(st, x, q, xs, M, int(K)), "linear (quantize)"));
+        return launched(gemm_dequant_skinny_xt(st, q, wp, out, N, xs, w_scale, b32, b16, int(M),
+                                               int(N), int(K)),
+                        "linear (gemm)");
+    }
     XPU_TRY(launched(convrot_quantize(st, x, q, xs, M, int(K), 0), "linear (quantize)"));
     return launched(gemm_dequant(st, q, K, w8, K, out, N, xs, w_scale, b32, b16, int(M), int(N),
-                                 int(K)),
+                                 int(K), wp),
                     "linear (gemm)");
 }
 
@@ -328,10 +335,17 @@ int ffn_run(hipStream_t st, const void* x, const int8_t* up_w8, const int8_t* up
         XPU_TRY(launched(gemm_act_pp_xt(st, xq, up_wp ? up_wp : up_w8, K, v, inner, xs, up_scale,
                                         int(M), int(inner), int(K), activation, up_wp != nullptr),
                          "ffn (up projection)"));
+    } else if (up_wp && skinny_applies(int(M), act_paired(activation)) &&
+               rowquant_can_tile(int(K))) {
+        // so does the skinny one, given the packed weight
+        XPU_TRY(launched(convrot_quantize_tiled(st, x, xq, xs, M, int(K)), "ffn (quantize)"));
+        XPU_TRY(launched(gemm_act_skinny_xt(st, xq, up_wp, v, inner, xs, up_scale, int(M),
+                                            int(inner), int(K), activation),
+                         "ffn (up projection)"));
     } else {
         XPU_TRY(launched(convrot_quantize(st, x, xq, xs, M, int(K), 0), "ffn (quantize)"));
         XPU_TRY(launched(gemm_act(st, xq, K, up_w8, K, v, inner, xs, up_scale, int(M),
-                                  int(inner), int(K), activation),
+                                  int(inner), int(K), activation, up_wp),
                          "ffn (up projection)"));
     }
     return linear_run(st, v, down_w8, down_scale, bias, bias_bf16, out, M, K, inner, region,
@@ -724,6 +738,10 @@ int xpuint8_linear_gemm_packed_stream(const void* stream, const int8_t* xq, cons
     if (splitk_applies(int(M), int(N), int(K)) && gemm_slices(int(M), int(N), int(K)) == 0)
         return launched(gemm_dequant_xt(st, xq, w8_packed, 0, out, N, x_scale, w_scale, b32, b16,
                                         int(M), int(N), int(K), true),
+                        "linear_gemm_packed");
+    if (skinny_applies(int(M), false) && gemm_slices(int(M), int(N), int(K)) == 0)
+        return launched(gemm_dequant_skinny_xt(st, xq, w8_packed, out, N, x_scale, w_scale, b32,
+                                               b16, int(M), int(N), int(K)),
                         "linear_gemm_packed");
     return fail(2, "linear_gemm_packed: this shape does not read the block layouts");
 }

@@ -1582,7 +1582,12 @@ hipError_t launch_splitk(hipStream_t st, const int8_t* X, int64_t ldx, const int
 // at ffn = 5120, K = 1280 took 6.0 / 9.4 / 13.5 us cold at M = 1 / 64 / 128
 // against 6.3 / 11.2 / 16.5 with one (every block reads all of X, so fewer,
 // wider blocks read less of it).
-template <int MB, int NW, int NB, class Epi>
+// WT: the weight packed (pack_weight), each lane's 16 bytes of a step read
+// from its block's contiguous 1 KB (chunk c of row r at (c ^ ((r >> 1) & 3)) *
+// 16), so one load instruction covers whole cache lines: 7.3 -> 6.2 us cold at
+// M = 16, N = K = 4096 (timing-only build of the pattern).  XT: X in the MFMA
+// block layout (tiled_offset) the same way.
+template <int MB, int NW, int NB, class Epi, bool WT = false, bool XT = false>
 __global__ __launch_bounds__(NW * 64) void gemm_i8_skinny_kernel(
     const int8_t* __restrict__ X, int64_t ldx, const int8_t* __restrict__ W, int64_t ldw, int M,
     int N, int K, Epi epi) {
@@ -1594,6 +1599,8 @@ __global__ __launch_bounds__(NW * 64) void gemm_i8_skinny_kernel(
     constexpr int NC = PAIRED ? NB / 2 : NB;                 // output column blocks
     static_assert(!PAIRED || NB % 2 == 0, "a paired epilogue takes both halves of each block");
     static_assert(NW * NB * MB <= 160, "the partial sums fit in the CU's 160 KB of LDS");
+    static_assert(!WT || !IsSliceEpi<Epi>::value, "the packed weight: whole-K products");
+    static_assert(!XT || !IsSliceEpi<Epi>::value, "x in the block layout: whole-K products");
     constexpr int D = NW >= 16 ? 4 : (MB * NB <= 2 ? 8 : (MB * NB <= 8 ? 4 : 2));  // steps in flight
     __shared__ v4i part[NW][NB * MB][64];
     // K slice blockIdx.y of a split across blocks (EpiSliceI32): K is the
@@ -1605,7 +1612,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_i8_skinny_kernel(
         W += int64_t(blockIdx.y) * K;
     } else {
         m_base = int(blockIdx.y) * 16 * MB;
-        X += int64_t(m_base) * ldx;
+        if constexpr (!XT) X += int64_t(m_base) * ldx;
         M -= m_base;
     }
     const int lane = threadIdx.x & 63;
@@ -1615,13 +1622,34 @@ __global__ __launch_bounds__(NW * 64) void gemm_i8_skinny_kernel(
     const int8_t* wrow[NB];
 #pragma unroll
     for (int p = 0; p < NB; ++p) {
-        const int r = min(n0 + 16 * (p % NC) + (lane & 15), N - 1) +
-                      (p >= NC ? pair_offset(epi) : 0);
-        wrow[p] = W + int64_t(r) * ldw + kb;
+        if constexpr (WT) {
+            // block n/16 of the packed weight (the last one past N), or the
+            // gate half's pair_offset/16 further; this lane's chunk in it
+            const int nb = min(n0 / 16 + (p % NC), (N - 1) / 16) +
+                           (p >= NC ? pair_offset(epi) / 16 : 0);
+            const int r = lane & 15;
+            wrow[p] = W + int64_t(nb) * ((K + 63) / 64) * 1024 + r * 64 +
+                      ((((lane >> 4) ^ (r >> 1)) & 3) << 4);
+        } else {
+            const int r = min(n0 + 16 * (p % NC) + (lane & 15), N - 1) +
+                          (p >= NC ? pair_offset(epi) : 0);
+            wrow[p] = W + int64_t(r) * ldw + kb;
+        }
     }
     const int8_t* xrow[MB];
 #pragma unroll
-    for (int b = 0; b < MB; ++b) xrow[b] = X + int64_t(min(16 * b + (lane & 15), M - 1)) * ldx + kb;
+    for (int b = 0; b < MB; ++b) {
+        if constexpr (XT) {
+            // the block of rows m_base + 16b (the last one past M): its rows
+            // past M hold whatever the quantizer left, read into outputs the
+            // epilogue never stores
+            const int r = lane & 15;
+            xrow[b] = X + (int64_t(m_base / 16 + min(b, (M - 1) / 16)) * ((K + 63) / 64)) * 1024 +
+                      r * 64 + ((((lane >> 4) ^ (r >> 1)) & 3) << 4);
+        } else {
+            xrow[b] = X + int64_t(min(16 * b + (lane & 15), M - 1)) * ldx + kb;
+        }
+    }
     const int S = (K + 63) / 64;                             // K steps
     // the wave's t-th step (pairing consecutive steps in one wave, so it reads
     // both halves of a 128-byte row segment back to back, measured slower)
@@ -1631,9 +1659,11 @@ __global__ __launch_bounds__(NW * 64) void gemm_i8_skinny_kernel(
         const int k = step * 64;
         if (step < S && k + kb < K) {
 #pragma unroll
-            for (int p = 0; p < NB; ++p) wbuf[slot][p] = *reinterpret_cast<const v4i*>(wrow[p] + k);
+            for (int p = 0; p < NB; ++p)
+                wbuf[slot][p] = *reinterpret_cast<const v4i*>(wrow[p] + (WT ? int64_t(step) * 1024 : k));
 #pragma unroll
-            for (int b = 0; b < MB; ++b) xbuf[slot][b] = *reinterpret_cast<const v4i*>(xrow[b] + k);
+            for (int b = 0; b < MB; ++b)
+                xbuf[slot][b] = *reinterpret_cast<const v4i*>(xrow[b] + (XT ? int64_t(step) * 1024 : k));
         } else {
 #pragma unroll
             for (int p = 0; p < NB; ++p) wbuf[slot][p] = v4i{0, 0, 0, 0};
@@ -1698,7 +1728,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_i8_skinny_kernel(
 // K steps.  M <= 64 for any epilogue; up to 128 (8 m-blocks) for a paired or
 // slice epilogue; a paired epilogue above 128 rows over a (ceil(N / 8NB),
 // ceil(M / 128)) grid of 128-row chunks.
-template <int NB, class Epi>
+template <int NB, class Epi, bool WT = false, bool XT = false>
 hipError_t launch_skinny(hipStream_t st, const int8_t* X, int64_t ldx, const int8_t* W,
                          int64_t ldw, int M, int N, int K, const Epi& epi, int nsl = 1) {
     constexpr bool kWide = Epi::kPaired || IsSliceEpi<Epi>::value;
@@ -1711,8 +1741,8 @@ hipError_t launch_skinny(hipStream_t st, const int8_t* X, int64_t ldx, const int
         constexpr int NWV = decltype(NWc)::value;
         const dim3 block(NWV * 64);
 #define XPU_SKINNY(MBV)                                                                         \
-    hipLaunchKernelGGL((gemm_i8_skinny_kernel<MBV, NWV, NB, Epi>), grid, block, 0, st, X, ldx, W, \
-                       ldw, M, N, K, epi)
+    hipLaunchKernelGGL((gemm_i8_skinny_kernel<MBV, NWV, NB, Epi, WT, XT>), grid, block, 0, st, X, \
+                       ldx, W, ldw, M, N, K, epi)
         switch ((mrows + 15) / 16) {
             case 1: XPU_SKINNY(1); break;
             case 2: XPU_SKINNY(2); break;
@@ -1783,10 +1813,18 @@ hipError_t launch_pp(hipStream_t st, const int8_t* X, int64_t ldx, const int8_t*
 
 template <class Epi>
 hipError_t launch_gemm(hipStream_t st, const int8_t* X, int64_t ldx, const int8_t* W, int64_t ldw,
-                       int M, int N, int K, const Epi& epi) {
+                       int M, int N, int K, const Epi& epi, const int8_t* Wp = nullptr) {
     constexpr int BM = 256, BN = 160, STAGES = 2;
+    // Wp (optional): pack_weight's copy of W, which the skinny kernel reads
+    // instead of W (the other kernels here read W)
+    constexpr bool kPackable = !IsSliceEpi<Epi>::value;
     if constexpr (Epi::kPaired) {
-        if (M <= kSkinnyPairedM) return launch_skinny<4>(st, X, ldx, W, ldw, M, N, K, epi);
+        if (M <= kSkinnyPairedM) {
+            if constexpr (kPackable) {
+                if (Wp) return launch_skinny<4, Epi, true>(st, X, ldx, Wp, 0, M, N, K, epi);
+            }
+            return launch_skinny<4>(st, X, ldx, W, ldw, M, N, K, epi);
+        }
         // the ping-pong tile, 4 x 2 waves of 64 x 160 (five whole pairs each),
         // when it gives one tile per CU (5% faster at the FFN up-projection)
         const int tm = (M + BM - 1) / BM, tn_pp = (N + 159) / 160;
@@ -1805,7 +1843,12 @@ hipError_t launch_gemm(hipStream_t st, const int8_t* X, int64_t ldx, const int8_
                                tm, tn, epi);
         return hipGetLastError();
     } else {
-        if (M <= 64) return launch_skinny<1>(st, X, ldx, W, ldw, M, N, K, epi);
+        if (M <= 64) {
+            if constexpr (kPackable) {
+                if (Wp) return launch_skinny<1, Epi, true>(st, X, ldx, Wp, 0, M, N, K, epi);
+            }
+            return launch_skinny<1>(st, X, ldx, W, ldw, M, N, K, epi);
+        }
         const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
         if constexpr (Epi::kStaged) {
             // narrow output, long K: split K inside 128 x 160 tiles instead
@@ -2081,9 +2124,9 @@ hipError_t gemm_i32(hipStream_t st, const int8_t* A, int64_t lda, const int8_t* 
 
 hipError_t gemm_dequant(hipStream_t st, const int8_t* A, int64_t lda, const int8_t* B, int64_t ldb,
                         void* out, int64_t ldo, const float* xs, const float* ws, const float* bias,
-                        const uint16_t* bias16, int M, int N, int K) {
+                        const uint16_t* bias16, int M, int N, int K, const int8_t* Bp) {
     return launch_gemm(st, A, lda, B, ldb, M, N, K,
-                       EpiDequant{static_cast<uint16_t*>(out), ldo, xs, ws, bias, bias16});
+                       EpiDequant{static_cast<uint16_t*>(out), ldo, xs, ws, bias, bias16}, Bp);
 }
 
 hipError_t gemm_dequant_nn(hipStream_t st, const int8_t* A, int64_t lda, const int8_t* Bkn,
@@ -2130,6 +2173,31 @@ hipError_t gemm_act_pp_xt(hipStream_t st, const int8_t* At, const int8_t* B, int
         case 3: return act_pp_xt(st, At, B, ldb, EpiAct<3>{o, ldo, xs, ws, N, tab}, M, N, K, packed);
         case 4: return act_pp_xt(st, At, B, ldb, EpiAct<4>{o, ldo, xs, ws, N, tab}, M, N, K, packed);
         case 5: return act_pp_xt(st, At, B, ldb, EpiAct<5>{o, ldo, xs, ws, N, tab}, M, N, K, packed);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+bool skinny_applies(int M, bool paired) { return M <= (paired ? kSkinnyPairedM : 64); }
+
+hipError_t gemm_dequant_skinny_xt(hipStream_t st, const int8_t* At, const int8_t* Bp, void* out,
+                                  int64_t ldo, const float* xs, const float* ws, const float* bias,
+                                  const uint16_t* bias16, int M, int N, int K) {
+    const EpiDequant epi{static_cast<uint16_t*>(out), ldo, xs, ws, bias, bias16};
+    return launch_skinny<1, EpiDequant, true, true>(st, At, 0, Bp, 0, M, N, K, epi);
+}
+
+hipError_t gemm_act_skinny_xt(hipStream_t st, const int8_t* At, const int8_t* Bp, void* out,
+                              int64_t ldo, const float* xs, const float* ws, int M, int N, int K,
+                              int act) {
+    uint16_t* o = static_cast<uint16_t*>(out);
+    const uint16_t* tab = activation_tables();
+    switch (act) {
+        case 3: return launch_skinny<4, EpiAct<3>, true, true>(st, At, 0, Bp, 0, M, N, K,
+                                                              EpiAct<3>{o, ldo, xs, ws, N, tab});
+        case 4: return launch_skinny<4, EpiAct<4>, true, true>(st, At, 0, Bp, 0, M, N, K,
+                                                              EpiAct<4>{o, ldo, xs, ws, N, tab});
+        case 5: return launch_skinny<1, EpiAct<5>, true, true>(st, At, 0, Bp, 0, M, N, K,
+                                                              EpiAct<5>{o, ldo, xs, ws, N, tab});
         default: return hipErrorInvalidValue;
     }
 }
@@ -2187,13 +2255,13 @@ hipError_t gemm_i32_pp_xt(hipStream_t st, const int8_t* At, const int8_t* B, int
 
 hipError_t gemm_act(hipStream_t st, const int8_t* A, int64_t lda, const int8_t* B, int64_t ldb,
                     void* out, int64_t ldo, const float* xs, const float* ws, int M, int N, int K,
-                    int act) {
+                    int act, const int8_t* Bp) {
     uint16_t* o = static_cast<uint16_t*>(out);
     const uint16_t* tab = activation_tables();
     switch (act) {
-        case 3: return launch_gemm(st, A, lda, B, ldb, M, N, K, EpiAct<3>{o, ldo, xs, ws, N, tab});
-        case 4: return launch_gemm(st, A, lda, B, ldb, M, N, K, EpiAct<4>{o, ldo, xs, ws, N, tab});
-        case 5: return launch_gemm(st, A, lda, B, ldb, M, N, K, EpiAct<5>{o, ldo, xs, ws, N, tab});
+        case 3: return launch_gemm(st, A, lda, B, ldb, M, N, K, EpiAct<3>{o, ldo, xs, ws, N, tab}, Bp);
+        case 4: return launch_gemm(st, A, lda, B, ldb, M, N, K, EpiAct<4>{o, ldo, xs, ws, N, tab}, Bp);
+        case 5: return launch_gemm(st, A, lda, B, ldb, M, N, K, EpiAct<5>{o, ldo, xs, ws, N, tab}, Bp);
         default: return hipErrorInvalidValue;
     }
 }

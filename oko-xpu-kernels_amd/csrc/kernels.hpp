@@ -52,9 +52,11 @@ hipError_t column_sum_bf16(hipStream_t st, const void* x, void* out, int64_t M, 
 // gemm_i8.hip
 hipError_t gemm_i32(hipStream_t st, const int8_t* A, int64_t lda, const int8_t* B, int64_t ldb,
                     int32_t* C, int64_t ldc, int M, int N, int K);
+// Bp (here and in gemm_act; optional): pack_weight's copy of B, which the
+// skinny kernel reads instead of B
 hipError_t gemm_dequant(hipStream_t st, const int8_t* A, int64_t lda, const int8_t* B, int64_t ldb,
                         void* out, int64_t ldo, const float* xs, const float* ws, const float* bias,
-                        const uint16_t* bias16, int M, int N, int K);
+                        const uint16_t* bias16, int M, int N, int K, const int8_t* Bp = nullptr);
 // the dequant GEMM with B stored [K, N] (the NN product, no column scale), when
 // the split-K kernel takes the shape; *done = false (nothing launched) otherwise
 hipError_t gemm_dequant_nn(hipStream_t st, const int8_t* A, int64_t lda, const int8_t* Bkn,
@@ -115,7 +117,17 @@ hipError_t gemm_i32_pp_xt(hipStream_t st, const int8_t* At, const int8_t* B, int
 // paired activations 3 (situ) and 4 (GEGLU), whose B has 2N rows; act 5 (GELU) takes N rows
 hipError_t gemm_act(hipStream_t st, const int8_t* A, int64_t lda, const int8_t* B, int64_t ldb,
                     void* out, int64_t ldo, const float* xs, const float* ws, int M, int N, int K,
-                    int act);
+                    int act, const int8_t* Bp = nullptr);
+// The skinny kernel with x in the MFMA block layout (At) and the packed weight
+// (Bp), for the batches launch_gemm gives it (skinny_applies: M <= 64; paired
+// activations 3 and 4, M <= 256); a linear's callers check gemm_slices first
+bool skinny_applies(int M, bool paired);
+hipError_t gemm_dequant_skinny_xt(hipStream_t st, const int8_t* At, const int8_t* Bp, void* out,
+                                  int64_t ldo, const float* xs, const float* ws, const float* bias,
+                                  const uint16_t* bias16, int M, int N, int K);
+hipError_t gemm_act_skinny_xt(hipStream_t st, const int8_t* At, const int8_t* Bp, void* out,
+                              int64_t ldo, const float* xs, const float* ws, int M, int N, int K,
+                              int act);
 hipError_t dequant_epilogue(hipStream_t st, const int32_t* acc, int64_t acc_ld, void* out,
                             const float* xs, const float* ws, const float* bias, int64_t M,
                             int64_t N);

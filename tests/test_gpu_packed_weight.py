@@ -75,10 +75,13 @@ def _both(dev, n, k, seed):
 
 # (M, N, K): the persistent kernel (config 3; a batch that is not a multiple
 # of 256), the split-K kernel (the SDXL N = 1280 shapes; ragged rows and a
-# last column tile of 16), K slices (M = 200, 512) and the skinny kernel (M = 16).
+# last column tile of 16), K slices (M = 200, 512; M = 48 at N < 2048) and the
+# skinny kernel reading the packed weight (M = 1, 7, 16, 48 at N >= 2048, 64;
+# the row counts one m-block to four, N = 1296 a last weight block alone)
 LINEAR_SHAPES = [(4096, 10240, 1280), (3000, 10240, 1280), (4096, 1280, 5120),
                  (4096, 1280, 2048), (4096, 1280, 1280), (2100, 1296, 2048), (200, 1280, 4096),
-                 (512, 4096, 4096), (16, 4096, 4096)]
+                 (512, 4096, 4096), (16, 4096, 4096), (1, 4096, 4096), (7, 1296, 2048),
+                 (48, 2064, 1280), (64, 10240, 1280), (48, 1280, 5120)]
 
 
 @pytest.mark.parametrize("m,n,k", LINEAR_SHAPES)
@@ -91,7 +94,8 @@ def test_linear_packed_equals_rowmajor(dev, m, n, k):
     assert np.array_equal(bits(yp), bits(yr)), mismatch(bits(yp), bits(yr))
 
 
-@pytest.mark.parametrize("m,n,k", [(4096, 10240, 1280), (4096, 1280, 1280), (1100, 1296, 2048)])
+@pytest.mark.parametrize("m,n,k", [(4096, 10240, 1280), (4096, 1280, 1280), (1100, 1296, 2048),
+                                   (16, 4096, 4096), (5, 1296, 1280)])
 def test_linear_packed_exact(dev, m, n, k):
     w8p, _, ws = _both(dev, n, k, seed=n + 13)
     x = activation(m, k, seed=2 * m + k)
@@ -103,7 +107,8 @@ def test_linear_packed_exact(dev, m, n, k):
 
 def test_linear_gemm_packed_entry(dev):
     """xpuint8_linear_gemm_packed_stream against xpuint8_linear_gemm_tiled_stream
-    (the block-layout x, row-major weight) at config 3 and a split-K shape."""
+    (the block-layout x, row-major weight) at config 3 and a split-K shape, and
+    against xpuint8_linear_gemm_stream at two skinny shapes."""
     lib = L._lib()
     for m, n, k in [(4096, 10240, 1280), (4096, 1280, 5120)]:
         w8p, _, ws = _both(dev, n, k, seed=n + 17)
@@ -125,22 +130,50 @@ def test_linear_gemm_packed_entry(dev):
                                                      L._ptr(ws), L._ptr(b), 1, L._ptr(o2),
                                                      m, n, k) == 0, lib.xpuint8_last_error()
         assert np.array_equal(bits(o1), bits(o2)), mismatch(bits(o1), bits(o2))
-    # a shape whose GEMM reads neither block layout is refused
-    xq = torch.zeros(16 * 4096, device=dev, dtype=torch.int8)
-    xs = torch.ones(16, device=dev)
-    o = torch.empty((16, 4096), device=dev, dtype=torch.bfloat16)
-    w8p, _, ws = _both(dev, 4096, 4096, seed=1)
+    # the skinny kernel (M = 16, 40) against xpuint8_linear_gemm_stream (q and
+    # the weight row-major)
+    for m, n, k in [(16, 4096, 4096), (40, 2064, 1280)]:
+        w8p, _, ws = _both(dev, n, k, seed=n + 19)
+        x = activation(m, k, seed=m + 5).to(dev)
+        q, xs = int8.quantize(x)
+        tb = ((m + 15) // 16) * ((k + 63) // 64) * 1024
+        xq = torch.empty(tb, device=dev, dtype=torch.int8)
+        xs_t = torch.empty(m, device=dev, dtype=torch.float32)
+        st = L._stream(dev)
+        assert lib.xpuint8_convrot_quantize_tiled_stream(st, L._ptr(x), L._ptr(xq),
+                                                         L._ptr(xs_t), m, k) == 0
+        assert torch.equal(xs, xs_t)
+        b = weight(1, n, seed=8, std=0.01)[0].to(dev)
+        o1 = torch.empty((m, n), device=dev, dtype=torch.bfloat16)
+        o2 = torch.empty((m, n), device=dev, dtype=torch.bfloat16)
+        assert lib.xpuint8_linear_gemm_stream(st, L._ptr(q), L._ptr(xs), L._ptr(w8p), L._ptr(ws),
+                                              L._ptr(b), 1, L._ptr(o1), m, n, k) == 0
+        assert lib.xpuint8_linear_gemm_packed_stream(
+            st, L._ptr(xq), L._ptr(xs_t), L._ptr(ops._packed_for(w8p)), L._ptr(ws), L._ptr(b), 1,
+            L._ptr(o2), m, n, k) == 0, lib.xpuint8_last_error()
+        assert np.array_equal(bits(o1), bits(o2)), mismatch(bits(o1), bits(o2))
+    # a shape whose GEMM reads neither block layout (K slices) is refused
+    xq = torch.zeros(48 * 5120, device=dev, dtype=torch.int8)
+    xs = torch.ones(48, device=dev)
+    o = torch.empty((48, 1280), device=dev, dtype=torch.bfloat16)
+    w8p, _, ws = _both(dev, 1280, 5120, seed=1)
     assert lib.xpuint8_linear_gemm_packed_stream(L._stream(dev), L._ptr(xq), L._ptr(xs),
                                                  L._ptr(ops._packed_for(w8p)), L._ptr(ws), None,
-                                                 0, L._ptr(o), 16, 4096, 4096) != 0
+                                                 0, L._ptr(o), 48, 1280, 5120) != 0
 
 
 # (M, K, inner, act): config 4 (GEGLU), a ragged batch, GELU-erf (an
-# unpaired up-projection), situ at a batch small enough for K slices below
+# unpaired up-projection), and the skinny up-projection reading the packed
+# weight: situ at 256 rows (two 128-row chunks) and K slices in the
+# down-projection, GEGLU at one row and 129 (a chunk of one row), GELU-erf at
+# 40 rows (unpaired)
 @pytest.mark.parametrize("m,k,inner,act", [(4096, 1280, 5120, "geglu_erf"),
                                            (2100, 1280, 5120, "geglu_erf"),
                                            (4096, 1280, 5120, "gelu_erf"),
-                                           (256, 1280, 5120, "situ")])
+                                           (256, 1280, 5120, "situ"),
+                                           (1, 1280, 5120, "geglu_erf"),
+                                           (129, 1280, 5120, "geglu_erf"),
+                                           (40, 1280, 5120, "gelu_erf")])
 def test_ffn_packed_equals_rowmajor(dev, m, k, inner, act):
     up_rows = 2 * inner if act in ("geglu_erf", "situ") else inner
     up_p, up_r, us = _both(dev, up_rows, k, seed=up_rows + 1)
