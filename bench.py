@@ -114,6 +114,38 @@ def timed(torch, fn, steps, warmup, settle_s=0.0):
     return a.elapsed_time(b) / steps
 
 
+def timed_graph(torch, fn, calls, reps=4, settle_s=0.0):
+    """Average ms per launch of ``fn(i, stream)`` for i = 0 .. calls-1,
+    captured once into a HIP graph on a side stream and replayed ``reps``
+    times (after a ``settle_s`` run-in of replays).  Launches in a graph leave
+    the host's per-call cost (ctypes, argument checks, the launch itself,
+    ~4 us from a Python loop) out of the figure, so a kernel shorter than
+    that is timed by the GPU, back to back with its neighbours, each launch
+    still on its own buffer set."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for i in range(3):
+            fn(i, s.cuda_stream)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        for i in range(calls):
+            fn(i, s.cuda_stream)
+    settle(torch, g.replay, settle_s)
+    g.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        g.replay()
+    b.record()
+    torch.cuda.synchronize()
+    del g
+    return a.elapsed_time(b) / (reps * calls)
+
+
 COLD_BYTES = 640 << 20           # buffer sets per cold measurement: > 2.5x the 256 MB MALL
 
 
@@ -373,16 +405,27 @@ def measure_side_rows(torch, int8, lib, L, st, dev, K, W, SET, extra, hbm_line, 
         t_i8 = timed(torch, lambda i: int8.linear(*ss[i % nss][:4]), K, W, SET)
         t_bf = timed(torch, lambda i: torch.nn.functional.linear(ss[i % nss][0], ss[i % nss][4],
                                                                  ss[i % nss][3]), K, W, SET)
+        # the same calls replayed from HIP graphs (one launch sequence per
+        # call, each call on its own set): the GPU's time per call without the
+        # Python host cost of either API (int8.linear's is ~16 us per call)
+        g_i8 = timed_graph(torch, lambda i, s: int8.linear(*ss[i % nss][:4]), nss, settle_s=SET)
+        g_bf = timed_graph(torch, lambda i, s: torch.nn.functional.linear(
+            ss[i % nss][0], ss[i % nss][4], ss[i % nss][3]), nss, settle_s=SET)
         sdxl[f"K{Ks}_N{Ns}_M{Ms}"] = {
             "int8_linear_ms_cold": round(t_i8, 5),
             "int8_TOP/s": round(2.0 * Ms * Ns * Ks / (t_i8 * 1e-3) / 1e12, 1),
             "torch_bf16_linear_ms_cold": round(t_bf, 5),
             "int8_over_bf16": round(t_i8 / t_bf, 3),
+            "graph_int8_linear_ms_cold": round(g_i8, 5),
+            "graph_torch_bf16_linear_ms_cold": round(g_bf, 5),
+            "graph_int8_over_bf16": round(g_i8 / g_bf, 3),
             "reference_b580_int8_ms": ref_ms}
         del ss
     extra["sdxl_shapes"] = sdxl
     log("[bench] SDXL shapes: " + ", ".join(f"{k} {v['int8_linear_ms_cold'] * 1e3:.1f} us "
-                                            f"(bf16 {v['torch_bf16_linear_ms_cold'] * 1e3:.1f})"
+                                            f"(bf16 {v['torch_bf16_linear_ms_cold'] * 1e3:.1f}; "
+                                            f"graphs {v['graph_int8_linear_ms_cold'] * 1e3:.1f} / "
+                                            f"{v['graph_torch_bf16_linear_ms_cold'] * 1e3:.1f})"
                                             for k, v in sdxl.items()))
 
     # int8_linear training step at config 5 shapes: forward, then backward
@@ -537,11 +580,15 @@ def main():
     def gbs(nbytes, ms):
         return nbytes / (ms * 1e-3) / 1e9
 
-    def hbm_line(nbytes, ms_cold, ms_warm, **more):
+    def hbm_line(nbytes, ms_cold, ms_warm, graph_ms_cold=None, **more):
         d = {"ms_cold": round(ms_cold, 5), "GB/s_cold": round(gbs(nbytes, ms_cold), 1),
              "frac_hbm_peak_cold": round(gbs(nbytes, ms_cold) / PEAK_HBM_GBPS, 4),
              "ms_warm": round(ms_warm, 5), "GB/s_warm": round(gbs(nbytes, ms_warm), 1),
              "bytes": int(nbytes)}
+        if graph_ms_cold is not None:
+            # the same cold launches replayed from a HIP graph (no host cost)
+            d["graph_ms_cold"] = round(graph_ms_cold, 5)
+            d["graph_frac_hbm_peak_cold"] = round(gbs(nbytes, graph_ms_cold) / PEAK_HBM_GBPS, 4)
         d.update(more)
         return d
 
@@ -639,18 +686,19 @@ def main():
     q3 = [(torch.empty(tiled_bytes, device=dev, dtype=torch.int8),
            torch.empty(M, device=dev, dtype=torch.float32)) for _ in range(n3)]
 
-    def quant3(i):
+    def quant3(i, s=st):
         xi = sets3[i % n3][0]
         qi, si = q3[i % n3]
-        lib.xpuint8_convrot_quantize_tiled_stream(st, L._ptr(xi), L._ptr(qi), L._ptr(si), M, Kd)
+        lib.xpuint8_convrot_quantize_tiled_stream(s, L._ptr(xi), L._ptr(qi), L._ptr(si), M, Kd)
     bytes_q3 = 3 * M * Kd + 4 * M
-    ms_q3 = ms_q3_warm = float("nan")
+    ms_q3 = ms_q3_warm = ms_q3_graph = float("nan")
     if not (args.only_rowquant or args.only_c45):
         ms_q3 = timed(torch, quant3, K, W, SET)
         ms_q3_warm = timed(torch, lambda i: quant3(0), K, W, SET)
+        ms_q3_graph = timed_graph(torch, quant3, K, settle_s=SET)
     log(f"[bench] step {ms:.4f} ms cold / {ms_warm:.4f} warm = {value:.1f} TOP/s; GEMM "
         f"{ms_gemm:.4f} / {ms_gemm_warm:.4f} ms = {gemm_tops:.1f} TOP/s; quantize "
-        f"{ms_q3:.4f} / {ms_q3_warm:.4f} ms")
+        f"{ms_q3:.4f} / {ms_q3_warm:.4f} ms (graph, cold {ms_q3_graph:.4f})")
     extra["config3_step_ms_warm"] = round(ms_warm, 5)
     extra["config3_TOP/s_warm"] = round(ops3 / (ms_warm * 1e-3) / 1e12, 2)
     extra["config3_gemm"] = {"ms_cold": round(ms_gemm, 5), "ms_warm": round(ms_gemm_warm, 5),
@@ -666,7 +714,7 @@ def main():
         extra["config3_rowmajor_weight"] = {"step_ms_cold": round(ms_rm, 5),
                                             "TOP/s_cold": round(ops3 / (ms_rm * 1e-3) / 1e12, 1)}
         del sets3r
-    extra["config3_quantize"] = hbm_line(bytes_q3, ms_q3, ms_q3_warm)
+    extra["config3_quantize"] = hbm_line(bytes_q3, ms_q3, ms_q3_warm, graph_ms_cold=ms_q3_graph)
     del gsets
 
     if not (args.only_main or args.only_c45):
@@ -682,9 +730,9 @@ def main():
                   torch.empty((Mr, Kr), device=dev, dtype=torch.int8),
                   torch.empty(Mr, device=dev, dtype=torch.float32)) for i in range(n2)]
 
-        def rq(i):
+        def rq(i, s=st):
             xi, qi, si = sets2[i % n2]
-            lib.xpuint8_convrot_quantize_stream(st, L._ptr(xi), L._ptr(qi), L._ptr(si), Mr, Kr)
+            lib.xpuint8_convrot_quantize_stream(s, L._ptr(xi), L._ptr(qi), L._ptr(si), Mr, Kr)
         ms_q = timed(torch, rq, K, W, SET)
         if args.only_rowquant:
             print(json.dumps({"only_rowquant": True, "rotate_quant_ms_cold": round(ms_q, 5),
@@ -692,6 +740,7 @@ def main():
                               "sets": n2}), flush=True)
             return
         ms_q_warm = timed(torch, lambda i: rq(0), K, W, SET)
+        ms_q_graph = timed_graph(torch, rq, K, settle_s=SET)
         ms_q_api = timed(torch, lambda i: int8.quantize(x2), K, W, SET)
         # the same traffic through torch's vectorized elementwise kernel (read
         # the bf16 tensor, write one byte per element: x != 0 into a bool
@@ -700,7 +749,7 @@ def main():
         ne_out = [torch.empty((Mr, Kr), device=dev, dtype=torch.bool) for _ in range(n2)]
         ms_copy = timed(torch, lambda i: torch.ne(sets2[i % n2][0], 0, out=ne_out[i % n2]), K, W, SET)
         extra["config2_rotate_quant"] = hbm_line(
-            bytes_q, ms_q, ms_q_warm, api_ms_warm=round(ms_q_api, 5), sets=n2,
+            bytes_q, ms_q, ms_q_warm, graph_ms_cold=ms_q_graph, api_ms_warm=round(ms_q_api, 5), sets=n2,
             streaming_ceiling_ms_cold=round(ms_copy, 5),
             streaming_ceiling_frac_hbm_peak_cold=round(gbs(3 * Mr * Kr, ms_copy) / PEAK_HBM_GBPS, 4))
         del sets2, ne_out
@@ -711,12 +760,14 @@ def main():
                   torch.empty((10240, 1280), device=dev, dtype=torch.int8),
                   torch.empty(10240, device=dev, dtype=torch.float32)) for i in range(npw)]
 
-        def pw(i):
+        def pw(i, s=st):
             wi, qi, si = setsp[i % npw]
-            lib.xpuint8_prepare_weight_stream(st, L._ptr(wi), L._ptr(qi), L._ptr(si), 10240, 1280)
+            lib.xpuint8_prepare_weight_stream(s, L._ptr(wi), L._ptr(qi), L._ptr(si), 10240, 1280)
         ms_p = timed(torch, pw, K, W, SET)
         ms_p_warm = timed(torch, lambda i: pw(0), K, W, SET)
-        extra["config2_prepare_weight"] = hbm_line(bytes_p, ms_p, ms_p_warm, sets=npw)
+        ms_p_graph = timed_graph(torch, pw, K, settle_s=SET)
+        extra["config2_prepare_weight"] = hbm_line(bytes_p, ms_p, ms_p_warm, graph_ms_cold=ms_p_graph,
+                                                   sets=npw)
         del setsp
         log(f"[bench] config 2: rotate+quant {ms_q:.4f} ms cold / {ms_q_warm:.4f} warm "
             f"(API {ms_q_api:.4f}), prepare_weight {ms_p:.4f} / {ms_p_warm:.4f} ms")
@@ -780,13 +831,15 @@ def main():
                   torch.empty((4096, 5120), device=dev, dtype=torch.int8),
                   torch.empty(4096, device=dev, dtype=torch.float32)) for i in range(nrq)]
 
-        def qrow(i):
+        def qrow(i, s=st):
             di, qi, si = setsr[i % nrq]
-            lib.xpuint8_quantize_row_stream(st, L._ptr(di), L._ptr(w5_s), L._ptr(qi), L._ptr(si),
+            lib.xpuint8_quantize_row_stream(s, L._ptr(di), L._ptr(w5_s), L._ptr(qi), L._ptr(si),
                                             4096, 5120)
         ms_rq = timed(torch, qrow, K, W, SET)
         ms_rq_warm = timed(torch, lambda i: qrow(0), K, W, SET)
-        extra["config5_quantize_row"] = hbm_line(bytes_rq, ms_rq, ms_rq_warm, sets=nrq)
+        ms_rq_graph = timed_graph(torch, qrow, K, settle_s=SET)
+        extra["config5_quantize_row"] = hbm_line(bytes_rq, ms_rq, ms_rq_warm,
+                                                 graph_ms_cold=ms_rq_graph, sets=nrq)
         del setsr
         # skinny M=16: the weight streamed once per call
         bytes_sk = 4096 * 4096 + 16 * 4096 + 2 * 16 * 4096 + 4 * 4096 + 4 * 16
@@ -806,9 +859,9 @@ def main():
         sk_p = [ops._packed_for(w_i) for w_i, _ in sk]
         assert all(p is not None for p in sk_p)
 
-        def skinny(i):
+        def skinny(i, s=st):
             j = i % nsk
-            lib.xpuint8_linear_gemm_packed_stream(st, L._ptr(q16t), L._ptr(s16t), L._ptr(sk_p[j]),
+            lib.xpuint8_linear_gemm_packed_stream(s, L._ptr(q16t), L._ptr(s16t), L._ptr(sk_p[j]),
                                                   L._ptr(sk[j][1]), None, 0, L._ptr(o16[j]), 16,
                                                   4096, 4096)
 
@@ -822,6 +875,7 @@ def main():
         assert torch.equal(o_p, o16[0]), "skinny: packed and row-major differ"
         ms_sk = timed(torch, skinny, K, W, SET)
         ms_sk_warm = timed(torch, lambda i: skinny(0), K, W, SET)
+        ms_sk_kgraph = timed_graph(torch, skinny, K, settle_s=SET)
         ms_sk_rm = timed(torch, skinny_rowmajor, K, W, SET)
         ms_sk_rm_warm = timed(torch, lambda i: skinny_rowmajor(0), K, W, SET)
         ms_sk_api = timed(torch, lambda i: int8.linear(xs16, *sk[0]), K, W, SET)
@@ -837,7 +891,8 @@ def main():
         with torch.cuda.graph(graph):
             int8.linear(xs16, *sk[0])
         ms_sk_graph = timed(torch, lambda i: graph.replay(), K, W, SET)
-        extra["config5_skinny_m16"] = hbm_line(bytes_sk, ms_sk, ms_sk_warm, sets=nsk,
+        extra["config5_skinny_m16"] = hbm_line(bytes_sk, ms_sk, ms_sk_warm, graph_ms_cold=ms_sk_kgraph,
+                                               sets=nsk,
                                                api_ms=round(ms_sk_api, 5),
                                                api_graph_replay_ms=round(ms_sk_graph, 5),
                                                rowmajor_ms_cold=round(ms_sk_rm, 5),
@@ -846,7 +901,7 @@ def main():
         log(f"[bench] config 5: dx {ms_dx_c:.4f} / {ms_dx:.4f} ms, dW {ms_dw_c:.4f} / {ms_dw:.4f} ms, "
             f"dense dx {ms_dxd_c:.4f} / {ms_dxd:.4f} ms (cold / warm), "
             f"quantize_row {ms_rq:.4f} / {ms_rq_warm:.4f} ms, skinny {ms_sk:.4f} / "
-            f"{ms_sk_warm:.4f} ms (API {ms_sk_api:.4f}, graph replay {ms_sk_graph:.4f})")
+            f"{ms_sk_warm:.4f} ms (graph, cold {ms_sk_kgraph:.4f}; API {ms_sk_api:.4f}, graph replay {ms_sk_graph:.4f})")
 
         # ------------------------------------ accumulator consumer: rms + rope
         # q slice [1, 4096, 24, 128] of a qkv accumulator [4096, 3*3072]
