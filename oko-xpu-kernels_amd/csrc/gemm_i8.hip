@@ -237,46 +237,88 @@ struct EpiAct {
         return make_uint2(cvt_pk_bf16(r0, r1), cvt_pk_bf16(r2, r3));
     }
     // convert / convert2 with the table read from the LDS window (win != 0):
-    // four 16-bit LDS reads at clamped positions, one wait, and the global
-    // table only for inputs outside the window, behind a wave-uniform branch
-    // that is rarely taken.  Same table words, so the same results.
-    __device__ __forceinline__ uint2 win_finish(const float (&a)[4], const float (&b)[4]) const {
-        uint32_t k[4], t[4];
-        bool miss = false;
+    // four 16-bit LDS reads, one wait, and the global table only for inputs
+    // outside the window, behind a wave-uniform branch that is rarely taken.
+    // Same table words, so the same results.
+    //
+    // The four dequantized keys (the table's inputs: the gate for GEGLU, the
+    // value for GELU) are rounded to bf16 two at a time, as packed pairs
+    // (v_cvt_pk_bf16_f32 rounds each half to nearest even, deq()'s rounding),
+    // and a pair's two window positions come from packed 16-bit integer
+    // arithmetic.  With t = key - kWinLo (16 bits, wrapping), a key lies in
+    // the window iff bits 11-14 of t are clear; t's bit 15 is then its sign
+    // and bits 0-10 its index, so its byte offset in the window (positive
+    // half first, win_bits' order) is (t << 1 & 0xFFE) | (t >> 3 & 0x1000).
+    // A key outside reads some entry inside (the offset is masked to the
+    // window) and is replaced from the global table.
+    typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
+    __device__ __forceinline__ uint2 win_finish(const float (&key)[4], const float (&val)[4]) const {
+        const uint32_t kp[2] = {cvt_pk_bf16(key[0], key[1]), cvt_pk_bf16(key[2], key[3])};
+        uint32_t t[4], tor = 0;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float x = ACT == 4 ? b[i] : a[i];
-            k[i] = __float_as_uint(x) >> 16;
-            const uint32_t rel = (k[i] & 0x7FFFu) - uint32_t(kWinLo);
-            miss = miss || rel >= uint32_t(kWinHalf);
-            const uint32_t addr = win + ((k[i] >> 15) << 12) + 2 * min(rel, uint32_t(kWinHalf - 1));
-            asm volatile("ds_read_u16 %0, %1" : "=v"(t[i]) : "v"(addr));
+        for (int j = 0; j < 2; ++j) {
+            const u16x2 tt = __builtin_bit_cast(u16x2, kp[j]) -
+                             u16x2{uint16_t(kWinLo), uint16_t(kWinLo)};
+            tor |= __builtin_bit_cast(uint32_t, tt);
+            const uint32_t lo2 = __builtin_bit_cast(uint32_t, u16x2(tt << u16x2{1, 1}));
+            const uint32_t hi3 = __builtin_bit_cast(uint32_t, u16x2(tt >> u16x2{3, 3}));
+            const uint32_t off = (lo2 & 0x0FFE0FFEu) | (hi3 & 0x10001000u);
+            // win + each 16-bit half of off, one SDWA add each (the compiler
+            // would fuse the low half's mask into the or above and add apart)
+            uint32_t a0, a1;
+            asm("v_add_u32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:WORD_0 "
+                "src1_sel:DWORD"
+                : "=v"(a0) : "v"(off), "v"(win));
+            asm("v_add_u32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:WORD_1 "
+                "src1_sel:DWORD"
+                : "=v"(a1) : "v"(off), "v"(win));
+            asm volatile("ds_read_u16 %0, %1" : "=v"(t[2 * j]) : "v"(a0));
+            asm volatile("ds_read_u16 %0, %1" : "=v"(t[2 * j + 1]) : "v"(a1));
         }
         asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(t[0]), "+v"(t[1]), "+v"(t[2]), "+v"(t[3]));
-        if (__builtin_amdgcn_ballot_w64(miss)) {
+        if (__builtin_amdgcn_ballot_w64((tor & 0x78007800u) != 0)) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                if ((k[i] & 0x7FFFu) - uint32_t(kWinLo) >= uint32_t(kWinHalf))
-                    t[i] = tab[kWinTab * kTabSize + k[i]];
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t k = (kp[i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
+                if (((k - uint32_t(kWinLo)) & 0x7800u) != 0)
+                    t[i] = tab[kWinTab * kTabSize + k];
+            }
         }
-        float r[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) r[i] = act_combine<ACT>(a[i], b[i], &t[i]);
-        return make_uint2(cvt_pk_bf16(r[0], r[1]), cvt_pk_bf16(r[2], r[3]));
+        if constexpr (ACT == 4) {
+            // the hidden values, rounded to bf16 in pairs, times the table's
+            // gelu(gate): each product exact in fp32, then the packing's
+            // rounding
+            const uint32_t vp0 = cvt_pk_bf16(val[0], val[1]), vp1 = cvt_pk_bf16(val[2], val[3]);
+            const float r0 = __uint_as_float(vp0 << 16) * tab_float(t[0]);
+            const float r1 = __uint_as_float(vp0 & 0xFFFF0000u) * tab_float(t[1]);
+            const float r2 = __uint_as_float(vp1 << 16) * tab_float(t[2]);
+            const float r3 = __uint_as_float(vp1 & 0xFFFF0000u) * tab_float(t[3]);
+            return make_uint2(cvt_pk_bf16(r0, r1), cvt_pk_bf16(r2, r3));
+        } else {
+            // a single lookup: the table's bf16 results through the same
+            // packing conversion as the unwindowed form (NaN words included)
+            return make_uint2(cvt_pk_bf16(tab_float(t[0]), tab_float(t[1])),
+                              cvt_pk_bf16(tab_float(t[2]), tab_float(t[3])));
+        }
+    }
+    // the dequant product before its bf16 rounding
+    __device__ __forceinline__ static float deq_raw(int a, float w, float x) {
+        return float(a) * (w * x);
     }
     __device__ __forceinline__ uint2 convert_w(const v4i& v, float x, const Col& c) const {
-        const float a[4] = {deq(v[0], c.w.x, x), deq(v[1], c.w.y, x), deq(v[2], c.w.z, x),
-                            deq(v[3], c.w.w, x)};
-        const float b[4] = {0.f, 0.f, 0.f, 0.f};
-        return win_finish(a, b);
+        static_assert(ACT == 5, "the windowed single-block form is GELU's");
+        const float k[4] = {deq_raw(v[0], c.w.x, x), deq_raw(v[1], c.w.y, x),
+                            deq_raw(v[2], c.w.z, x), deq_raw(v[3], c.w.w, x)};
+        return win_finish(k, k);
     }
     __device__ __forceinline__ uint2 convert2_w(const v4i& av, const v4i& bv, float x, const Col& ca,
                                                 const Col& cb) const {
-        const float a[4] = {deq(av[0], ca.w.x, x), deq(av[1], ca.w.y, x), deq(av[2], ca.w.z, x),
-                            deq(av[3], ca.w.w, x)};
-        const float b[4] = {deq(bv[0], cb.w.x, x), deq(bv[1], cb.w.y, x), deq(bv[2], cb.w.z, x),
-                            deq(bv[3], cb.w.w, x)};
-        return win_finish(a, b);
+        static_assert(ACT == 4, "the windowed pair form is GEGLU's");
+        const float a[4] = {deq_raw(av[0], ca.w.x, x), deq_raw(av[1], ca.w.y, x),
+                            deq_raw(av[2], ca.w.z, x), deq_raw(av[3], ca.w.w, x)};
+        const float b[4] = {deq_raw(bv[0], cb.w.x, x), deq_raw(bv[1], cb.w.y, x),
+                            deq_raw(bv[2], cb.w.z, x), deq_raw(bv[3], cb.w.w, x)};
+        return win_finish(b, a);
     }
     __device__ __forceinline__ void store16(int m, int n, const uint4& v) const {
         *reinterpret_cast<uint4*>(out + int64_t(m) * ldo + n) = v;
