@@ -593,6 +593,99 @@ __global__ __launch_bounds__(1024) void rowquant_seg_kernel(Loader load, int8_t*
     }
 }
 
+// Column-scaled rows (quantize_row with a column scale, e.g. linear_dx_int8's
+// dy): each lane owns 16 consecutive columns and a block takes RL rows
+// through the same lanes, so a lane loads its 16 fp32 column scales -- twice
+// the bytes of the bf16 row piece they scale -- and rounds them to bf16 once
+// for RL rows instead of once per row.  The arithmetic is LoadColScaled's and
+// the kDivide quantizer's: bf16(x * bf16(w)), the row max of |.| (one LDS slot
+// per row, one atomic max per 16 lanes), then rint(v / s).  Lanes past N load
+// column 0 and store nothing; rows past M load row M - 1 and store nothing.
+template <int RL, bool TILED>
+__global__ __launch_bounds__(1024) void rowquant_cs_kernel(const uint16_t* __restrict__ x,
+                                                          const float* __restrict__ colscale,
+                                                          int8_t* __restrict__ q,
+                                                          float* __restrict__ scale, int64_t M,
+                                                          int N) {
+    __shared__ uint32_t row_max[RL];
+    const int lc = int(threadIdx.x) * 16;
+    const bool has = lc < N;
+    const int col = has ? lc : 0;
+    const int64_t row0 = int64_t(blockIdx.x) * RL;
+    // the scales first, then every row: a row's values wait only for it
+    const float4* cp = reinterpret_cast<const float4*>(colscale + col);
+    const float4 c0 = cp[0], c1 = cp[1], c2 = cp[2], c3 = cp[3];
+    LoadBF16::Raw raw[RL];
+#pragma unroll
+    for (int r = 0; r < RL; ++r)
+        raw[r] = LoadBF16{x, N}.fetch(min(row0 + r, M - 1), col);
+    if (threadIdx.x < RL) row_max[threadIdx.x] = 0u;
+    // bf16(w), each packing conversion rounding two scales
+    const uint32_t wp[8] = {pack_bf16x2(c0.x, c0.y), pack_bf16x2(c0.z, c0.w),
+                            pack_bf16x2(c1.x, c1.y), pack_bf16x2(c1.z, c1.w),
+                            pack_bf16x2(c2.x, c2.y), pack_bf16x2(c2.z, c2.w),
+                            pack_bf16x2(c3.x, c3.y), pack_bf16x2(c3.z, c3.w)};
+    lds_barrier();                               // the zeroed maxima land before any atomic
+    uint32_t vp[RL][8];                          // bf16(x * bf16(w)), packed pairs
+#pragma unroll
+    for (int r = 0; r < RL; ++r) {
+        float v[16];
+        LoadBF16{x, N}.expand(raw[r], v);
+        float m = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t p = pack_bf16x2(v[2 * j] * __uint_as_float(wp[j] << 16),
+                                           v[2 * j + 1] * __uint_as_float(wp[j] & 0xFFFF0000u));
+            vp[r][j] = p;
+            m = fmaxf(m, fabsf(__uint_as_float(p << 16)));
+            m = fmaxf(m, fabsf(__uint_as_float(p & 0xFFFF0000u)));
+        }
+        if (!has) m = 0.f;
+        // m >= 0 (never NaN), so its bit pattern orders like its value
+        const uint32_t mb = segment_max_bits(__float_as_uint(m));
+        if ((threadIdx.x & 15) == 0) atomicMax(&row_max[r], mb);
+    }
+    lds_barrier();
+    const int KB = (N + 63) / 64;
+#pragma unroll
+    for (int r = 0; r < RL; ++r) {
+        const int64_t row = row0 + r;
+        if (row >= M) break;
+        const float sc = row_scale(kDivide, __uint_as_float(row_max[r]));
+        const float inv = rcp_rn(sc);
+        if (threadIdx.x == 0) scale[row] = sc;
+        float v[16];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            v[2 * j] = __uint_as_float(vp[r][j] << 16);
+            v[2 * j + 1] = __uint_as_float(vp[r][j] & 0xFFFF0000u);
+        }
+        const uint4 w = quant16<false, kDivide>(v, sc, inv, 1.0f);
+        if (has) {
+            if constexpr (TILED)
+                *reinterpret_cast<uint4*>(q + tiled_offset(row, col, KB)) = w;
+            else
+                *reinterpret_cast<uint4*>(q + row * N + col) = w;
+        }
+    }
+}
+
+// The column-scaled kernel's rows per block, and whether it takes a shape:
+// whole 16-column pieces, one lane each, at most one block's 1024 lanes.
+constexpr int kColScaledRows = 2;
+inline bool colscaled_rows_applies(int N) { return N % 16 == 0 && N > 0 && N <= 16 * 1024; }
+
+template <bool TILED>
+hipError_t launch_colscaled(hipStream_t st, const uint16_t* x, const float* colscale, int8_t* q,
+                            float* scale, int64_t M, int N) {
+    const int threads = ((N / 16 + 63) / 64) * 64;
+    const dim3 grid(unsigned((M + kColScaledRows - 1) / kColScaledRows));
+    const dim3 block{unsigned(threads)};
+    hipLaunchKernelGGL((rowquant_cs_kernel<kColScaledRows, TILED>), grid, block, 0, st, x,
+                       colscale, q, scale, M, N);
+    return hipGetLastError();
+}
+
 // Rows too long for registers: pass 1 finds the row max, pass 2 recomputes
 // each slot (the re-read comes from L2) and stores it.
 template <bool ROT, int MODE, class Loader>
@@ -887,6 +980,11 @@ hipError_t prepare_weight(hipStream_t st, const void* w, int8_t* q, float* scale
 
 hipError_t quantize_row(hipStream_t st, const void* x, const float* colscale, int8_t* q,
                         float* scale, int64_t M, int N, bool tiled) {
+    if (colscale && colscaled_rows_applies(N)) {
+        const uint16_t* xb = static_cast<const uint16_t*>(x);
+        if (tiled) return launch_colscaled<true>(st, xb, colscale, q, scale, M, N);
+        return launch_colscaled<false>(st, xb, colscale, q, scale, M, N);
+    }
     const LoadColScaled ld{static_cast<const uint16_t*>(x), N, colscale};
     if (tiled) return launch_rowquant<false, kDivide, LoadColScaled, true>(st, ld, q, scale, M, N);
     return launch_rowquant<false, kDivide>(st, ld, q, scale, M, N);
