@@ -397,6 +397,23 @@ def test_quantize_row_column_scaled(dev):
     assert np.array_equal(npy(q), wq) and np.array_equal(npy(s), ws)
 
 
+@pytest.mark.parametrize("m,n", [(1, 16), (3, 48), (5, 1040), (7, 5120), (33, 16384),
+                                 (2, 16400)])
+def test_quantize_row_column_scaled_edges(dev, m, n):
+    """The column-scaled quantizer at its edges: one row, odd row counts (a
+    row pair's second row past M), widths that leave the last wave partly
+    idle, the widest row one block of lanes takes (16384) and one past it
+    (the segmented kernel); a row of zeros takes the scale floor."""
+    dy = activation(m, n, seed=m + n, scale=1e-3, n_out=0)
+    dy[m // 2] = 0
+    wsc = (torch.rand(n, generator=torch.Generator().manual_seed(n)) * 1e-3).float()
+    q, s = int8.quantize_row(dy.to(dev), wsc.to(dev))
+    d = O.f32_to_bf16(O.bf16_to_f32(bits(dy)) * O.bf16_round(npy(wsc))[None, :])
+    wq, ws = O.quantize_row(d)
+    assert np.array_equal(npy(s).view(np.uint32), ws.view(np.uint32))
+    assert np.array_equal(npy(q), wq), mismatch(npy(q), wq)
+
+
 # ------------------------------------------------------------- epilogues
 def test_dequant_rounding_edge_cases(dev):
     """The bf16 conversion at its edges, through the dequant epilogue: exact
